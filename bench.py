@@ -1,0 +1,324 @@
+"""Benchmark of the Voyager quantization hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2] [--no-cpu]
+
+A step is one pass of a hot-path kernel over one batch of synthetic, seeded
+input already resident in HBM.  The headline (``value``) is BASELINE.json
+NF4 block-64 encode of a bf16 4096x11008 weight (C2), in
+quantized elements per second; every other config is reported in
+``configs``.  Kernel time is measured with HIP events on the launch stream
+(the kernels launch on torch's current stream, so torch.cuda.Event sees
+them).  ``cpu_baseline`` times the CPU oracle (a restatement of the
+reference's PyTorch CPU path) on this host's cores.
+"""
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default=None, help="comma list of config keys to run")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-iters", type=int, default=3)
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# configs: setup() -> (launch callable, info)
+# ---------------------------------------------------------------------------
+def _c(ptrs):
+    return ptrs
+
+
+def setup_c1(vqx, torch, L):
+    torch.manual_seed(0)
+    x = torch.randn(4096, 4096, dtype=torch.float32).cuda()
+    y = torch.empty_like(x)
+    codes = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
+    desc = vqx.parse_format("posit8_1").desc(x.device)
+    st = L.stream_of(x)
+    args = (L.ptr(x), L.F32, x.numel(), L.ctypes.byref(desc), None, 1, 1, 1, L.ptr(y), L.ptr(codes), 1, st)
+    fn = L.load().vqx_fake_quant
+    n = x.numel()
+    return (lambda: fn(*args)), dict(
+        name="C1 posit8_1 fake-quant + uint8 codes, fp32 4096x4096 N(0,1) seed 0",
+        elements=n, bytes=9 * n, bound="hbm", dtype="f32->u8")
+
+
+def c2_input(torch, rows=4096, cols=11008, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    w = 0.02 * torch.randn(rows, cols, generator=g)
+    n = round(0.001 * w.numel())
+    idx = torch.randperm(w.numel(), generator=g)[:n]
+    sign = torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0)
+    w.view(-1)[idx] = sign * 8 * 0.02
+    return w.to(torch.bfloat16)
+
+
+def setup_c2(vqx, torch, L, decode=False):
+    xc = c2_input(torch)
+    x = xc.cuda()
+    n = x.numel()
+    fmt = vqx.parse_format("nf4")
+    desc = fmt.desc(x.device)
+    codes = torch.empty(n // 2, dtype=torch.uint8, device="cuda")
+    scale = torch.empty(4096, 11008 // 64, dtype=torch.float32, device="cuda")
+    st = L.stream_of(x)
+    enc = L.load().vqx_mx_quantize
+    eargs = (L.ptr(x), L.BF16, 4096, 11008, 1, 64, L.ctypes.byref(desc), 1, 0, L.ctypes.c_float(1.0), None,
+             None, L.ptr(scale), None, None, None, L.ptr(codes), 0, st)
+    algo = n * 2 + n // 2 + scale.numel() * 4
+    if not decode:
+        return (lambda: enc(*eargs)), dict(
+            name="C2 NF4 block-64 absmax encode, bf16 4096x11008 N(0,0.02)+0.1% outliers seed 1 "
+                 "-> packed 4-bit codes + fp32 scales",
+            elements=n, bytes=algo, bound="hbm", dtype="bf16->u4", cpu_input=xc)
+    enc(*eargs)
+    out = torch.empty_like(x)
+    dtab = fmt.tables(x.device)["decode"]
+    dec = L.load().vqx_mx_decode
+    dargs = (L.ptr(codes), 4, L.ptr(dtab), dtab.numel(), L.ptr(scale), 0, n, 64, L.ptr(out), L.BF16, st)
+    return (lambda: dec(*dargs)), dict(
+        name="C2 NF4 block-64 decode: packed codes + fp32 scales -> bf16 4096x11008",
+        elements=n, bytes=algo, bound="hbm", dtype="u4->bf16")
+
+
+def c3_input(torch, rows=8192, cols=8192, seed=2):
+    g = torch.Generator().manual_seed(seed)
+    u = torch.rand(rows, cols, generator=g) - 0.5
+    lap = -torch.sign(u) * torch.log1p(-2 * u.abs())
+    mult = 10 ** (torch.rand(cols, generator=g) * 2 - 1)
+    return (lap * mult).to(torch.bfloat16)
+
+
+_C3_X = {}
+
+
+def setup_c3(vqx, torch, L, dtype, qmax, fake=False):
+    if "x" not in _C3_X:
+        _C3_X["x"] = c3_input(torch).cuda()
+    x = _C3_X["x"]
+    n = x.numel()
+    fmt = vqx.parse_format(dtype)
+    desc = fmt.desc(x.device)
+    st = L.stream_of(x)
+    shift = math.floor(math.log2(qmax))
+    fn = L.load().vqx_mx_quantize
+    if fake:
+        y = torch.empty_like(x)
+        sc = torch.empty(8192, 256, dtype=torch.bfloat16, device="cuda")
+        args = (L.ptr(x), L.BF16, 8192, 8192, 1, 32, L.ctypes.byref(desc), 0, shift, L.ctypes.c_float(qmax),
+                None, L.ptr(sc), None, None, None, L.ptr(y), None, 1, st)
+        return (lambda: fn(*args)), dict(
+            name=f"C3 MX block-32 {dtype} fake-quant (bf16 values + bf16 scales), bf16 8192x8192 Laplace seed 2",
+            elements=n, bytes=n * 4 + sc.numel() * 2, bound="hbm", dtype="bf16")
+    cb = fmt.code_bits
+    codes = torch.empty(n * cb // 8, dtype=torch.uint8, device="cuda")
+    e8 = torch.empty(8192, 256, dtype=torch.uint8, device="cuda")
+    args = (L.ptr(x), L.BF16, 8192, 8192, 1, 32, L.ctypes.byref(desc), 0, shift, L.ctypes.c_float(qmax),
+            None, None, None, L.ptr(e8), None, None, L.ptr(codes), 0, st)
+    return (lambda: fn(*args)), dict(
+        name=f"C3 MX block-32 {dtype} + E8M0 scales, bf16 8192x8192 Laplace x 10^U(-1,1) seed 2 -> packed codes",
+        elements=n, bytes=n * 2 + n * cb // 8 + e8.numel(), bound="hbm", dtype=f"bf16->{dtype}")
+
+
+def c4_codebooks(torch, rows, K, seed=3):
+    import numpy as np
+    from scipy.stats import norm
+
+    g = torch.Generator().manual_seed(seed)
+    q = torch.tensor(norm.ppf((np.arange(K) + 0.5) / K), dtype=torch.float32)
+    spacing = torch.diff(q, prepend=q[:1] - (q[1] - q[0]))
+    jit = (torch.rand(rows, K, generator=g) - 0.5) * 0.5 * spacing
+    return torch.sort(q + jit, dim=1).values
+
+
+def setup_c4(vqx, torch, L, K, decode=False):
+    g = torch.Generator().manual_seed(3)
+    xc = torch.randn(4096, 4096, generator=g)
+    x = xc.cuda()
+    cbc = c4_codebooks(torch, 4096, K)
+    cb = cbc.cuda()
+    codes = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
+    st = L.stream_of(x)
+    n = x.numel()
+    algo = 5 * n + cb.numel() * 4
+    enc = L.load().vqx_codebook_encode
+    eargs = (L.ptr(x), L.F32, 4096, 4096, L.ptr(cb), K, L.ptr(codes), st)
+    if not decode:
+        return (lambda: enc(*eargs)), dict(
+            name=f"C4 per-channel codebook encode K={K}, fp32 4096x4096 N(0,1) seed 3 -> uint8 indices",
+            elements=n, bytes=algo, bound="hbm", dtype="f32->u8", cpu_input=(xc, cbc))
+    enc(*eargs)
+    out = torch.empty_like(x)
+    dec = L.load().vqx_codebook_decode
+    dargs = (L.ptr(codes), 4096, 4096, L.ptr(cb), K, L.ptr(out), L.F32, st)
+    return (lambda: dec(*dargs)), dict(
+        name=f"C4 per-channel codebook decode K={K}: uint8 indices -> fp32 4096x4096",
+        elements=n, bytes=algo, bound="hbm", dtype="u8->f32")
+
+
+CONFIGS = {
+    "c2": lambda v, t, L: setup_c2(v, t, L),
+    "c1": lambda v, t, L: setup_c1(v, t, L),
+    "c2_decode": lambda v, t, L: setup_c2(v, t, L, decode=True),
+    "c3_e4m3": lambda v, t, L: setup_c3(v, t, L, "fp8_e4m3", 448.0),
+    "c3_e3m2": lambda v, t, L: setup_c3(v, t, L, "fp6_e3m2", 28.0),
+    "c3_e2m1": lambda v, t, L: setup_c3(v, t, L, "fp4_e2m1", 6.0),
+    "c3_e4m3_fq": lambda v, t, L: setup_c3(v, t, L, "fp8_e4m3", 448.0, fake=True),
+    "c4_k16": lambda v, t, L: setup_c4(v, t, L, 16),
+    "c4_k256": lambda v, t, L: setup_c4(v, t, L, 256),
+    "c4_k16_decode": lambda v, t, L: setup_c4(v, t, L, 16, decode=True),
+}
+HEADLINE = "c2"
+
+
+def time_config(torch, launch, steps, warmup):
+    for _ in range(warmup):
+        rc = launch()
+        if rc != 0:
+            raise RuntimeError(f"launch failed: {rc}")
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    t0.record()
+    for i in range(steps):
+        starts[i].record()
+        launch()
+        ends[i].record()
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return {"kernel_ms_avg": statistics.fmean(per), "kernel_ms_median": statistics.median(per),
+            "region_ms": t0.elapsed_time(t1), "wall_s": wall}
+
+
+def cpu_baseline_c2(torch, x):
+    """The reference's CPU path for C2 (calculate_mx_qparam absmax + quantize
+    with the NF index table), timed on this host."""
+    import numpy as np
+
+    from oracle import formats as F
+    from oracle import reference_ops as R
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    lv = F.nf_levels(4)
+    idx_q = torch.from_numpy(F.nf_index_table(lv).astype(np.float32)).to(torch.bfloat16)
+    # bounded sample: 1024 of the 4096 rows (~11.3M elements)
+    xs = x[:1024].contiguous()
+
+    def run():
+        s = R.calculate_mx_qparam(xs, [-1], 64, 1.0, False)
+        return R.quantize(xs, s, None, [-1], 64, idx_q)
+
+    run()
+    ts = []
+    for _ in range(3):
+        t = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t)
+    med = statistics.median(ts)
+    return {"value": xs.numel() / med, "unit": "elements/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"C2 rows 0..1023 of 4096 (11,272,192 bf16 elements), 1 warm-up + 3 timed runs, median "
+                      f"{med:.3f} s; torch-CPU restatement of calculate_mx_qparam + quantize",
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "bench.py runs on one GPU only: this build has no multi-GPU path "
+                                   f"(asked for --gpus {a.gpus})"}))
+        sys.exit(2)
+    import torch
+
+    import __graft_entry__
+
+    vqx = __graft_entry__.load_package()
+    L = vqx._lib
+    keys = list(CONFIGS) if a.only is None else a.only.split(",")
+    if HEADLINE not in keys:
+        keys = [HEADLINE] + keys
+    results = {}
+    info_head = None
+    for k in keys:
+        print(f"[bench] {k}: setup", file=sys.stderr, flush=True)
+        launch, info = CONFIGS[k](vqx, torch, L)
+        tm = time_config(torch, launch, a.steps, a.warmup)
+        ms = tm["kernel_ms_avg"]
+        gbs = info["bytes"] / (ms * 1e-3) / 1e9
+        results[k] = {
+            "workload": info["name"], "elements_per_s": info["elements"] / (ms * 1e-3),
+            "kernel_ms": ms, "region_ms_per_step": tm["region_ms"] / a.steps,
+            "algorithmic_bytes": info["bytes"], "achieved_GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+            "dtype": info["dtype"]}
+        print(f"[bench] {k}: {ms * 1e3:.1f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)",
+              file=sys.stderr, flush=True)
+        if k == HEADLINE:
+            info_head = info
+        del launch
+        torch.cuda.empty_cache()
+    head = results[HEADLINE]
+    cpu = None
+    if not a.no_cpu:
+        print("[bench] cpu baseline (C2 sample)", file=sys.stderr, flush=True)
+        cpu = cpu_baseline_c2(torch, info_head["cpu_input"])
+    out = {
+        "metric": "quantized elements/sec",
+        "value": head["elements_per_s"],
+        "unit": "elements/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": head["region_ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded, BASELINE.json configs)",
+        "config": {"workload": head["workload"], "block_size": 64, "format": "nf4", "shape": [4096, 11008]},
+        "roofline": {"bound": "hbm", "achieved": head["achieved_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["hbm_frac"], "traffic": None,
+                     "kernel": "mx_group_kernel<bf16, EncLevels, 4, 4>",
+                     "algorithmic_bytes_per_launch": head["algorithmic_bytes"],
+                     "kernel_ms_avg": head["kernel_ms"]},
+        "cpu_baseline": cpu,
+        "configs": results,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

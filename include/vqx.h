@@ -1,0 +1,207 @@
+/*
+ * vqx — MI355X (gfx950) kernels for the Voyager quantization hot path.
+ *
+ * C ABI of libvqx.so.  Every pointer argument named as a tensor is a device
+ * pointer (hipMalloc / torch CUDA-device memory) unless stated otherwise; sizes
+ * are element counts.  Every call enqueues work on `stream` and returns
+ * without synchronizing; it returns VQX_OK (0) or a negative status, with a
+ * message from vqx_last_error() (thread-local).  The library keeps no device
+ * allocations of its own: callers own every buffer.
+ *
+ * Reference interfaces (paths relative to the voyager-compiler repository,
+ * src/vc = src/voyager_compiler) are cited on each entry point.
+ */
+#ifndef VQX_H_
+#define VQX_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* vqx_stream_t; /* hipStream_t; NULL = the default stream */
+
+enum {
+  VQX_OK = 0,
+  VQX_ERR_INVALID = -1,     /* bad argument: shape, dtype, alignment, format */
+  VQX_ERR_LAUNCH = -2,      /* HIP runtime / kernel launch failure */
+  VQX_ERR_UNSUPPORTED = -3, /* valid request this build does not implement */
+};
+
+/* dtype tags */
+enum {
+  VQX_F32 = 0,
+  VQX_BF16 = 1,
+  VQX_F16 = 2,
+  VQX_U8 = 3,
+};
+
+/* Element format kinds (the dtype strings get_quantization_map accepts,
+ * src/vc/quantization/fake_quantize.py:30-98). */
+enum {
+  VQX_FMT_IDENTITY = 0, /* "float32", "bfloat16" */
+  VQX_FMT_FP16 = 1,     /* "float16" */
+  VQX_FMT_INT = 2,      /* "int<n>" / "uint<n>":   p0 = n, p1 = signed (1) */
+  VQX_FMT_FP = 3,       /* "fp<N>_e<E>m<M>":       p0 = E, p1 = M, max_norm */
+  VQX_FMT_NV_FP8 = 4,   /* "e4m3" / "e5m2":        p0 = 4 or 5 */
+  VQX_FMT_POSIT = 5,    /* "posit<n>_<es>":        p0 = n, p1 = es */
+  VQX_FMT_LEVELS = 6,   /* "nf<k>[_<b>]", codebook tables: levels + code table */
+  VQX_FMT_TABLE = 7,    /* any 65536-entry bf16 table (a user qmap); no codes */
+};
+
+#define VQX_FLAG_UNSIGNED 1 /* fp<N>_e<E>m<M> with N == E + M */
+
+/* Format descriptor.  Host struct; its table pointers are device pointers,
+ * read only for VQX_FMT_LEVELS (boundaries, levels, code_table) and
+ * VQX_FMT_TABLE (value_table). */
+typedef struct vqx_format {
+  int32_t kind;
+  int32_t p0;
+  int32_t p1;
+  int32_t flags;
+  float max_norm;
+  int32_t code_bits;           /* width of one packed code: 4, 6, 8 or 16 */
+  const float* boundaries;     /* LEVELS: nlevels-1 fp32 boundaries */
+  const uint16_t* levels;      /* LEVELS: nlevels bf16 level patterns */
+  const uint8_t* code_table;   /* LEVELS: 65536 codes, one per bf16 pattern */
+  const uint16_t* value_table; /* TABLE: 65536 bf16 values, one per bf16 pattern */
+} vqx_format;
+
+/* Where element i of x finds its scale / zero point.  x is viewed as
+ * [outer, L, inner] (i = (o * L + l) * inner + in) and reads
+ * scale[o * s_o + (l / block) * s_l + in * s_in]; strides of 0 broadcast.
+ * Per-tensor: all strides 0.  Per-channel along the middle axis: block 1,
+ * s_l 1.  Blocks of `block` along L: s_o = ceil(L/block) * inner,
+ * s_l = inner, s_in = 1.  scale / zero_point are in x's dtype. */
+typedef struct vqx_scale_map {
+  const void* scale;
+  const void* zero_point; /* optional */
+  int64_t L, inner, block;
+  int64_t s_o, s_l, s_in;
+} vqx_scale_map;
+
+/* Library version string. */
+const char* vqx_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* vqx_last_error(void);
+
+/* Number of compute units of the current device (used for launch sizing). */
+int vqx_device_cus(void);
+
+/*
+ * quantized_ops::vmap  (src/vc/ops/quantized.py:98-121)
+ * y[i] = table[bf16_bits(x[i])], returned in x's dtype.  x: n elements of
+ * x_dtype (F32, BF16, F16); table: 65536 bf16 patterns; y: n elements of x_dtype.
+ */
+int vqx_vmap(const void* x, int32_t x_dtype, int64_t n, const uint16_t* table, void* y,
+             vqx_stream_t stream);
+
+/*
+ * FakeQuantizeFunction.forward  (src/vc/quantization/fake_quantize.py:101-115)
+ * and quantized_ops::quantize without block_size (src/vc/ops/quantized.py:131-172):
+ *   y = vmap(x / s, qmap) * s   (mul_back = 1)   or   y = vmap(x / s, qmap)
+ * with the format's table computed in closed form.  scale: NULL (s = 1) or
+ * scale_numel fp32 values; element i uses scale[(i / scale_inner) % scale_numel].
+ * codes (optional, NULL to skip): one code per element, code_bytes (1 or 2)
+ * wide: posit/int two's complement, fp OCP-style bits, level index.
+ */
+int vqx_fake_quant(const void* x, int32_t x_dtype, int64_t n, const vqx_format* fmt,
+                   const float* scale, int64_t scale_numel, int64_t scale_inner,
+                   int32_t mul_back, void* y, void* codes, int32_t code_bytes,
+                   vqx_stream_t stream);
+
+/*
+ * quantized_ops::quantize  (src/vc/ops/quantized.py:124-172) with any scale
+ * layout: y = vmap(x / s [+ zp], qmap) with the format (or a TABLE format for
+ * an arbitrary qmap), every op rounded to x's dtype (F32, BF16, F16).
+ * mul_back = 1 multiplies back (y = vmap(...) * s: fake-quant).
+ * codes: optional, code_bytes (1 or 2) per element.
+ */
+int vqx_quantize_mapped(const void* x, int32_t x_dtype, int64_t n, const vqx_format* fmt,
+                        const vqx_scale_map* sm, int32_t mul_back, void* y, void* codes,
+                        int32_t code_bytes, vqx_stream_t stream);
+
+/*
+ * quantized_ops::dequantize  (src/vc/ops/quantized.py:175-227):
+ * y = out_map((in_map(x) [- zp]) * s), in_map / out_map optional 65536-entry
+ * bf16 tables (input_qmap / output_qmap), every op in x's dtype.
+ */
+int vqx_dequantize_mapped(const void* x, int32_t x_dtype, int64_t n, const uint16_t* input_qmap,
+                          const vqx_scale_map* sm, const uint16_t* output_qmap, void* y,
+                          vqx_stream_t stream);
+
+/*
+ * get_quantization_map  (src/vc/quantization/fake_quantize.py:30-98)
+ * values[h] = the format's value for bf16 pattern h (65536 bf16 patterns);
+ * codes[h] (optional) = its code.
+ */
+int vqx_build_table(const vqx_format* fmt, uint16_t* values, uint16_t* codes,
+                    vqx_stream_t stream);
+
+/*
+ * Level-set tables for quantize_to_nf (src/vc/quantization/dtypes/normal_float.py:54-60,
+ * mode 0: bf16 arithmetic) and codebook_qmap (src/vc/quantization/lcq.py:270-291,
+ * mode 1: fp32 arithmetic).  levels: K fp32 values (the bf16 levels for mode 0).
+ * Writes index_table[65536] (argmin index per bf16 pattern) and boundaries[K-1];
+ * work: K uint32 scratch; bad: one int, set to the number of patterns whose
+ * index the boundaries do not reproduce (0 = the level set is monotone).
+ */
+int vqx_level_tables(const float* levels, int32_t K, int32_t mode, uint8_t* index_table,
+                     float* boundaries, uint32_t* work, int32_t* bad, vqx_stream_t stream);
+
+/*
+ * quantized_ops::calculate_mx_qparam + quantize / quantize_mx fused
+ * (src/vc/ops/quantized.py:435-529) and MXFakeQuantizeFunction.forward
+ * (src/vc/quantization/fake_quantize.py:123-153).
+ * x viewed as [outer, L, inner] with blocks of block_size along L.
+ * scale_mode 0: power of two, pow2_shift = floor(log2(quant_max));
+ * scale_mode 1: absmax / quant_max, then scale_qmap (65536 bf16, optional).
+ * Outputs (each optional): scale_out [outer, ceil(L/bs), inner] in x's dtype;
+ * scale_f32 (same shape, fp32); scale_e8m0 (uint8, power-of-two mode only);
+ * qvals [n] in x's dtype = quantize()'s output; fq [n] = qvals * scale;
+ * codes: code_layout 0 = packed bitstream of fmt->code_bits per element
+ * (element i at bits [cb*i, cb*i+cb), little endian; needs inner == 1,
+ * block_size 16, 32, 64 or 128 dividing L, 16-byte aligned buffers),
+ * 1 / 2 = one uint8 / uint16 per element.
+ */
+int vqx_mx_quantize(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                    int64_t block_size, const vqx_format* fmt, int32_t scale_mode,
+                    int32_t pow2_shift, float quant_max, const uint16_t* scale_qmap,
+                    void* scale_out, float* scale_f32, uint8_t* scale_e8m0, void* qvals,
+                    void* fq, void* codes, int32_t code_layout, vqx_stream_t stream);
+
+/*
+ * quantized_ops::dequantize with input_qmap (src/vc/ops/quantized.py:175-227),
+ * on packed codes: out[i] = decode_table[code(i)] * scale[i / block_size],
+ * rounded to out_dtype (F32 or BF16).  scale_kind 0 = fp32, 1 = bf16,
+ * 2 = E8M0 uint8.  decode_table: ntab bf16 values indexed by code.
+ */
+int vqx_mx_decode(const uint8_t* codes, int32_t code_bits, const uint16_t* decode_table,
+                  int32_t ntab, const void* scale, int32_t scale_kind, int64_t n,
+                  int64_t block_size, void* out, int32_t out_dtype, vqx_stream_t stream);
+
+/* decode_table[code] = value of the format, for codes < ntab. */
+int vqx_decode_table(const vqx_format* fmt, uint16_t* decode_table, int32_t ntab,
+                     vqx_stream_t stream);
+
+/*
+ * Per-channel codebook encode (the per-row form of codebook_qmap + vmap,
+ * src/vc/quantization/lcq.py:270-291, src/vc/ops/quantized.py:101-121):
+ * codes[r, c] = argmin_k |clamp(bf16(x[r, c])) - cb[r, k]| in fp32, lowest k
+ * on ties, NaN -> 0.  cb: [rows, K] fp32, each row sorted ascending, K <= 256.
+ * x: [rows, cols] F32 or BF16, cols % 16 == 0.
+ */
+int vqx_codebook_encode(const void* x, int32_t x_dtype, int64_t rows, int64_t cols,
+                        const float* cb, int32_t K, uint8_t* codes, vqx_stream_t stream);
+
+/* out[r, c] = bf16(cb[r, codes[r, c]]) stored as out_dtype (F32 or BF16). */
+int vqx_codebook_decode(const uint8_t* codes, int64_t rows, int64_t cols, const float* cb,
+                        int32_t K, void* out, int32_t out_dtype, vqx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VQX_H_ */

@@ -1,0 +1,112 @@
+"""Host-side logic without a GPU: the C-ABI library loads and exports every
+entry point include/vqx.h declares, spec strings parse as the reference's
+grammar does, dtype strings route as get_quantization_map does, and CPU
+tensors are refused (no CPU path)."""
+
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "vqx.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(vqx_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol(vqx):
+    lib = vqx._lib.load()
+    names = declared_symbols()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(vqx._lib.exported_symbols()) == names
+    assert lib.vqx_version().decode().startswith("vqx")
+
+
+def test_spec_parsing(vqx):
+    from voyager_compiler_amd.quantization import QScheme, QuantizationSpec, parse_spec_fields
+
+    p = parse_spec_fields("int8,qs=microscaling,bs=16,ax=-1,scale=fp8_e5m3")
+    assert p == {"dtype": "int8", "qscheme": QScheme.MICROSCALING, "block_size": 16, "ch_axis": -1,
+                 "scale_dtype": "fp8_e5m3", "quant_min": -128.0, "quant_max": 127.0}
+    p = parse_spec_fields("posit8_1")
+    assert p == {"dtype": "posit8_1"}
+    p = parse_spec_fields("fp8_e4m3,qs=per_tensor_symmetric")
+    assert p["quant_max"] == 448.0 and p["amax_history_len"] == 16
+    p = parse_spec_fields("nf4_6,qs=microscaling,bs=64,ax=(2,3)")
+    assert p["ch_axis"] == (2, 3) and p["quant_max"] == 31.0
+    assert parse_spec_fields("posit8_1,qs=per_channel_symmetric")["quant_max"] == 4096.0
+    assert parse_spec_fields("fp6_e3m2,qs=microscaling,bs=32")["quant_max"] == 28.0
+    assert parse_spec_fields("fp4_e2m1,qs=microscaling,bs=32")["quant_max"] == 6.0
+    with pytest.raises(ValueError, match="empty"):
+        parse_spec_fields("")
+    with pytest.raises(ValueError, match="key=value"):
+        parse_spec_fields("int8,bogus")
+    with pytest.raises(ValueError, match="Unknown argument"):
+        parse_spec_fields("int8,foo=1")
+    with pytest.raises(ValueError, match="block_size is required"):
+        QuantizationSpec.from_str("int8,qs=microscaling")
+    with pytest.raises(ValueError, match="quant_max is required"):
+        QuantizationSpec(dtype="int8", qscheme=QScheme.PER_TENSOR_SYMMETRIC)
+
+
+@pytest.mark.parametrize("dtype,kind,p0,p1", [
+    ("int8", 2, 8, 1), ("UINT4", 2, 4, 0), ("e4m3", 4, 4, 0), ("fp8.e5m2", 4, 5, 0),
+    ("fp8_e4m3", 3, 4, 3), ("fp6_e3m2", 3, 3, 2), ("fp4_e2m1", 3, 2, 1), ("fp8_e5m3", 3, 5, 3),
+    ("posit8_1", 5, 8, 1), ("posit16_1", 5, 16, 1), ("nf4", 6, 0, 0), ("bfloat16", 0, 0, 0),
+    ("float16", 1, 0, 0)])
+def test_format_routing(vqx, dtype, kind, p0, p1):
+    f = vqx.parse_format(dtype)
+    assert (f.kind, f.p0, f.p1) == (kind, p0, p1)
+
+
+def test_format_details(vqx):
+    assert vqx.parse_format("fp8_e4m3").max_norm == 448.0
+    assert vqx.parse_format("fp8_e5m2").max_norm == 57344.0
+    assert vqx.parse_format("fp6_e3m2").code_bits == 6
+    assert vqx.parse_format("fp8_e5m3").flags == 1
+    assert vqx.parse_format("nf4").code_bits == 4 and vqx.parse_format("nf4").nlevels == 16
+    with pytest.raises(ValueError, match="Unsupported dtype"):
+        vqx.parse_format("mxfoo")
+    with pytest.raises(AssertionError):
+        vqx.parse_format("fp8_e2m2")
+
+
+def test_cpu_tensors_are_refused(vqx):
+    x = torch.randn(8)
+    with pytest.raises(NotImplementedError):
+        torch.ops.quantized_ops.vmap(x, torch.zeros(65536, dtype=torch.bfloat16))
+    with pytest.raises(NotImplementedError):
+        torch.ops.quantized_ops.fake_quant(x, "posit8_1", None, True, False)
+    with pytest.raises(NotImplementedError):
+        torch.ops.quantized_ops.quantize_mx(x.reshape(1, 8), torch.zeros(65536, dtype=torch.bfloat16),
+                                            [-1], 8, 448.0, True)
+
+
+def test_fake_impls_trace(vqx):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        x = torch.empty(4, 64, dtype=torch.bfloat16)
+        s, q = torch.ops.quantized_ops.quantize_mx(x, torch.empty(65536, dtype=torch.bfloat16), [-1],
+                                                   32, 448.0, True)
+        assert s.shape == (4, 2) and q.shape == (4, 64)
+        sc, codes = torch.ops.quantized_ops.quantize_mx_packed(x, "fp4_e2m1", -1, 32)
+        assert sc.shape == (4, 2) and sc.dtype == torch.uint8 and codes.numel() == 128
+
+
+def test_fake_quantize_module_state_on_cpu(vqx):
+    from voyager_compiler_amd.quantization import FusedAmaxObsFakeQuantize, QuantizationSpec
+
+    fq = QuantizationSpec.from_str("fp8_e4m3,qs=per_tensor_symmetric").make_fake_quantize()
+    assert bool(fq.observer_enabled[0]) and fq.amax_history_len == 16
+    sd = {"scale": torch.tensor([2.0]), "amax_history": torch.ones(16, 1), "fake_quant_enabled": torch.tensor([1], dtype=torch.uint8),
+          "observer_enabled": torch.tensor([1], dtype=torch.uint8), "zero_point": torch.tensor([1.0])}
+    fq.load_state_dict(sd)
+    assert fq.amax_history.shape == (16, 1) and fq.scale.item() == 2.0
+    fq2 = FusedAmaxObsFakeQuantize("posit8_1")
+    assert not bool(fq2.observer_enabled[0])

@@ -1,0 +1,207 @@
+"""GPU parity of the blockwise path against the CPU oracle: MX block-32
+power-of-two scales with fp8/fp6/fp4 elements (C3), NormalFloat block-64
+absmax (C2), packed codes and E8M0 scales, and the edge cases the reference's
+arithmetic produces (zero / NaN / Inf / subnormal / huge blocks)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as F
+from oracle import reference_ops as R
+from tests.conftest import assert_bitexact
+
+Q = torch.ops.quantized_ops
+
+MX = [("fp8_e4m3", 448.0), ("fp6_e3m2", 28.0), ("fp4_e2m1", 6.0)]
+
+
+def c3_input(rows, cols, seed=2):
+    g = torch.Generator().manual_seed(seed)
+    u = torch.rand(rows, cols, generator=g) - 0.5
+    lap = -torch.sign(u) * torch.log1p(-2 * u.abs())
+    mult = 10 ** (torch.rand(cols, generator=g) * 2 - 1)
+    return (lap * mult).to(torch.bfloat16)
+
+
+def edge_rows(cols):
+    rows = torch.zeros(8, cols, dtype=torch.float32)
+    rows[1, 5] = float("nan")
+    rows[1, 40:48] = 3.0
+    rows[2, 7] = float("inf")
+    rows[2, 33] = -float("inf")
+    rows[3, :] = 2.0**-130  # subnormal bf16
+    rows[4, :] = 3.0e38  # huge: the fp tables' NaN region
+    rows[5, ::2] = 1.99 * 2.0**-120
+    rows[6, :] = torch.linspace(-31.75, 31.75, cols)
+    rows[7, 3] = -0.0
+    return rows.to(torch.bfloat16)
+
+
+def oracle_qmap(dtype):
+    return R.table_tensor(F.quantization_table(dtype))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qmax", [448.0, 28.0, 6.0, 1.0, 127.0, 31.0, 0.5])
+def test_pow2_scale_every_amax(vqx, qmax):
+    # one 32-element block per positive bf16 pattern, amax = that pattern
+    a = torch.arange(0, 0x7F81, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = torch.zeros(a.numel(), 32, dtype=torch.bfloat16)
+    x[:, 0] = a
+    x[:, 1] = -a * 0.5
+    got = Q.calculate_mx_qparam(x.cuda(), [-1], 32, qmax, True, None)
+    want = R.calculate_mx_qparam(x, [-1], 32, qmax, True)
+    assert_bitexact(got.cpu(), want, f"pow2 scales qmax={qmax}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qmax", [1.0, 31.0, 448.0])
+def test_absmax_scale_every_amax(vqx, qmax):
+    a = torch.arange(0, 0x7F81, 3, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = torch.zeros(a.numel(), 64, dtype=torch.bfloat16)
+    x[:, 63] = -a
+    got = Q.calculate_mx_qparam(x.cuda(), [-1], 64, qmax, False, None)
+    assert_bitexact(got.cpu(), R.calculate_mx_qparam(x, [-1], 64, qmax, False), f"absmax qmax={qmax}")
+    sq = oracle_qmap("fp8_e5m3")
+    got = Q.calculate_mx_qparam(x.cuda(), [-1], 64, qmax, False, sq.cuda())
+    assert_bitexact(got.cpu(), R.calculate_mx_qparam(x, [-1], 64, qmax, False, sq), "scale_qmap")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,qmax", MX)
+@pytest.mark.parametrize("closed_form", [True, False])
+def test_quantize_mx_c3(vqx, dtype, qmax, closed_form):
+    x = torch.cat([c3_input(248, 1024), edge_rows(1024)])
+    qm = vqx.get_quantization_map(dtype, "cuda")
+    if closed_form:
+        vqx.ops.register_table(qm, vqx.parse_format(dtype))
+    else:
+        qm = qm.clone()
+    s, q = Q.quantize_mx(x.cuda(), qm, [-1], 32, qmax, True, None, None)
+    ws, wq = R.quantize_mx(x, oracle_qmap(dtype), [-1], 32, qmax, True)
+    assert_bitexact(s.cpu(), ws, f"{dtype} scales")
+    assert_bitexact(q.cpu(), wq, f"{dtype} values")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,qmax", MX)
+def test_mx_axis1_and_short_last_block(vqx, dtype, qmax):
+    # blocks along a middle axis with a short last block (the general path)
+    x = c3_input(4 * 100, 6).reshape(4, 100, 6)
+    qm = vqx.get_quantization_map(dtype, "cuda")
+    s, q = Q.quantize_mx(x.cuda(), qm, [1], 32, qmax, True, None, None)
+    ws, wq = R.quantize_mx(x, oracle_qmap(dtype), [1], 32, qmax, True)
+    assert_bitexact(s.cpu(), ws, "scales")
+    assert_bitexact(q.cpu(), wq, "values")
+
+
+def ocp_code(vals, eb, mb):
+    """OCP element code of representable values (no NaN), numpy."""
+    v = vals.astype(np.float64)
+    s = (np.signbit(v)).astype(np.int64)
+    a = np.abs(v)
+    emin = 2 - 2 ** (eb - 1)
+    with np.errstate(divide="ignore"):
+        e = np.floor(np.log2(np.where(a > 0, a, 1)))
+    e = np.maximum(e, emin)
+    normal = a >= 2.0**emin
+    field = np.where(normal, e - emin + 1, 0).astype(np.int64)
+    mant = np.where(normal, a / 2.0**e - 1, a / 2.0**emin) * 2**mb
+    mant = np.rint(mant).astype(np.int64)
+    return (s << (eb + mb)) | (field << mb) | mant
+
+
+def unpack(codes, cb, n):
+    b = codes.cpu().numpy().astype(np.uint64)
+    if cb == 8:
+        return b.astype(np.int64)
+    if cb == 4:
+        out = np.empty(n, np.int64)
+        out[0::2] = b & 0xF
+        out[1::2] = b >> 4
+        return out
+    g = b.reshape(-1, 3)
+    w = g[:, 0] | (g[:, 1] << 8) | (g[:, 2] << 16)
+    return np.stack([(w >> (6 * j)) & 0x3F for j in range(4)], 1).reshape(-1).astype(np.int64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,qmax", MX)
+def test_packed_mx_codes_e8m0_and_decode(vqx, dtype, qmax):
+    x = c3_input(256, 2048)
+    sc, codes = Q.quantize_mx_packed(x.cuda(), dtype, -1, 32, True, qmax, "e8m0")
+    ws, wq = R.quantize_mx(x, oracle_qmap(dtype), [-1], 32, qmax, True)
+    # E8M0 byte = biased exponent of the reference's power-of-two scale
+    want_e8 = ((ws.float().view(torch.int32) >> 23) & 0xFF).to(torch.uint8)
+    assert torch.equal(sc.cpu(), want_e8)
+    eb, mb, _, _ = F.fp_core_params(dtype)
+    got_codes = unpack(codes, eb + mb + 1, x.numel())
+    assert np.array_equal(got_codes, ocp_code(wq.float().reshape(-1).numpy(), eb, mb))
+    # decode(codes, E8M0) = the reference's fake-quant values
+    dq = Q.dequantize_mx_packed(codes, sc, dtype, 32, list(x.shape), torch.bfloat16)
+    assert_bitexact(dq.cpu(), wq * R.expand(ws, wq.shape, 32), f"{dtype} decode")
+    # bf16 / fp32 scale outputs carry the reference scale exactly
+    sb, codes2 = Q.quantize_mx_packed(x.cuda(), dtype, -1, 32, True, qmax, "bfloat16")
+    assert_bitexact(sb.cpu(), ws, "bf16 scales")
+    assert torch.equal(codes2, codes)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,qmax", MX)
+def test_mx_fake_quant_module(vqx, dtype, qmax):
+    from voyager_compiler_amd.quantization import QuantizationSpec
+
+    spec = QuantizationSpec.from_str(f"{dtype},qs=microscaling,bs=32,ax=-1")
+    fq = spec.make_fake_quantize(device="cuda").cuda()
+    fq.force_scale_power_of_two = True
+    x = torch.cat([c3_input(120, 512), edge_rows(512)])
+    y = fq(x.cuda())
+    ws, wy = R.mx_fake_quantize(x, oracle_qmap(dtype), [-1], 32, qmax, True)
+    assert_bitexact(y.cpu(), wy, f"{dtype} fake-quant")
+    assert_bitexact(fq.scale.cpu().to(torch.bfloat16), ws, "module scale")
+
+
+def c2_input(rows, cols, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    w = 0.02 * torch.randn(rows, cols, generator=g)
+    n = round(0.001 * w.numel())
+    idx = torch.randperm(w.numel(), generator=g)[:n]
+    sign = torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0)
+    w.view(-1)[idx] = sign * 8 * 0.02
+    return w.to(torch.bfloat16)
+
+
+@pytest.mark.gpu
+def test_nf4_block64_c2(vqx):
+    x = torch.cat([c2_input(512, 1024), edge_rows(1024)])
+    sc, codes = Q.quantize_mx_packed(x.cuda(), "nf4", -1, 64, False, 1.0, "float32")
+    lv = F.nf_levels(4)
+    idx_table = F.nf_index_table(lv)
+    # oracle: absmax scale (qmax 1), the reference's quantize with the index
+    # table that convert installs for codebook dtypes (quantize_pt2e.py:456-466)
+    ws = R.calculate_mx_qparam(x, [-1], 64, 1.0, False)
+    idx_q = torch.from_numpy(idx_table.astype(np.float32)).to(torch.bfloat16)
+    wq = R.quantize(x, ws, None, [-1], 64, idx_q)
+    assert_bitexact(sc.cpu(), ws.float(), "nf4 scales")
+    got = unpack(codes, 4, x.numel())
+    assert np.array_equal(got, wq.float().reshape(-1).numpy().astype(np.int64))
+    # round trip: bf16(level[code] * scale), as linear_mx decodes
+    dq = Q.dequantize_mx_packed(codes, sc, "nf4", 64, list(x.shape), torch.bfloat16)
+    levels = R.table_tensor(lv)
+    want = levels[wq.long()] * R.expand(ws, x.shape, 64)
+    assert_bitexact(dq.cpu(), want, "nf4 decode")
+
+
+@pytest.mark.gpu
+def test_nf4_fake_quant_module(vqx):
+    from voyager_compiler_amd.quantization import QuantizationSpec
+
+    fq = QuantizationSpec.from_str("nf4,qs=microscaling,bs=64,ax=-1").make_fake_quantize("cuda").cuda()
+    x = c2_input(64, 1024)
+    y = fq(x.cuda())
+    qmap = R.table_tensor(F.quantization_table("nf4"))
+    ws, wy = R.mx_fake_quantize(x, qmap, [-1], 64, 1.0, False)
+    assert_bitexact(y.cpu(), wy, "nf4 fake-quant")

@@ -1,0 +1,479 @@
+// Blockwise kernels: the MX / absmax block scale (calculate_mx_qparam) fused
+// with the element encode (quantize / quantize_mx), with every output the
+// path needs written in the same pass: the reference's scale and quantized
+// values, the fake-quant product, packed codes, fp32 and E8M0 scales.  Plus
+// the decode of packed codes back to values (dequantize).
+#include <type_traits>
+
+#include "vqx_kernels.h"
+
+namespace vqx {
+
+// ---------------------------------------------------------------------------
+// dtype traits for blockwise inputs
+// ---------------------------------------------------------------------------
+template <typename T>
+struct BT;
+
+template <>
+struct BT<uint16_t> {  // bf16 bits
+  static constexpr uint32_t kMagMask = 0x7FFFu;
+  static constexpr uint32_t kInf = 0x7F80u;
+  __device__ static uint32_t bits(const uint16_t* p) { return *p; }
+  __device__ static float val(uint32_t b) { return u2f(b << 16); }
+  __device__ static uint32_t round_bits(float f) { return f2bf(f); }
+  __device__ static void load16(const uint16_t* p, uint32_t (&b)[16]) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(p);
+    u32x4 a0 = ld_nt(q), a1 = ld_nt(q + 1);
+    uint32_t w[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      b[2 * j] = w[j] & 0xFFFFu;
+      b[2 * j + 1] = w[j] >> 16;
+    }
+  }
+  __device__ static void store16(uint16_t* p, const uint32_t (&b)[16]) {
+    u32x4* q = reinterpret_cast<u32x4*>(p);
+    u32x4 a0 = {b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+    u32x4 a1 = {b[8] | (b[9] << 16), b[10] | (b[11] << 16), b[12] | (b[13] << 16),
+                b[14] | (b[15] << 16)};
+    st_nt(q, a0);
+    st_nt(q + 1, a1);
+  }
+  __device__ static void put(uint16_t* p, uint32_t b) { *p = (uint16_t)b; }
+};
+
+template <>
+struct BT<float> {
+  static constexpr uint32_t kMagMask = 0x7FFFFFFFu;
+  static constexpr uint32_t kInf = 0x7F800000u;
+  __device__ static uint32_t bits(const float* p) { return f2u(*p); }
+  __device__ static float val(uint32_t b) { return u2f(b); }
+  __device__ static uint32_t round_bits(float f) { return f2u(f); }
+  __device__ static void load16(const float* p, uint32_t (&b)[16]) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      u32x4 a = ld_nt(q + k);
+      b[4 * k] = a.x;
+      b[4 * k + 1] = a.y;
+      b[4 * k + 2] = a.z;
+      b[4 * k + 3] = a.w;
+    }
+  }
+  __device__ static void store16(float* p, const uint32_t (&b)[16]) {
+    u32x4* q = reinterpret_cast<u32x4*>(p);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      u32x4 a = {b[4 * k], b[4 * k + 1], b[4 * k + 2], b[4 * k + 3]};
+      st_nt(q + k, a);
+    }
+  }
+  __device__ static void put(float* p, uint32_t b) { *reinterpret_cast<uint32_t*>(p) = b; }
+};
+
+// ---------------------------------------------------------------------------
+// block scale  (ops/quantized.py:442-499, mx_utils.py:16-59)
+// ---------------------------------------------------------------------------
+// floor(log2) of a block amax, in the input dtype's arithmetic.  bf16: the
+// bf16-rounded log (see log2floor_bf16).  fp32: the correctly rounded fp32
+// log, which steps up exactly when the 23-bit mantissa reaches
+// 2^23 (2^(1 - u/2) - 1), u the fp32 spacing next to the integer above.
+__device__ __forceinline__ int log2floor_f32(uint32_t mag) {
+  uint32_t E = mag >> 23, m = mag & 0x7FFFFFu;
+  if (E == 0) return (31 - clz32(m)) - 149;  // subnormal amax: floor of the exact log
+  int p = (int)E - 127;
+  int band;
+  if (p >= 0) {
+    uint32_t n = (uint32_t)p + 1u;
+    band = 31 - clz32(n);
+    if ((n & (n - 1u)) == 0) band -= 1;
+  } else if (p == -1) {
+    return p;
+  } else {
+    uint32_t n = (uint32_t)(-p - 1);
+    band = 31 - clz32(n);
+  }
+  // The top J = floor(2^24 (1 - 2^(-u/2))) mantissas of the binade round up,
+  // u = 2^(band - 23); J by band -1 .. 6.
+  const uint32_t kTop[8] = {0, 0, 1, 2, 5, 11, 22, 44};
+  uint32_t J = kTop[band + 1];
+  return p + (J != 0 && m >= 0x800000u - J ? 1 : 0);
+}
+
+// Returns the block scale in the input dtype (as a float holding that value).
+template <typename T>
+__device__ __forceinline__ float block_scale(uint32_t amax_bits, const ScaleParams& sp) {
+  constexpr bool kBf16 = std::is_same<T, uint16_t>::value;
+  const uint32_t inf = BT<T>::kInf;
+  float scale;
+  if (sp.mode == 0) {
+    if (amax_bits > inf) return 1.0f;  // NaN amax -> NaN scale -> 1.0
+    if (amax_bits == inf) return __builtin_huge_valf();
+    // amax == 0 -> log2(2^-126) = -126 (mx_utils.py:45)
+    int e = amax_bits == 0 ? -126
+                           : (kBf16 ? log2floor_bf16(amax_bits) : log2floor_f32(amax_bits));
+    e -= sp.shift;
+    // 2**e in the input dtype: bf16 keeps 2^-133 .. 2^127, 2^-134 ties to 0
+    int lo = kBf16 ? -133 : -149;
+    if (e > 127)
+      scale = __builtin_huge_valf();
+    else if (e >= lo)
+      scale = exp2i(e);
+    else
+      scale = 0.0f;
+  } else {
+    float amax = BT<T>::val(amax_bits);
+    scale = BT<T>::val(BT<T>::round_bits(amax / sp.quant_max));
+    if (sp.scale_qmap) {
+      uint32_t h = f2bf(scale);
+      scale = BT<T>::val(BT<T>::round_bits(bf2f(sp.scale_qmap[h])));
+    }
+  }
+  // torch.where(scale > 0, scale, 1.0): zero and NaN scales become 1
+  return scale > 0.0f ? scale : 1.0f;
+}
+
+// E8M0 byte of a scale: 2^(byte - 127) for powers of two in [2^-127, 2^127],
+// 0xFF for +Inf; scales below E8M0's range clamp to 0x00 (the exact scale is
+// in the bf16/fp32 scale outputs).
+__device__ __forceinline__ uint32_t e8m0_of(float s) {
+  uint32_t b = f2u(s);
+  uint32_t E = (b >> 23) & 0xFFu;
+  if (E == 0xFFu) return 0xFFu;
+  return E;  // subnormal scales (2^-127 and below) give 0
+}
+
+// x / s rounded as the input dtype divides: exactly by the reciprocal when s
+// is a power of two whose reciprocal is a normal-or-exact fp32, else IEEE.
+template <typename T>
+__device__ __forceinline__ uint32_t div_to_bf16(float x, float s, float rcp, bool pow2) {
+  float q = pow2 ? x * rcp : x / s;
+  return f2bf(BT<T>::val(BT<T>::round_bits(q)));
+}
+
+// ---------------------------------------------------------------------------
+// packing helpers: element i of a group of 16 at bits [cb*i, cb*i + cb)
+// ---------------------------------------------------------------------------
+template <int CB>
+__device__ __forceinline__ void store_group_codes(uint8_t* base, int64_t g, const uint32_t (&c)[16]) {
+  if constexpr (CB == 4) {
+    u32x2 w;
+    w.x = 0;
+    w.y = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      w.x |= (c[j] & 0xFu) << (4 * j);
+      w.y |= (c[j + 8] & 0xFu) << (4 * j);
+    }
+    st_nt(reinterpret_cast<u32x2*>(base + g * 8), w);
+  } else if constexpr (CB == 6) {
+    uint32_t k[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) k[j] = c[j] & 0x3Fu;
+    uint32_t w0 = k[0] | (k[1] << 6) | (k[2] << 12) | (k[3] << 18) | (k[4] << 24) | (k[5] << 30);
+    uint32_t w1 = (k[5] >> 2) | (k[6] << 4) | (k[7] << 10) | (k[8] << 16) | (k[9] << 22) | (k[10] << 28);
+    uint32_t w2 = (k[10] >> 4) | (k[11] << 2) | (k[12] << 8) | (k[13] << 14) | (k[14] << 20) | (k[15] << 26);
+    uint32_t* q = reinterpret_cast<uint32_t*>(base + g * 12);
+    __builtin_nontemporal_store(w0, q);
+    __builtin_nontemporal_store(w1, q + 1);
+    __builtin_nontemporal_store(w2, q + 2);
+  } else if constexpr (CB == 8) {
+    u32x4 w;
+    w.x = (c[0] & 0xFF) | ((c[1] & 0xFF) << 8) | ((c[2] & 0xFF) << 16) | (c[3] << 24);
+    w.y = (c[4] & 0xFF) | ((c[5] & 0xFF) << 8) | ((c[6] & 0xFF) << 16) | (c[7] << 24);
+    w.z = (c[8] & 0xFF) | ((c[9] & 0xFF) << 8) | ((c[10] & 0xFF) << 16) | (c[11] << 24);
+    w.w = (c[12] & 0xFF) | ((c[13] & 0xFF) << 8) | ((c[14] & 0xFF) << 16) | (c[15] << 24);
+    st_nt(reinterpret_cast<u32x4*>(base + g * 16), w);
+  } else if constexpr (CB == 16) {
+    u32x4* q = reinterpret_cast<u32x4*>(base + g * 32);
+    u32x4 a = {(c[0] & 0xFFFF) | (c[1] << 16), (c[2] & 0xFFFF) | (c[3] << 16),
+               (c[4] & 0xFFFF) | (c[5] << 16), (c[6] & 0xFFFF) | (c[7] << 16)};
+    u32x4 b = {(c[8] & 0xFFFF) | (c[9] << 16), (c[10] & 0xFFFF) | (c[11] << 16),
+               (c[12] & 0xFFFF) | (c[13] << 16), (c[14] & 0xFFFF) | (c[15] << 16)};
+    st_nt(q, a);
+    st_nt(q + 1, b);
+  }
+}
+
+// Fast path: blocks of 16 * LPB contiguous elements (last-dim blocks), each
+// thread one 16-element group, the LPB threads of a block adjacent in the wave.
+template <typename T, typename Enc, int CB, int LPB>
+__global__ __launch_bounds__(256) void mx_group_kernel(const T* __restrict__ x, int64_t ngroups,
+                                                       ScaleParams sp, Enc enc, MxOut out) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
+    uint32_t b[16];
+    BT<T>::load16(x + g * 16, b);
+    uint32_t amax = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) amax = umax32(amax, b[j] & BT<T>::kMagMask);
+#pragma unroll
+    for (int off = 1; off < LPB; off <<= 1) amax = umax32(amax, (uint32_t)__shfl_xor((int)amax, off, 64));
+    float s = block_scale<T>(amax, sp);
+    uint32_t sb = f2u(s);
+    bool pow2 = (sb & 0x7FFFFFu) == 0 && ((sb >> 23) & 0xFF) >= 1 && ((sb >> 23) & 0xFF) <= 253;
+    float rcp = pow2 ? u2f((uint32_t)(254 - ((sb >> 23) & 0xFF)) << 23) : 0.0f;
+    uint32_t code[16], qv[16], fv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      uint32_t h = div_to_bf16<T>(BT<T>::val(b[j]), s, rcp, pow2);
+      Result r = enc.encode(h);
+      code[j] = r.code;
+      float v = BT<T>::val(BT<T>::round_bits(bf2f(r.value)));
+      qv[j] = BT<T>::round_bits(v);
+      if (std::is_same<T, uint16_t>::value) qv[j] = r.value;
+      fv[j] = BT<T>::round_bits(v * s);
+    }
+    if (out.qvals) BT<T>::store16(static_cast<T*>(out.qvals) + g * 16, qv);
+    if (out.fq) BT<T>::store16(static_cast<T*>(out.fq) + g * 16, fv);
+    if constexpr (CB > 0) store_group_codes<CB>(static_cast<uint8_t*>(out.codes), g, code);
+    if ((threadIdx.x & (LPB - 1)) == 0) {
+      int64_t blk = g / LPB;
+      if (out.scale) BT<T>::put(static_cast<T*>(out.scale) + blk, BT<T>::round_bits(s));
+      if (out.scale_f32) out.scale_f32[blk] = s;
+      if (out.scale_e8m0) out.scale_e8m0[blk] = (uint8_t)e8m0_of(s);
+    }
+  }
+}
+
+// General path: x viewed as [outer, L, inner], blocks of bs along L (the last
+// block may be short: the reference zero-pads it, which leaves its amax
+// unchanged).  One thread per block; codes unpacked (1 or 2 bytes each).
+template <typename T, typename Enc>
+__global__ __launch_bounds__(256) void mx_block_kernel(const T* __restrict__ x, int64_t outer, int64_t L,
+                                                       int64_t inner, int64_t bs, ScaleParams sp, Enc enc,
+                                                       MxOut out, int code_bytes) {
+  const int64_t nblk_l = (L + bs - 1) / bs;
+  const int64_t total = outer * nblk_l * inner;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+    // scale tensor index order = [outer, nblk_l, inner]
+    int64_t in = t % inner;
+    int64_t rest = t / inner;
+    int64_t bl = rest % nblk_l;
+    int64_t o = rest / nblk_l;
+    int64_t l0 = bl * bs;
+    int64_t l1 = l0 + bs < L ? l0 + bs : L;
+    const T* base = x + (o * L) * inner + in;
+    uint32_t amax = 0;
+    for (int64_t l = l0; l < l1; ++l) amax = umax32(amax, BT<T>::bits(base + l * inner) & BT<T>::kMagMask);
+    float s = block_scale<T>(amax, sp);
+    uint32_t sb = f2u(s);
+    bool pow2 = (sb & 0x7FFFFFu) == 0 && ((sb >> 23) & 0xFF) >= 1 && ((sb >> 23) & 0xFF) <= 253;
+    float rcp = pow2 ? u2f((uint32_t)(254 - ((sb >> 23) & 0xFF)) << 23) : 0.0f;
+    for (int64_t l = l0; l < l1; ++l) {
+      int64_t i = (o * L + l) * inner + in;
+      uint32_t xb = BT<T>::bits(x + i);
+      uint32_t h = div_to_bf16<T>(BT<T>::val(xb), s, rcp, pow2);
+      Result r = enc.encode(h);
+      float v = BT<T>::val(BT<T>::round_bits(bf2f(r.value)));
+      uint32_t q = std::is_same<T, uint16_t>::value ? r.value : BT<T>::round_bits(v);
+      if (out.qvals) BT<T>::put(static_cast<T*>(out.qvals) + i, q);
+      if (out.fq) BT<T>::put(static_cast<T*>(out.fq) + i, BT<T>::round_bits(v * s));
+      if (out.codes) {
+        if (code_bytes == 1) static_cast<uint8_t*>(out.codes)[i] = (uint8_t)r.code;
+        else static_cast<uint16_t*>(out.codes)[i] = (uint16_t)r.code;
+      }
+    }
+    if (out.scale) BT<T>::put(static_cast<T*>(out.scale) + t, BT<T>::round_bits(s));
+    if (out.scale_f32) out.scale_f32[t] = s;
+    if (out.scale_e8m0) out.scale_e8m0[t] = (uint8_t)e8m0_of(s);
+  }
+}
+
+template <typename T, typename Enc, int CB>
+static int launch_group(const T* x, int64_t n, int lpb, const ScaleParams& sp, const Enc& enc,
+                        const MxOut& out, hipStream_t st) {
+  int64_t ngroups = n / 16;
+  const int bs = 256;
+  unsigned grid = grid_for(ngroups, bs);
+  switch (lpb) {
+#define VQX_LPB(L)                                                                                 \
+  case L:                                                                                          \
+    hipLaunchKernelGGL((mx_group_kernel<T, Enc, CB, L>), dim3(grid), dim3(bs), 0, st, x, ngroups, \
+                       sp, enc, out);                                                              \
+    break;
+    VQX_LPB(1)
+    VQX_LPB(2)
+    VQX_LPB(4)
+    VQX_LPB(8)
+#undef VQX_LPB
+    default:
+      return set_error(kErrInvalid, "block size %d not supported on the packed path", lpb * 16);
+  }
+  return check_launch("mx_quantize");
+}
+
+template <typename T, typename Enc>
+static int mx_quantize_t(const T* x, int64_t outer, int64_t L, int64_t inner, int64_t bs,
+                         const ScaleParams& sp, const Enc& enc, const MxOut& out, int code_layout,
+                         int code_bits, hipStream_t st) {
+  int64_t n = outer * L * inner;
+  if (n == 0) return kOk;
+  int64_t lpb = bs / 16;
+  bool fast = inner == 1 && bs % 16 == 0 && L % bs == 0 && lpb >= 1 && lpb <= 8 &&
+              (lpb & (lpb - 1)) == 0 && aligned(x, 16) &&
+              (!out.qvals || aligned(out.qvals, 16)) && (!out.fq || aligned(out.fq, 16)) &&
+              (!out.codes || aligned(out.codes, 16));
+  if (out.codes && code_layout == 0) {  // packed codes need the group path
+    if (!fast)
+      return set_error(kErrInvalid,
+                       "packed codes need last-dim blocks (inner == 1), block size 16, 32, 64 or 128 "
+                       "dividing the row, and 16-byte aligned buffers");
+    if constexpr (Enc::kBits != 0) {
+      if (code_bits != Enc::kBits)
+        return set_error(kErrInvalid, "format packs %d-bit codes, not %d", Enc::kBits, code_bits);
+      return launch_group<T, Enc, Enc::kBits>(x, n, (int)lpb, sp, enc, out, st);
+    } else {
+      switch (code_bits) {
+        case 4: return launch_group<T, Enc, 4>(x, n, (int)lpb, sp, enc, out, st);
+        case 6: return launch_group<T, Enc, 6>(x, n, (int)lpb, sp, enc, out, st);
+        case 8: return launch_group<T, Enc, 8>(x, n, (int)lpb, sp, enc, out, st);
+        case 16: return launch_group<T, Enc, 16>(x, n, (int)lpb, sp, enc, out, st);
+        default: return set_error(kErrInvalid, "packed code width %d not in {4, 6, 8, 16}", code_bits);
+      }
+    }
+  }
+  if (fast && !out.codes) return launch_group<T, Enc, 0>(x, n, (int)lpb, sp, enc, out, st);
+  if (out.codes && code_layout != 1 && code_layout != 2)
+    return set_error(kErrInvalid, "unpacked code layout must be 1 or 2 bytes");
+  int64_t nblocks = outer * ((L + bs - 1) / bs) * inner;
+  unsigned grid = grid_for(nblocks, 256);
+  hipLaunchKernelGGL((mx_block_kernel<T, Enc>), dim3(grid), dim3(256), 0, st, x, outer, L, inner, bs, sp,
+                     enc, out, code_layout);
+  return check_launch("mx_quantize");
+}
+
+int mx_quantize(const void* x, int dtype, int64_t outer, int64_t L, int64_t inner, int64_t bs,
+                const FormatDesc& fmt, const ScaleParams& sp, const MxOut& out, int code_layout,
+                hipStream_t st) {
+  if (outer < 0 || L < 0 || inner < 1 || bs < 1)
+    return set_error(kErrInvalid, "bad block geometry outer=%lld L=%lld inner=%lld bs=%lld",
+                     (long long)outer, (long long)L, (long long)inner, (long long)bs);
+  if (code_layout < 0 || code_layout > 2) return set_error(kErrInvalid, "code layout must be 0, 1 or 2");
+  if (out.scale_e8m0 && sp.mode != 0)
+    return set_error(kErrInvalid, "E8M0 scales need power-of-two scaling");
+  return with_encoder(fmt, [&](auto enc) -> int {
+    using E = decltype(enc);
+    if (dtype == kBF16)
+      return mx_quantize_t<uint16_t, E>((const uint16_t*)x, outer, L, inner, bs, sp, enc, out,
+                                        code_layout, fmt.code_bits, st);
+    if (dtype == kF32)
+      return mx_quantize_t<float, E>((const float*)x, outer, L, inner, bs, sp, enc, out, code_layout,
+                                     fmt.code_bits, st);
+    return set_error(kErrInvalid, "blockwise input dtype %d not supported (float32, bfloat16)", dtype);
+  });
+}
+
+// ---------------------------------------------------------------------------
+// decode: codes -> value table -> times the block scale, in the output dtype
+// (dequantize, ops/quantized.py:211-222; linear_mx's weight decode :319-326)
+// ---------------------------------------------------------------------------
+// scale_kind: 0 fp32, 1 bf16, 2 E8M0
+__device__ __forceinline__ float load_scale(const void* s, int kind, int64_t i) {
+  if (kind == 0) return static_cast<const float*>(s)[i];
+  if (kind == 1) return bf2f(static_cast<const uint16_t*>(s)[i]);
+  uint32_t e = static_cast<const uint8_t*>(s)[i];
+  return e == 0xFFu ? __builtin_huge_valf() : (e == 0 ? u2f(0x00400000u) : u2f(e << 23));
+}
+
+template <typename T, int CB, int LPB>
+__global__ __launch_bounds__(256) void decode_group_kernel(const uint8_t* __restrict__ codes,
+                                                           const void* __restrict__ scale, int scale_kind,
+                                                           const uint16_t* __restrict__ dtab, int ntab,
+                                                           T* __restrict__ out, int64_t ngroups) {
+  __shared__ uint16_t tab[1 << (CB > 8 ? 8 : CB)];
+  for (int i = threadIdx.x; i < ntab && i < (1 << (CB > 8 ? 8 : CB)); i += blockDim.x) tab[i] = dtab[i];
+  __syncthreads();
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
+    uint32_t c[16];
+    if constexpr (CB == 4) {
+      u32x2 w = ld_nt(reinterpret_cast<const u32x2*>(codes + g * 8));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        c[j] = (w.x >> (4 * j)) & 0xFu;
+        c[j + 8] = (w.y >> (4 * j)) & 0xFu;
+      }
+    } else if constexpr (CB == 6) {
+      const uint32_t* q = reinterpret_cast<const uint32_t*>(codes + g * 12);
+      uint32_t w0 = __builtin_nontemporal_load(q), w1 = __builtin_nontemporal_load(q + 1),
+               w2 = __builtin_nontemporal_load(q + 2);
+      uint64_t lo = (uint64_t)w0 | ((uint64_t)w1 << 32);
+#pragma unroll
+      for (int j = 0; j < 10; ++j) c[j] = (uint32_t)(lo >> (6 * j)) & 0x3Fu;
+      c[10] = ((w1 >> 28) | (w2 << 4)) & 0x3Fu;
+#pragma unroll
+      for (int j = 11; j < 16; ++j) c[j] = (w2 >> (6 * j - 64)) & 0x3Fu;
+    } else {
+      u32x4 w = ld_nt(reinterpret_cast<const u32x4*>(codes + g * 16));
+      uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) c[j] = (ww[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+    }
+    float s = load_scale(scale, scale_kind, g / LPB);
+    uint32_t o[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[j] = BT<T>::round_bits(bf2f(tab[c[j]]) * s);
+    BT<T>::store16(out + g * 16, o);
+  }
+}
+
+int mx_decode(const uint8_t* codes, int code_bits, const uint16_t* decode_table, int ntab,
+              const void* scale, int scale_kind, int64_t n, int64_t bs, void* out, int out_dtype,
+              hipStream_t st) {
+  if (n == 0) return kOk;
+  int64_t lpb = bs / 16;
+  if (n % bs != 0 || bs % 16 != 0 || lpb > 8 || (lpb & (lpb - 1)) != 0 || !aligned(codes, 16) ||
+      !aligned(out, 16))
+    return set_error(kErrInvalid, "decode needs n %% bs == 0, bs in {16, 32, 64, 128}, aligned buffers");
+  if (code_bits != 4 && code_bits != 6 && code_bits != 8)
+    return set_error(kErrInvalid, "decode code width %d not in {4, 6, 8}", code_bits);
+  if (scale_kind < 0 || scale_kind > 2) return set_error(kErrInvalid, "scale kind must be 0, 1 or 2");
+  int64_t ngroups = n / 16;
+  unsigned grid = grid_for(ngroups, 256);
+#define VQX_DEC(T, CB, L)                                                                      \
+  hipLaunchKernelGGL((decode_group_kernel<T, CB, L>), dim3(grid), dim3(256), 0, st, codes, scale, \
+                     scale_kind, decode_table, ntab, (T*)out, ngroups)
+#define VQX_DEC_L(T, CB)            \
+  switch (lpb) {                    \
+    case 1: VQX_DEC(T, CB, 1); break;  \
+    case 2: VQX_DEC(T, CB, 2); break;  \
+    case 4: VQX_DEC(T, CB, 4); break;  \
+    default: VQX_DEC(T, CB, 8); break;  \
+  }
+  if (out_dtype == kBF16) {
+    if (code_bits == 4) { VQX_DEC_L(uint16_t, 4) }
+    else if (code_bits == 6) { VQX_DEC_L(uint16_t, 6) }
+    else { VQX_DEC_L(uint16_t, 8) }
+  } else if (out_dtype == kF32) {
+    if (code_bits == 4) { VQX_DEC_L(float, 4) }
+    else if (code_bits == 6) { VQX_DEC_L(float, 6) }
+    else { VQX_DEC_L(float, 8) }
+  } else {
+    return set_error(kErrInvalid, "decode output dtype %d not supported", out_dtype);
+  }
+#undef VQX_DEC_L
+#undef VQX_DEC
+  return check_launch("mx_decode");
+}
+
+// Inverse table of a format: dtab[code] = value for every code some bf16
+// pattern encodes to (all patterns sharing a code share its value).
+template <typename Enc>
+__global__ __launch_bounds__(256) void decode_table_kernel(uint16_t* dtab, int ntab, Enc enc) {
+  uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= 65536u) return;
+  Result r = enc.encode(h);
+  if ((int)r.code < ntab && (h & 0x7FFFu) <= 0x7F80u) dtab[r.code] = (uint16_t)r.value;
+}
+
+int decode_table(const FormatDesc& fmt, uint16_t* dtab, int ntab, hipStream_t st) {
+  return with_encoder(fmt, [&](auto enc) {
+    hipLaunchKernelGGL((decode_table_kernel<decltype(enc)>), dim3(256), dim3(256), 0, st, dtab, ntab, enc);
+    return check_launch("decode_table");
+  });
+}
+
+}  // namespace vqx

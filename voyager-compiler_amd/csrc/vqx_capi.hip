@@ -1,0 +1,189 @@
+// C ABI of libvqx.so (declared in include/vqx.h): argument checks, the
+// thread-local error message, and dispatch into the kernel families.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/vqx.h"
+#include "vqx_kernels.h"
+
+namespace vqx {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(kErrLaunch, "%s: %s", what, hipGetErrorString(e));
+  return kOk;
+}
+
+int num_cus() {
+  static thread_local int cached_dev = -1, cached_cus = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached_dev = dev;
+    cached_cus = cus;
+  }
+  return cached_cus;
+}
+
+static int to_desc(const vqx_format* f, FormatDesc* d) {
+  if (!f) return set_error(kErrInvalid, "format descriptor is NULL");
+  d->kind = f->kind;
+  d->p0 = f->p0;
+  d->p1 = f->p1;
+  d->flags = f->flags;
+  d->max_norm = f->max_norm;
+  d->code_bits = f->code_bits;
+  d->boundaries = f->boundaries;
+  d->levels = f->levels;
+  d->code_table = f->code_table;
+  d->value_table = f->value_table;
+  return kOk;
+}
+
+static int to_map(const vqx_scale_map* sm, ScaleMap* m) {
+  if (!sm) {
+    *m = ScaleMap{nullptr, nullptr, 1, 1, 1, 0, 0, 0};
+    return kOk;
+  }
+  *m = ScaleMap{sm->scale, sm->zero_point, sm->L, sm->inner, sm->block, sm->s_o, sm->s_l, sm->s_in};
+  return kOk;
+}
+
+}  // namespace vqx
+
+using namespace vqx;
+
+#define VQX_TRY(expr)          \
+  do {                         \
+    int _rc = (expr);          \
+    if (_rc != kOk) return _rc; \
+  } while (0)
+
+extern "C" {
+
+const char* vqx_version(void) { return "vqx 0.1.0 gfx950"; }
+
+const char* vqx_last_error(void) { return g_err; }
+
+int vqx_device_cus(void) { return num_cus(); }
+
+int vqx_vmap(const void* x, int32_t x_dtype, int64_t n, const uint16_t* table, void* y,
+             vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (n > 0 && (!x || !y)) return set_error(kErrInvalid, "vmap: null tensor");
+  return lut_gather(x, x_dtype, n, table, y, (hipStream_t)stream);
+}
+
+int vqx_fake_quant(const void* x, int32_t x_dtype, int64_t n, const vqx_format* fmt,
+                   const float* scale, int64_t scale_numel, int64_t scale_inner, int32_t mul_back,
+                   void* y, void* codes, int32_t code_bytes, vqx_stream_t stream) {
+  g_err[0] = 0;
+  FormatDesc d;
+  VQX_TRY(to_desc(fmt, &d));
+  if (n > 0 && !x) return set_error(kErrInvalid, "fake_quant: null input");
+  if (!codes) code_bytes = 0;
+  if (scale && scale_numel < 1) return set_error(kErrInvalid, "fake_quant: scale_numel must be >= 1");
+  return fake_quant(x, x_dtype, n, d, scale, scale ? scale_numel : 1, scale_inner, mul_back != 0, y,
+                    codes, code_bytes, (hipStream_t)stream);
+}
+
+int vqx_quantize_mapped(const void* x, int32_t x_dtype, int64_t n, const vqx_format* fmt,
+                        const vqx_scale_map* sm, int32_t mul_back, void* y, void* codes,
+                        int32_t code_bytes, vqx_stream_t stream) {
+  g_err[0] = 0;
+  FormatDesc d;
+  VQX_TRY(to_desc(fmt, &d));
+  ScaleMap m;
+  VQX_TRY(to_map(sm, &m));
+  if (n > 0 && !x) return set_error(kErrInvalid, "quantize: null input");
+  return quantize_mapped(x, x_dtype, n, d, m, mul_back != 0, y, codes, code_bytes, (hipStream_t)stream);
+}
+
+int vqx_dequantize_mapped(const void* x, int32_t x_dtype, int64_t n, const uint16_t* input_qmap,
+                          const vqx_scale_map* sm, const uint16_t* output_qmap, void* y,
+                          vqx_stream_t stream) {
+  g_err[0] = 0;
+  ScaleMap m;
+  VQX_TRY(to_map(sm, &m));
+  if (n > 0 && (!x || !y)) return set_error(kErrInvalid, "dequantize: null tensor");
+  return dequantize_mapped(x, x_dtype, n, input_qmap, m, output_qmap, y, (hipStream_t)stream);
+}
+
+int vqx_build_table(const vqx_format* fmt, uint16_t* values, uint16_t* codes, vqx_stream_t stream) {
+  g_err[0] = 0;
+  FormatDesc d;
+  VQX_TRY(to_desc(fmt, &d));
+  return build_table(d, values, codes, (hipStream_t)stream);
+}
+
+int vqx_level_tables(const float* levels, int32_t K, int32_t mode, uint8_t* index_table,
+                     float* boundaries, uint32_t* work, int32_t* bad, vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (!levels || !index_table || (K > 1 && (!boundaries || !work || !bad)))
+    return set_error(kErrInvalid, "level_tables: null buffer");
+  if (mode != 0 && mode != 1) return set_error(kErrInvalid, "level_tables: mode must be 0 or 1");
+  return level_tables(levels, K, mode, index_table, boundaries, work, bad, (hipStream_t)stream);
+}
+
+int vqx_mx_quantize(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                    int64_t block_size, const vqx_format* fmt, int32_t scale_mode, int32_t pow2_shift,
+                    float quant_max, const uint16_t* scale_qmap, void* scale_out, float* scale_f32,
+                    uint8_t* scale_e8m0, void* qvals, void* fq, void* codes, int32_t code_layout,
+                    vqx_stream_t stream) {
+  g_err[0] = 0;
+  FormatDesc d;
+  VQX_TRY(to_desc(fmt, &d));
+  if (!x && outer * L * inner > 0) return set_error(kErrInvalid, "mx_quantize: null input");
+  if (scale_mode != 0 && scale_mode != 1) return set_error(kErrInvalid, "mx_quantize: scale_mode must be 0 or 1");
+  ScaleParams sp{scale_mode, pow2_shift, quant_max, scale_qmap};
+  MxOut out{scale_out, scale_f32, scale_e8m0, qvals, fq, codes};
+  return mx_quantize(x, x_dtype, outer, L, inner, block_size, d, sp, out, code_layout, (hipStream_t)stream);
+}
+
+int vqx_mx_decode(const uint8_t* codes, int32_t code_bits, const uint16_t* decode_table, int32_t ntab,
+                  const void* scale, int32_t scale_kind, int64_t n, int64_t block_size, void* out,
+                  int32_t out_dtype, vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (n > 0 && (!codes || !decode_table || !scale || !out))
+    return set_error(kErrInvalid, "mx_decode: null buffer");
+  if (block_size < 1) return set_error(kErrInvalid, "mx_decode: block_size must be >= 1");
+  return mx_decode(codes, code_bits, decode_table, ntab, scale, scale_kind, n, block_size, out, out_dtype,
+                   (hipStream_t)stream);
+}
+
+int vqx_decode_table(const vqx_format* fmt, uint16_t* dtab, int32_t ntab, vqx_stream_t stream) {
+  g_err[0] = 0;
+  FormatDesc d;
+  VQX_TRY(to_desc(fmt, &d));
+  if (!dtab || ntab < 1 || ntab > 65536) return set_error(kErrInvalid, "decode_table: bad table");
+  return decode_table(d, dtab, ntab, (hipStream_t)stream);
+}
+
+int vqx_codebook_encode(const void* x, int32_t x_dtype, int64_t rows, int64_t cols, const float* cb,
+                        int32_t K, uint8_t* codes, vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (rows * cols > 0 && (!x || !cb || !codes)) return set_error(kErrInvalid, "codebook_encode: null buffer");
+  return codebook_encode(x, x_dtype, rows, cols, cb, K, codes, (hipStream_t)stream);
+}
+
+int vqx_codebook_decode(const uint8_t* codes, int64_t rows, int64_t cols, const float* cb, int32_t K,
+                        void* out, int32_t out_dtype, vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (rows * cols > 0 && (!codes || !cb || !out)) return set_error(kErrInvalid, "codebook_decode: null buffer");
+  return codebook_decode(codes, rows, cols, cb, K, out, out_dtype, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,72 @@
+// Shared HIP plumbing for the vqx kernels: error state, launch sizing,
+// streaming loads/stores and wave64 reductions.  gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vqx_formats.h"
+
+namespace vqx {
+
+// ---------------------------------------------------------------------------
+// error state (thread-local message; entry points return a negative status)
+// ---------------------------------------------------------------------------
+enum Status : int {
+  kOk = 0,
+  kErrInvalid = -1,   // bad argument: shape, dtype, alignment, format
+  kErrLaunch = -2,    // kernel launch / HIP runtime failure
+  kErrUnsupported = -3,
+};
+
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+int num_cus();
+
+// dtype tags used across the C ABI
+enum DType : int32_t {
+  kF32 = 0,
+  kBF16 = 1,
+  kF16 = 2,
+  kU8 = 3,
+  kI64 = 4,
+};
+
+// ---------------------------------------------------------------------------
+// memory helpers
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T ld_nt(const T* p) {
+  return __builtin_nontemporal_load(p);
+}
+template <typename T>
+__device__ __forceinline__ void st_nt(T* p, T v) {
+  __builtin_nontemporal_store(v, p);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) {
+  return a > b ? a : b;
+}
+
+// Round-to-nearest-even fp32 -> bf16 pattern, every NaN to 0x7FC0.
+__device__ __forceinline__ uint32_t f2bf_dev(float f) { return f2bf(f); }
+
+// Grid sizing: enough workgroups to cover the work, capped at a few per CU;
+// kernels loop grid-stride beyond that.
+inline unsigned grid_for(int64_t work_items, int per_block, int max_per_cu = 8) {
+  int64_t need = (work_items + per_block - 1) / per_block;
+  int64_t cap = (int64_t)num_cus() * max_per_cu;
+  if (need < 1) need = 1;
+  return (unsigned)(need < cap ? need : cap);
+}
+
+inline bool aligned(const void* p, unsigned a) {
+  return ((uintptr_t)p & (a - 1)) == 0;
+}
+
+}  // namespace vqx

@@ -1,0 +1,480 @@
+// Elementwise kernels: the LUT gather behind quantized_ops::vmap, the
+// closed-form per-tensor fake-quant (FakeQuantizeFunction) with optional
+// format codes, and the setup kernels that tabulate a format over all 2^16
+// bf16 patterns (get_quantization_map) and derive level-set boundaries.
+#include <math.h>
+
+#include <type_traits>
+
+#include "vqx_kernels.h"
+
+namespace vqx {
+
+// ---------------------------------------------------------------------------
+// element access by dtype
+// ---------------------------------------------------------------------------
+template <typename T>
+struct IO;
+
+template <>
+struct IO<float> {
+  static constexpr int kVec = 8;  // elements per thread per step (2 x 16 B)
+  __device__ static void load(const float* p, float (&v)[8]) {
+    f32x4 a = ld_nt(reinterpret_cast<const f32x4*>(p));
+    f32x4 b = ld_nt(reinterpret_cast<const f32x4*>(p) + 1);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  __device__ static void store(float* p, const float (&v)[8]) {
+    f32x4 a = {v[0], v[1], v[2], v[3]};
+    f32x4 b = {v[4], v[5], v[6], v[7]};
+    st_nt(reinterpret_cast<f32x4*>(p), a);
+    st_nt(reinterpret_cast<f32x4*>(p) + 1, b);
+  }
+  __device__ static float get(const float* p) { return *p; }
+  __device__ static void put(float* p, float v) { *p = v; }
+};
+
+template <>
+struct IO<uint16_t> {  // bf16 stored as raw bits
+  static constexpr int kVec = 8;  // 1 x 16 B
+  __device__ static void load(const uint16_t* p, float (&v)[8]) {
+    u32x4 a = ld_nt(reinterpret_cast<const u32x4*>(p));
+    uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = u2f(w[j] << 16);
+      v[2 * j + 1] = u2f(w[j] & 0xFFFF0000u);
+    }
+  }
+  // values already rounded to bf16 (their low 16 bits are zero)
+  __device__ static void store(uint16_t* p, const float (&v)[8]) {
+    u32x4 a;
+    a.x = (f2u(v[0]) >> 16) | (f2u(v[1]) & 0xFFFF0000u);
+    a.y = (f2u(v[2]) >> 16) | (f2u(v[3]) & 0xFFFF0000u);
+    a.z = (f2u(v[4]) >> 16) | (f2u(v[5]) & 0xFFFF0000u);
+    a.w = (f2u(v[6]) >> 16) | (f2u(v[7]) & 0xFFFF0000u);
+    st_nt(reinterpret_cast<u32x4*>(p), a);
+  }
+  __device__ static float get(const uint16_t* p) { return u2f((uint32_t)*p << 16); }
+  __device__ static void put(uint16_t* p, float v) { *p = (uint16_t)(f2u(v) >> 16); }
+};
+
+template <>
+struct IO<__half> {
+  static constexpr int kVec = 8;
+  __device__ static void load(const __half* p, float (&v)[8]) {
+    u32x4 a = ld_nt(reinterpret_cast<const u32x4*>(p));
+    uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      __half lo = __ushort_as_half((unsigned short)(w[j] & 0xFFFFu));
+      __half hi = __ushort_as_half((unsigned short)(w[j] >> 16));
+      v[2 * j] = __half2float(lo);
+      v[2 * j + 1] = __half2float(hi);
+    }
+  }
+  __device__ static void store(__half* p, const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t lo = __half_as_ushort(__float2half_rn(v[2 * j]));
+      uint32_t hi = __half_as_ushort(__float2half_rn(v[2 * j + 1]));
+      w[j] = lo | (hi << 16);
+    }
+    u32x4 a = {w[0], w[1], w[2], w[3]};
+    st_nt(reinterpret_cast<u32x4*>(p), a);
+  }
+  __device__ static float get(const __half* p) { return __half2float(*p); }
+  __device__ static void put(__half* p, float v) { *p = __float2half_rn(v); }
+};
+
+// Rounding of a float to the input dtype, as torch stores an op result.
+template <typename T>
+__device__ __forceinline__ float to_dtype(float v);
+template <>
+__device__ __forceinline__ float to_dtype<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_dtype<uint16_t>(float v) { return bf2f(f2bf(v)); }
+template <>
+__device__ __forceinline__ float to_dtype<__half>(float v) {
+  return __half2float(__float2half_rn(v));
+}
+
+// One element of FakeQuantizeFunction.forward (fake_quantize.py:112-115):
+//   s = scale.to(x.dtype);  y = vmap(x / s, qmap) * s
+// where every op rounds to x's dtype and vmap first casts to bf16
+// (quantized.py:107-108).  unit: s == 1, so the division and product are
+// identities and are skipped; a bf16 input then indexes the table with its
+// raw bits and the table entry is stored as is, like the reference's gather.
+template <typename T, typename Enc>
+__device__ __forceinline__ float fq_one(float x, float s, bool unit, bool mul, const Enc& enc,
+                                        uint32_t& code) {
+  constexpr bool kBf16 = std::is_same<T, uint16_t>::value;
+  uint32_t h;
+  if (unit)
+    h = kBf16 ? (f2u(x) >> 16) : f2bf(x);
+  else
+    h = f2bf(to_dtype<T>(x / s));
+  Result r = enc.encode(h);
+  code = r.code;
+  if (unit) return kBf16 ? u2f(r.value << 16) : to_dtype<T>(bf2f(r.value));
+  float v = to_dtype<T>(bf2f(r.value));
+  return mul ? to_dtype<T>(v * s) : v;
+}
+
+template <int CB>
+__device__ __forceinline__ void store_codes8(void* codes, int64_t i, const uint32_t (&c)[8]) {
+  if constexpr (CB == 1) {
+    u32x2 w;
+    w.x = (c[0] & 0xFF) | ((c[1] & 0xFF) << 8) | ((c[2] & 0xFF) << 16) | (c[3] << 24);
+    w.y = (c[4] & 0xFF) | ((c[5] & 0xFF) << 8) | ((c[6] & 0xFF) << 16) | (c[7] << 24);
+    st_nt(reinterpret_cast<u32x2*>(static_cast<uint8_t*>(codes) + i), w);
+  } else if constexpr (CB == 2) {
+    u32x4 w;
+    w.x = (c[0] & 0xFFFF) | (c[1] << 16);
+    w.y = (c[2] & 0xFFFF) | (c[3] << 16);
+    w.z = (c[4] & 0xFFFF) | (c[5] << 16);
+    w.w = (c[6] & 0xFFFF) | (c[7] << 16);
+    st_nt(reinterpret_cast<u32x4*>(static_cast<uint16_t*>(codes) + i), w);
+  }
+}
+
+template <int CB>
+__device__ __forceinline__ void store_code1(void* codes, int64_t i, uint32_t c) {
+  if constexpr (CB == 1) static_cast<uint8_t*>(codes)[i] = (uint8_t)c;
+  if constexpr (CB == 2) static_cast<uint16_t*>(codes)[i] = (uint16_t)c;
+}
+
+// Per-tensor (C == 1) fake-quant, 8 elements per thread per step, 16-byte
+// streaming loads/stores.  x, y 16-byte aligned; codes 8 (CB=1) or 16 (CB=2)
+// byte aligned; the < 8-element tail is done one element per thread.
+template <typename T, typename Enc, int CB>
+__global__ __launch_bounds__(256) void fq_vec_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                     void* __restrict__ codes, int64_t n,
+                                                     const float* __restrict__ scale, bool mul, Enc enc) {
+  float s = scale ? scale[0] : 1.0f;
+  s = to_dtype<T>(s);
+  bool unit = s == 1.0f;
+  const int64_t nvec = n / 8;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < nvec; g += stride) {
+    float v[8];
+    uint32_t c[8];
+    IO<T>::load(x + g * 8, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = fq_one<T>(v[j], s, unit, mul, enc, c[j]);
+    if (y) IO<T>::store(y + g * 8, v);
+    if constexpr (CB > 0) store_codes8<CB>(codes, g * 8, c);
+  }
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t i = nvec * 8 + t;
+  if (i < n) {
+    uint32_t c;
+    float v = fq_one<T>(IO<T>::get(x + i), s, unit, mul, enc, c);
+    if (y) IO<T>::put(y + i, v);
+    if constexpr (CB > 0) store_code1<CB>(codes, i, c);
+  }
+}
+
+// General path: any alignment, per-channel scales (channel of element i is
+// (i / inner) % C).
+template <typename T, typename Enc, int CB>
+__global__ __launch_bounds__(256) void fq_scalar_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                        void* __restrict__ codes, int64_t n,
+                                                        const float* __restrict__ scale,
+                                                        int64_t inner, int64_t C, bool mul, Enc enc) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float s = 1.0f;
+    if (scale) s = scale[C > 1 ? (i / inner) % C : 0];
+    s = to_dtype<T>(s);
+    uint32_t c;
+    float v = fq_one<T>(IO<T>::get(x + i), s, s == 1.0f, mul, enc, c);
+    if (y) IO<T>::put(y + i, v);
+    if constexpr (CB > 0) store_code1<CB>(codes, i, c);
+  }
+}
+
+template <typename T, typename Enc>
+static int launch_fq(const T* x, T* y, void* codes, int code_bytes, int64_t n, const float* scale,
+                     int64_t inner, int64_t C, bool mul, const Enc& enc, hipStream_t st) {
+  if (n == 0) return kOk;
+  const int bs = 256;
+  bool vec = C <= 1 && aligned(x, 16) && (!y || aligned(y, 16)) &&
+             (code_bytes == 0 || aligned(codes, code_bytes == 1 ? 8 : 16));
+  if (vec) {
+    unsigned grid = grid_for(n / 8 + 1, bs);
+    if (code_bytes == 0)
+      hipLaunchKernelGGL((fq_vec_kernel<T, Enc, 0>), dim3(grid), dim3(bs), 0, st, x, y, codes, n, scale, mul, enc);
+    else if (code_bytes == 1)
+      hipLaunchKernelGGL((fq_vec_kernel<T, Enc, 1>), dim3(grid), dim3(bs), 0, st, x, y, codes, n, scale, mul, enc);
+    else
+      hipLaunchKernelGGL((fq_vec_kernel<T, Enc, 2>), dim3(grid), dim3(bs), 0, st, x, y, codes, n, scale, mul, enc);
+  } else {
+    unsigned grid = grid_for(n, bs);
+    if (code_bytes == 0)
+      hipLaunchKernelGGL((fq_scalar_kernel<T, Enc, 0>), dim3(grid), dim3(bs), 0, st, x, y, codes, n, scale, inner, C, mul, enc);
+    else if (code_bytes == 1)
+      hipLaunchKernelGGL((fq_scalar_kernel<T, Enc, 1>), dim3(grid), dim3(bs), 0, st, x, y, codes, n, scale, inner, C, mul, enc);
+    else
+      hipLaunchKernelGGL((fq_scalar_kernel<T, Enc, 2>), dim3(grid), dim3(bs), 0, st, x, y, codes, n, scale, inner, C, mul, enc);
+  }
+  return check_launch("fake_quant");
+}
+
+template <typename Enc>
+static int launch_fq_dtype(const void* x, int dtype, void* y, void* codes, int code_bytes, int64_t n,
+                           const float* scale, int64_t inner, int64_t C, bool mul, const Enc& enc,
+                           hipStream_t st) {
+  switch (dtype) {
+    case kF32:
+      return launch_fq((const float*)x, (float*)y, codes, code_bytes, n, scale, inner, C, mul, enc, st);
+    case kBF16:
+      return launch_fq((const uint16_t*)x, (uint16_t*)y, codes, code_bytes, n, scale, inner, C, mul, enc, st);
+    case kF16:
+      return launch_fq((const __half*)x, (__half*)y, codes, code_bytes, n, scale, inner, C, mul, enc, st);
+    default:
+      return set_error(kErrInvalid, "input dtype %d not supported (float32, bfloat16, float16)", dtype);
+  }
+}
+
+int fake_quant(const void* x, int dtype, int64_t n, const FormatDesc& fmt, const float* scale,
+               int64_t scale_numel, int64_t scale_inner, bool mul, void* y, void* codes, int code_bytes,
+               hipStream_t st) {
+  if (n < 0) return set_error(kErrInvalid, "negative element count");
+  if (code_bytes != 0 && code_bytes != 1 && code_bytes != 2)
+    return set_error(kErrInvalid, "code width must be 1 or 2 bytes");
+  if (scale_numel > 1 && scale_inner < 1) return set_error(kErrInvalid, "scale_inner must be >= 1");
+  return with_encoder(fmt, [&](auto enc) {
+    return launch_fq_dtype(x, dtype, y, codes, code_bytes, n, scale, scale_inner, scale_numel, mul, enc, st);
+  });
+}
+
+int lut_gather(const void* x, int dtype, int64_t n, const uint16_t* table, void* y, hipStream_t st) {
+  if (n < 0) return set_error(kErrInvalid, "negative element count");
+  if (!table) return set_error(kErrInvalid, "table is null");
+  return launch_fq_dtype(x, dtype, y, nullptr, 0, n, nullptr, 1, 1, false, EncTable{table}, st);
+}
+
+// ---------------------------------------------------------------------------
+// quantize / dequantize with any scale layout (vqx_scale_map)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t scale_index(int64_t i, const ScaleMap& m) {
+  int64_t in = i % m.inner;
+  int64_t r = i / m.inner;
+  int64_t l = r % m.L;
+  int64_t o = r / m.L;
+  return o * m.s_o + (l / m.block) * m.s_l + in * m.s_in;
+}
+
+template <typename T, typename Enc, int CB>
+__global__ __launch_bounds__(256) void quant_mapped_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                           void* __restrict__ codes, int64_t n,
+                                                           ScaleMap m, bool mul, Enc enc) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    int64_t si = scale_index(i, m);
+    float s = IO<T>::get(static_cast<const T*>(m.scale) + si);
+    float xv = IO<T>::get(x + i);
+    float t = to_dtype<T>(xv / s);
+    if (m.zero_point) t = to_dtype<T>(t + IO<T>::get(static_cast<const T*>(m.zero_point) + si));
+    Result r = enc.encode(f2bf(t));
+    float v = to_dtype<T>(bf2f(r.value));
+    if (mul) {
+      if (m.zero_point) v = to_dtype<T>(v - IO<T>::get(static_cast<const T*>(m.zero_point) + si));
+      v = to_dtype<T>(v * s);
+    }
+    if (y) IO<T>::put(y + i, v);
+    if constexpr (CB > 0) store_code1<CB>(codes, i, r.code);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_mapped_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                             int64_t n, const uint16_t* __restrict__ in_map,
+                                                             ScaleMap m, const uint16_t* __restrict__ out_map) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float v = IO<T>::get(x + i);
+    if (in_map) v = to_dtype<T>(bf2f(in_map[f2bf(v)]));
+    if (m.scale) {
+      int64_t si = scale_index(i, m);
+      if (m.zero_point) v = to_dtype<T>(v - IO<T>::get(static_cast<const T*>(m.zero_point) + si));
+      v = to_dtype<T>(v * IO<T>::get(static_cast<const T*>(m.scale) + si));
+    }
+    if (out_map) v = to_dtype<T>(bf2f(out_map[f2bf(v)]));
+    IO<T>::put(y + i, v);
+  }
+}
+
+template <typename T, typename Enc>
+static int launch_qmapped(const T* x, T* y, void* codes, int code_bytes, int64_t n, const ScaleMap& m,
+                          bool mul, const Enc& enc, hipStream_t st) {
+  unsigned grid = grid_for(n, 256);
+  if (code_bytes == 0)
+    hipLaunchKernelGGL((quant_mapped_kernel<T, Enc, 0>), dim3(grid), dim3(256), 0, st, x, y, codes, n, m, mul, enc);
+  else if (code_bytes == 1)
+    hipLaunchKernelGGL((quant_mapped_kernel<T, Enc, 1>), dim3(grid), dim3(256), 0, st, x, y, codes, n, m, mul, enc);
+  else
+    hipLaunchKernelGGL((quant_mapped_kernel<T, Enc, 2>), dim3(grid), dim3(256), 0, st, x, y, codes, n, m, mul, enc);
+  return check_launch("quantize_mapped");
+}
+
+static int check_map(const ScaleMap& m) {
+  if (m.L < 1 || m.inner < 1 || m.block < 1)
+    return set_error(kErrInvalid, "scale map: L, inner, block must be >= 1");
+  if (m.s_o < 0 || m.s_l < 0 || m.s_in < 0) return set_error(kErrInvalid, "scale map: negative stride");
+  return kOk;
+}
+
+int quantize_mapped(const void* x, int dtype, int64_t n, const FormatDesc& fmt, const ScaleMap& m,
+                    bool mul, void* y, void* codes, int code_bytes, hipStream_t st) {
+  if (n < 0) return set_error(kErrInvalid, "negative element count");
+  if (n == 0) return kOk;
+  if (!m.scale) return set_error(kErrInvalid, "quantize: scale is required");
+  int rc = check_map(m);
+  if (rc != kOk) return rc;
+  if (!codes) code_bytes = 0;
+  if (code_bytes < 0 || code_bytes > 2) return set_error(kErrInvalid, "code width must be 1 or 2 bytes");
+  return with_encoder(fmt, [&](auto enc) -> int {
+    using E = decltype(enc);
+    switch (dtype) {
+      case kF32: return launch_qmapped<float, E>((const float*)x, (float*)y, codes, code_bytes, n, m, mul, enc, st);
+      case kBF16: return launch_qmapped<uint16_t, E>((const uint16_t*)x, (uint16_t*)y, codes, code_bytes, n, m, mul, enc, st);
+      case kF16: return launch_qmapped<__half, E>((const __half*)x, (__half*)y, codes, code_bytes, n, m, mul, enc, st);
+      default: return set_error(kErrInvalid, "input dtype %d not supported", dtype);
+    }
+  });
+}
+
+int dequantize_mapped(const void* x, int dtype, int64_t n, const uint16_t* in_map, const ScaleMap& m,
+                      const uint16_t* out_map, void* y, hipStream_t st) {
+  if (n < 0) return set_error(kErrInvalid, "negative element count");
+  if (n == 0) return kOk;
+  if (m.scale) {
+    int rc = check_map(m);
+    if (rc != kOk) return rc;
+  }
+  unsigned grid = grid_for(n, 256);
+  switch (dtype) {
+    case kF32:
+      hipLaunchKernelGGL((dequant_mapped_kernel<float>), dim3(grid), dim3(256), 0, st, (const float*)x, (float*)y, n, in_map, m, out_map);
+      break;
+    case kBF16:
+      hipLaunchKernelGGL((dequant_mapped_kernel<uint16_t>), dim3(grid), dim3(256), 0, st, (const uint16_t*)x, (uint16_t*)y, n, in_map, m, out_map);
+      break;
+    case kF16:
+      hipLaunchKernelGGL((dequant_mapped_kernel<__half>), dim3(grid), dim3(256), 0, st, (const __half*)x, (__half*)y, n, in_map, m, out_map);
+      break;
+    default:
+      return set_error(kErrInvalid, "input dtype %d not supported", dtype);
+  }
+  return check_launch("dequantize_mapped");
+}
+
+// ---------------------------------------------------------------------------
+// setup: tabulate a format over every bf16 pattern
+// ---------------------------------------------------------------------------
+template <typename Enc>
+__global__ __launch_bounds__(256) void build_table_kernel(uint16_t* values, uint16_t* codes, Enc enc) {
+  uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= 65536u) return;
+  Result r = enc.encode(h);
+  if (values) values[h] = (uint16_t)r.value;
+  if (codes) codes[h] = (uint16_t)r.code;
+}
+
+int build_table(const FormatDesc& fmt, uint16_t* values, uint16_t* codes, hipStream_t st) {
+  return with_encoder(fmt, [&](auto enc) {
+    hipLaunchKernelGGL((build_table_kernel<decltype(enc)>), dim3(256), dim3(256), 0, st, values, codes, enc);
+    return check_launch("build_table");
+  });
+}
+
+// Index table of a level set for every bf16 pattern:
+//  mode 0 (NormalFloat, normal_float.py:58-60): levels are bf16, the input is
+//    clamped to [min, max], and |level - x| is rounded to bf16 before argmin;
+//  mode 1 (codebook, lcq.py:286-291): levels fp32, clamp and |x - level| fp32.
+// argmin takes the first index of the minimum; NaN inputs give index 0.
+__global__ __launch_bounds__(256) void level_index_kernel(const float* levels, int K, int mode,
+                                                          uint8_t* out) {
+  uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= 65536u) return;
+  float x = bf2f(h);
+  if (x != x) {
+    out[h] = 0;
+    return;
+  }
+  float lo = levels[0], hi = levels[0];
+  for (int k = 1; k < K; ++k) {
+    lo = fminf(lo, levels[k]);
+    hi = fmaxf(hi, levels[k]);
+  }
+  float xc = x < lo ? lo : x;
+  xc = xc > hi ? hi : xc;
+  int best = 0;
+  float bd = 0.0f;
+  for (int k = 0; k < K; ++k) {
+    float d = mode == 0 ? levels[k] - xc : xc - levels[k];
+    if (mode == 0) d = bf2f(f2bf(d));
+    d = fabsf(d);
+    if (k == 0 || d < bd) {
+      bd = d;
+      best = k;
+    }
+  }
+  out[h] = (uint8_t)best;
+}
+
+// Order-preserving key of a float: unsigned comparison of keys = float order.
+__device__ __forceinline__ uint32_t order_key(uint32_t bits) {
+  return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+}
+__device__ __forceinline__ uint32_t key_bits(uint32_t key) {
+  return (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key;
+}
+
+// first[c] = least (order key of a) bf16 value whose index is c.
+__global__ __launch_bounds__(256) void level_first_kernel(const uint8_t* idx, uint32_t* first) {
+  uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= 65536u) return;
+  if ((h & 0x7FFFu) > 0x7F80u) return;  // NaN
+  atomicMin(&first[idx[h]], order_key(h << 16));
+}
+
+// boundaries[j-1] = min_{c >= j} first[c]  (suffix minimum), as fp32 values.
+__global__ void level_boundary_kernel(const uint32_t* first, int K, float* boundaries) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  uint32_t m = 0xFFFFFFFFu;
+  for (int j = K - 1; j >= 1; --j) {
+    m = first[j] < m ? first[j] : m;
+    // a code no bf16 value reaches gets a NaN boundary: v >= NaN never holds
+    boundaries[j - 1] = m == 0xFFFFFFFFu ? __builtin_nanf("") : u2f(key_bits(m));
+  }
+}
+
+// Check that counting boundaries reproduces the index table everywhere.
+__global__ __launch_bounds__(256) void level_verify_kernel(const uint8_t* idx, const float* boundaries,
+                                                           int K, int* bad) {
+  uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= 65536u) return;
+  uint32_t c = count_le(boundaries, K - 1, bf2f(h));
+  if (c != idx[h]) atomicAdd(bad, 1);
+}
+
+int level_tables(const float* levels, int K, int mode, uint8_t* index_table, float* boundaries,
+                 uint32_t* work, int* bad, hipStream_t st) {
+  if (K < 1 || K > 256) return set_error(kErrInvalid, "level count %d outside [1,256]", K);
+  hipLaunchKernelGGL(level_index_kernel, dim3(256), dim3(256), 0, st, levels, K, mode, index_table);
+  if (K == 1) return check_launch("level_tables");
+  if (hipMemsetAsync(work, 0xFF, sizeof(uint32_t) * K, st) != hipSuccess ||
+      hipMemsetAsync(bad, 0, sizeof(int), st) != hipSuccess)
+    return set_error(kErrLaunch, "hipMemsetAsync failed");
+  hipLaunchKernelGGL(level_first_kernel, dim3(256), dim3(256), 0, st, index_table, work);
+  hipLaunchKernelGGL(level_boundary_kernel, dim3(1), dim3(64), 0, st, work, K, boundaries);
+  hipLaunchKernelGGL(level_verify_kernel, dim3(256), dim3(256), 0, st, index_table, boundaries, K, bad);
+  return check_launch("level_tables");
+}
+
+}  // namespace vqx

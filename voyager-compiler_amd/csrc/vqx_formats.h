@@ -136,6 +136,7 @@ enum FormatKind : int32_t {
   kFmtNvFp8 = 4,     // e4m3 / e5m2: fp32-bit RNE (fp8.py:13-74)
   kFmtPosit = 5,     // posit<n>_<es> (posit.py:8-73)
   kFmtLevels = 6,    // nf<k>[_<b>] or a sorted codebook: boundary search
+  kFmtTable = 7,     // any 65536-entry bf16 table (a caller's qmap)
 };
 
 enum FormatFlags : int32_t {

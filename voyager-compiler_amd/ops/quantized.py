@@ -1,0 +1,612 @@
+"""The ``quantized_ops`` torch library on MI355X kernels.
+
+Same qualified names and schema strings as the reference library
+(src/voyager_compiler/ops/quantized.py:12, :98, :124-128, :175-179, :286-292,
+:363-368, :435-439, :502-506), so converted graphs and FakeQuantize modules
+call into these kernels unchanged.  Every op has a kernel for the CUDA
+dispatch key only (HIP tensors on ROCm dispatch there) plus a fake
+implementation for tracing; CPU tensors raise, there is no CPU path.
+
+Ops beyond the reference's (packed storage is this build's own):
+``fake_quant``, ``quantize_mx_packed``, ``dequantize_mx_packed``,
+``codebook_encode``, ``codebook_decode``, ``linear_nf4``.
+"""
+
+import math
+import weakref
+from typing import List, Optional, Tuple
+
+import torch
+from torch.library import Library
+
+from .. import _lib
+from ..formats import Format, parse_format
+
+quantized_ops_lib = Library("quantized_ops", "DEF")
+
+_SCHEMAS = {
+    "vmap": "vmap(Tensor self, Tensor other) -> Tensor",
+    "quantize": (
+        "quantize(Tensor input, Tensor scale, Tensor? zero_point=None, "
+        "SymInt[]? axes=None, int? block_size=None, Tensor? qmap=None, "
+        "Tensor? output_code=None) -> Tensor"),
+    "dequantize": (
+        "dequantize(Tensor input, Tensor scale, Tensor? zero_point=None, "
+        "SymInt[]? axes=None, int? block_size=None, Tensor? input_qmap=None, "
+        "Tensor? output_qmap=None) -> Tensor"),
+    "linear_mx": (
+        "linear_mx(Tensor input, Tensor weight, Tensor? bias=None, *, "
+        "Tensor? input_scale=None, Tensor? weight_scale=None, "
+        "int? block_size=None, Tensor? input_code=None, Tensor? weight_code=None, "
+        "Tensor? A_data=None, Tensor? A_indices=None, Tensor? A_indptr=None, "
+        'str weight_layout="kc") -> Tensor'),
+    "matmul_mx": (
+        "matmul_mx(Tensor self, Tensor other, *, Tensor? input_scale=None, "
+        "Tensor? weight_scale=None, int? block_size=None, Tensor? input_code=None, "
+        "Tensor? weight_code=None, Tensor? A_data=None, Tensor? A_indices=None, "
+        'Tensor? A_indptr=None, str weight_layout="ck") -> Tensor'),
+    "calculate_mx_qparam": (
+        "calculate_mx_qparam(Tensor self, SymInt[] axes, int block_size, "
+        "float quant_max, bool force_scale_power_of_two=False, "
+        "Tensor scale_qmap=None) -> Tensor"),
+    "quantize_mx": (
+        "quantize_mx(Tensor self, Tensor qmap, SymInt[] axes, int block_size, "
+        "float quant_max, bool force_scale_power_of_two=False, "
+        "Tensor scale_qmap=None, Tensor output_code=None) -> (Tensor, Tensor)"),
+    # this build's own
+    "fake_quant": (
+        "fake_quant(Tensor self, str dtype, Tensor? scale=None, bool mul_back=True, "
+        "bool return_codes=False) -> (Tensor, Tensor)"),
+    "quantize_mx_packed": (
+        "quantize_mx_packed(Tensor self, str dtype, int axis, int block_size, "
+        "bool force_scale_power_of_two=True, float? quant_max=None, "
+        'str scale_dtype="e8m0") -> (Tensor, Tensor)'),
+    "dequantize_mx_packed": (
+        "dequantize_mx_packed(Tensor codes, Tensor scale, str dtype, int block_size, "
+        "SymInt[] shape, ScalarType out_dtype=bfloat16) -> Tensor"),
+    "codebook_encode": "codebook_encode(Tensor self, Tensor codebook) -> Tensor",
+    "codebook_decode": (
+        "codebook_decode(Tensor codes, Tensor codebook, ScalarType dtype=float) -> Tensor"),
+}
+for _s in _SCHEMAS.values():
+    quantized_ops_lib.define(_s)
+
+
+def _impl(name):
+    return torch.library.impl(quantized_ops_lib, name, "CUDA")
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+_TABLE_FMT = {}  # data_ptr -> (weakref to table tensor, version, Format)
+
+
+def register_table(t: torch.Tensor, fmt: Format):
+    """Remember that table ``t`` is ``fmt``'s, so ops given ``t`` as a qmap
+    can run the closed-form encoder instead of the table gather."""
+    _TABLE_FMT[t.data_ptr()] = (weakref.ref(t), t._version, fmt)
+
+
+def _format_of_table(qmap: torch.Tensor) -> Optional[Format]:
+    ent = _TABLE_FMT.get(qmap.data_ptr())
+    if ent is None:
+        return None
+    ref, ver, fmt = ent
+    if ref() is not qmap or qmap._version != ver:
+        return None
+    return fmt
+
+
+_BF16_TABLES = {}
+
+
+def _table_bf16(qmap: torch.Tensor) -> torch.Tensor:
+    """A 65536-entry qmap as a contiguous bf16 table on its device."""
+    if qmap.numel() != 65536:
+        raise ValueError(f"qmap must have 65536 entries (one per bf16 pattern), got {qmap.numel()}")
+    if qmap.dtype == torch.bfloat16 and qmap.is_contiguous():
+        return qmap
+    key = (qmap.data_ptr(), qmap._version, qmap.dtype)
+    hit = _BF16_TABLES.get(key)
+    if hit is not None and hit[0]() is qmap:
+        return hit[1]
+    t = qmap.reshape(-1).to(torch.bfloat16).contiguous()
+    _BF16_TABLES[key] = (weakref.ref(qmap), t)
+    return t
+
+
+def _table_desc(qmap: torch.Tensor, device) -> Tuple[object, object]:
+    """(vqx_format, keep-alive) for a qmap: closed form when it is a known
+    format's table, else the table itself."""
+    fmt = _format_of_table(qmap)
+    if fmt is not None:
+        return fmt.desc(device), None
+    t = _table_bf16(qmap)
+    d = _lib.VqxFormat()
+    d.kind = _lib.FMT_TABLE
+    d.code_bits = 16
+    d.value_table = t.data_ptr()
+    return d, t
+
+
+def _axis_geometry(shape, axis):
+    nd = len(shape)
+    axis = axis + nd if axis < 0 else axis
+    if not 0 <= axis < nd:
+        raise ValueError(f"axis {axis} out of range for {nd}-d tensor")
+    outer = math.prod(shape[:axis])
+    inner = math.prod(shape[axis + 1:])
+    return axis, outer, shape[axis], inner
+
+
+def _single_axis(axes):
+    if axes is None:
+        raise ValueError("axes required")
+    axes = [axes] if isinstance(axes, int) else list(axes)
+    if len(axes) != 1:
+        raise NotImplementedError(
+            f"vqx: blocks along {len(axes)} axes are not implemented (one axis only)")
+    return int(axes[0])
+
+
+def _scale_map(x: torch.Tensor, scale: torch.Tensor, zp: Optional[torch.Tensor], block_size):
+    """vqx_scale_map for a scale broadcast (block_size None) or expanded by
+    ``expand`` (quantized.py:82-95) against x; None if the layout needs the
+    general broadcast path."""
+    nd = x.dim()
+    s = scale
+    while s.dim() < nd:
+        s = s.unsqueeze(0)
+    if s.dim() != nd:
+        return None
+    differ = [d for d in range(nd) if s.shape[d] != x.shape[d]]
+    m = _lib.VqxScaleMap()
+    m.scale = scale.data_ptr()
+    m.zero_point = zp.data_ptr() if zp is not None else None
+    if block_size is None:
+        live = [d for d in range(nd) if s.shape[d] != 1]
+        if any(s.shape[d] != x.shape[d] for d in live):
+            return None
+        if not live:
+            m.L, m.inner, m.block, m.s_o, m.s_l, m.s_in = 1, 1, 1, 0, 0, 0
+            return m
+        if live != list(range(live[0], live[-1] + 1)):
+            return None
+        d0, d1 = live[0], live[-1]
+        m.L = math.prod(x.shape[d0:d1 + 1])
+        m.inner = math.prod(x.shape[d1 + 1:])
+        m.block, m.s_o, m.s_l, m.s_in = 1, 0, 1, 0
+        return m
+    if len(differ) != 1:
+        return None
+    d = differ[0]
+    L = x.shape[d]
+    nblk = s.shape[d]
+    if nblk != -(-L // block_size):
+        return None
+    m.L = L
+    m.inner = math.prod(x.shape[d + 1:])
+    m.block = block_size
+    m.s_o, m.s_l, m.s_in = nblk * m.inner, m.inner, 1
+    return m
+
+
+def _expand(input, shape, block_size):
+    """The reference's scale broadcast (quantized.py:82-95), for the rare
+    layouts the scale map cannot describe."""
+    while input.ndim < len(shape):
+        input = input.unsqueeze(0)
+    for dim in range(len(shape)):
+        if input.shape[dim] != shape[dim]:
+            input = torch.repeat_interleave(input, block_size, dim)
+    if list(input.shape) != list(shape):
+        input = input[[slice(0, x) for x in shape]]
+    return input
+
+
+# ---------------------------------------------------------------------------
+# vmap  (quantized.py:98-121)
+# ---------------------------------------------------------------------------
+@_impl("vmap")
+def vmap(input: torch.Tensor, qmap: torch.Tensor) -> torch.Tensor:
+    _lib.require_device(input, "vmap")
+    table = _table_bf16(qmap.to(input.device))
+    dt = input.dtype
+    x = input if dt in (torch.float32, torch.bfloat16, torch.float16) else input.to(torch.bfloat16)
+    x = x.contiguous()
+    y = torch.empty_like(x, memory_format=torch.contiguous_format)
+    _lib.call("vqx_vmap", _lib.ptr(x), _lib.dtype_tag(x.dtype), x.numel(), _lib.ptr(table),
+              _lib.ptr(y), _lib.stream_of(x))
+    return y if y.dtype == dt else y.to(dt)
+
+
+# ---------------------------------------------------------------------------
+# quantize / dequantize  (quantized.py:124-227)
+# ---------------------------------------------------------------------------
+def _compute_dtype(*ts):
+    dt = ts[0].dtype
+    for t in ts[1:]:
+        if t is not None:
+            dt = torch.promote_types(dt, t.dtype)
+    return dt
+
+
+@_impl("quantize")
+def quantize(input, scale, zero_point=None, axes=None, block_size=None, qmap=None, output_code=None):
+    assert qmap is not None, "qmap must be provided for quantization"
+    _lib.require_device(input, "quantize")
+    cdt = _compute_dtype(input, scale, zero_point)
+    if cdt not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError(f"vqx: quantize computes in float32/bfloat16/float16, not {cdt}")
+    x = input.to(cdt).contiguous()
+    s = scale.to(device=x.device, dtype=cdt).contiguous()
+    zp = zero_point.to(device=x.device, dtype=cdt).contiguous() if zero_point is not None else None
+    m = _scale_map(x, s, zp, block_size)
+    if m is None or (zp is not None and zp.shape != s.shape):
+        # layouts outside the scale map: broadcast with torch, then one map
+        s = (_expand(s, x.shape, block_size) if block_size is not None else s.expand(x.shape)).contiguous()
+        zp = None if zp is None else (
+            _expand(zp, x.shape, block_size) if block_size is not None else zp.expand(x.shape)).contiguous()
+        m = _lib.VqxScaleMap(s.data_ptr(), zp.data_ptr() if zp is not None else None,
+                             x.numel(), 1, 1, 0, 1, 0)
+    desc, keep = _table_desc(qmap.to(x.device), x.device)
+    y = torch.empty_like(x)
+    _lib.call("vqx_quantize_mapped", _lib.ptr(x), _lib.dtype_tag(cdt), x.numel(), _lib.ctypes.byref(desc),
+              _lib.ctypes.byref(m), 0, _lib.ptr(y), None, 0, _lib.stream_of(x))
+    del keep
+    return y
+
+
+@_impl("dequantize")
+def dequantize(input, scale, zero_point=None, axes=None, block_size=None, input_qmap=None,
+               output_qmap=None):
+    _lib.require_device(input, "dequantize")
+    cdt = _compute_dtype(input, scale, zero_point)
+    if cdt not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError(f"vqx: dequantize computes in float32/bfloat16/float16, not {cdt}")
+    if input_qmap is not None and input.dtype != cdt:
+        input = vmap(input, input_qmap)
+        input_qmap = None
+    x = input.to(cdt).contiguous()
+    s = scale.to(device=x.device, dtype=cdt).contiguous()
+    zp = zero_point.to(device=x.device, dtype=cdt).contiguous() if zero_point is not None else None
+    m = _scale_map(x, s, zp, block_size)
+    if m is None or (zp is not None and zp.shape != s.shape):
+        s = (_expand(s, x.shape, block_size) if block_size is not None else s.expand(x.shape)).contiguous()
+        zp = None if zp is None else (
+            _expand(zp, x.shape, block_size) if block_size is not None else zp.expand(x.shape)).contiguous()
+        m = _lib.VqxScaleMap(s.data_ptr(), zp.data_ptr() if zp is not None else None,
+                             x.numel(), 1, 1, 0, 1, 0)
+    inm = _table_bf16(input_qmap.to(x.device)) if input_qmap is not None else None
+    outm = _table_bf16(output_qmap.to(x.device)) if output_qmap is not None else None
+    y = torch.empty_like(x)
+    _lib.call("vqx_dequantize_mapped", _lib.ptr(x), _lib.dtype_tag(cdt), x.numel(), _lib.ptr(inm),
+              _lib.ctypes.byref(m), _lib.ptr(outm), _lib.ptr(y), _lib.stream_of(x))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# calculate_mx_qparam / quantize_mx  (quantized.py:435-529)
+# ---------------------------------------------------------------------------
+_IDENTITY = None
+
+
+def _identity_desc(device):
+    global _IDENTITY
+    if _IDENTITY is None:
+        _IDENTITY = parse_format("bfloat16")
+    return _IDENTITY.desc(device)
+
+
+def _mx_call(x, axis, block_size, quant_max, force_pow2, scale_qmap, desc, want_scale=True,
+             want_qvals=False, want_fq=False, scale_f32=None, e8m0=None, codes=None, code_layout=1):
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"vqx: block scales are computed for bfloat16/float32 inputs, not {x.dtype}")
+    if block_size <= 0:
+        raise AssertionError("block_size must be positive")
+    x = x.contiguous()
+    axis, outer, L, inner = _axis_geometry(list(x.shape), axis)
+    sshape = list(x.shape)
+    sshape[axis] = -(-L // block_size)
+    scale = torch.empty(sshape, dtype=x.dtype, device=x.device) if want_scale else None
+    qv = torch.empty_like(x) if want_qvals else None
+    fq = torch.empty_like(x) if want_fq else None
+    sq = _table_bf16(scale_qmap.to(x.device)) if (scale_qmap is not None and not force_pow2) else None
+    shift = math.floor(math.log2(quant_max)) if force_pow2 else 0
+    _lib.call("vqx_mx_quantize", _lib.ptr(x), _lib.dtype_tag(x.dtype), outer, L, inner, block_size,
+              _lib.ctypes.byref(desc), 0 if force_pow2 else 1, shift, float(quant_max), _lib.ptr(sq),
+              _lib.ptr(scale), _lib.ptr(scale_f32), _lib.ptr(e8m0), _lib.ptr(qv), _lib.ptr(fq),
+              _lib.ptr(codes), code_layout, _lib.stream_of(x))
+    return scale, qv, fq
+
+
+@_impl("calculate_mx_qparam")
+def calculate_mx_qparam(input, axes, block_size, quant_max, force_scale_power_of_two=False,
+                        scale_qmap=None):
+    _lib.require_device(input, "calculate_mx_qparam")
+    axis = _single_axis(axes)
+    scale, _, _ = _mx_call(input, axis, block_size, quant_max, force_scale_power_of_two, scale_qmap,
+                           _identity_desc(input.device))
+    return scale
+
+
+@_impl("quantize_mx")
+def quantize_mx(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False,
+                scale_qmap=None, output_code=None):
+    _lib.require_device(input, "quantize_mx")
+    axis = _single_axis(axes)
+    desc, keep = _table_desc(qmap.to(input.device), input.device)
+    scale, qv, _ = _mx_call(input, axis, block_size, quant_max, force_scale_power_of_two, scale_qmap,
+                            desc, want_qvals=True)
+    del keep
+    return scale, qv
+
+
+def mx_fake_quantize(input, fmt: Format, axis, block_size, quant_max, force_pow2, scale_qmap=None):
+    """MXFakeQuantizeFunction.forward's numerics (fake_quantize.py:143-153):
+    (scale, quantize_mx values * expand(scale)) in one pass."""
+    scale, _, fq = _mx_call(input, axis, block_size, quant_max, force_pow2, scale_qmap,
+                            fmt.desc(input.device), want_fq=True)
+    return scale, fq
+
+
+# ---------------------------------------------------------------------------
+# linear_mx / matmul_mx  (quantized.py:286-432): decode on the GPU, then the
+# dense product (hipBLASLt).  The fused NF4 product is linear_nf4.
+# ---------------------------------------------------------------------------
+_CODE_LUTS = {}
+
+
+def _code_lut(code: torch.Tensor) -> torch.Tensor:
+    """65536-entry table sending the bf16 pattern of k to code[k] (the
+    reference indexes ``code[x.long()]`` with integer-valued x)."""
+    key = (code.data_ptr(), code._version, code.numel(), code.dtype)
+    hit = _CODE_LUTS.get(key)
+    if hit is not None and hit[0]() is code:
+        return hit[1]
+    K = code.numel()
+    if K > 256:
+        raise ValueError("code tables hold at most 256 entries")
+    lut = torch.zeros(65536, dtype=torch.bfloat16, device=code.device)
+    ks = torch.arange(K, device=code.device, dtype=torch.float32).to(torch.bfloat16)
+    idx = ks.view(torch.int16).to(torch.int64) & 0xFFFF
+    lut[idx] = code.reshape(-1).to(torch.bfloat16)
+    _CODE_LUTS[key] = (weakref.ref(code), lut)
+    return lut
+
+
+def _decode_operand(t, code, scale, block_size):
+    if code is None and scale is None:
+        return t
+    if code is not None:
+        lut = _code_lut(code.to(t.device))
+    else:
+        lut = None
+    if scale is None:
+        return vmap(t, lut)
+    return dequantize(t, scale, None, None, block_size, lut, None)
+
+
+def _no_outliers(A_data):
+    if A_data is not None:
+        raise NotImplementedError("vqx: the CSR outlier path (A_data/A_indices/A_indptr) is not implemented")
+
+
+@_impl("linear_mx")
+def linear_mx(input, weight, bias=None, *, input_scale=None, weight_scale=None, block_size=None,
+              input_code=None, weight_code=None, A_data=None, A_indices=None, A_indptr=None,
+              weight_layout="kc"):
+    assert weight_layout in ("kc", "ck"), weight_layout
+    _lib.require_device(input, "linear_mx")
+    _no_outliers(A_data)
+    if weight_layout != "kc":
+        raise NotImplementedError("vqx: the 'ck' hardware weight layout is not implemented")
+    x = _decode_operand(input, input_code, input_scale, block_size)
+    w = _decode_operand(weight, weight_code, weight_scale, block_size)
+    if weight_code is not None:
+        w = w.to(weight.dtype)
+    return torch.nn.functional.linear(x, w, bias)
+
+
+@_impl("matmul_mx")
+def matmul_mx(self, other, *, input_scale=None, weight_scale=None, block_size=None, input_code=None,
+              weight_code=None, A_data=None, A_indices=None, A_indptr=None, weight_layout="ck"):
+    assert weight_layout in ("kc", "ck"), weight_layout
+    _lib.require_device(self, "matmul_mx")
+    _no_outliers(A_data)
+    if weight_layout != "ck":
+        raise NotImplementedError("vqx: the 'kc' hardware layout for matmul is not implemented")
+    a = _decode_operand(self, input_code, input_scale, block_size)
+    b = _decode_operand(other, weight_code, weight_scale, block_size)
+    return torch.matmul(a, b.contiguous())
+
+
+# ---------------------------------------------------------------------------
+# this build's own ops
+# ---------------------------------------------------------------------------
+@_impl("fake_quant")
+def fake_quant(input, dtype, scale=None, mul_back=True, return_codes=False):
+    """Closed-form FakeQuantizeFunction (fake_quantize.py:101-115) with an
+    optional per-tensor or per-channel fp32 scale and optional codes."""
+    _lib.require_device(input, "fake_quant")
+    fmt = parse_format(dtype)
+    x = input.contiguous()
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError(f"vqx: fake_quant input must be float32/bfloat16/float16, not {x.dtype}")
+    y = torch.empty_like(x)
+    cb = 1 if fmt.code_bits <= 8 else 2
+    codes = (torch.empty(x.shape, dtype=torch.uint8 if cb == 1 else torch.int16, device=x.device)
+             if return_codes else torch.empty(0, dtype=torch.uint8, device=x.device))
+    s, sn, si = None, 1, 1
+    if scale is not None:
+        s = scale.to(device=x.device, dtype=torch.float32).contiguous()
+        sn = s.numel()
+        if sn > 1:
+            m = _scale_map(x, s, None, None)
+            if m is None or m.s_l != 1:
+                raise ValueError("fake_quant: scale must be per-tensor or vary along one axis run")
+            si = m.inner
+    _lib.call("vqx_fake_quant", _lib.ptr(x), _lib.dtype_tag(x.dtype), x.numel(),
+              _lib.ctypes.byref(fmt.desc(x.device)), _lib.ptr(s), sn, si, int(bool(mul_back)),
+              _lib.ptr(y), _lib.ptr(codes) if return_codes else None, cb, _lib.stream_of(x))
+    return y, codes
+
+
+_SCALE_DTYPES = {"e8m0": torch.uint8, "float32": torch.float32, "bfloat16": torch.bfloat16}
+
+
+@_impl("quantize_mx_packed")
+def quantize_mx_packed(input, dtype, axis, block_size, force_scale_power_of_two=True, quant_max=None,
+                       scale_dtype="e8m0"):
+    """Block scales + packed codes (code_bits per element, element i at bits
+    [cb*i, cb*i+cb) of a little-endian bitstream) along the last axis."""
+    _lib.require_device(input, "quantize_mx_packed")
+    fmt = parse_format(dtype)
+    if quant_max is None:
+        from ..formats import quant_range
+        quant_max = float(quant_range(dtype)[1])
+    x = input.contiguous()
+    ax, outer, L, inner = _axis_geometry(list(x.shape), axis)
+    if inner != 1:
+        raise ValueError("quantize_mx_packed blocks run along the last axis")
+    if scale_dtype not in _SCALE_DTYPES:
+        raise ValueError(f"scale_dtype must be one of {sorted(_SCALE_DTYPES)}")
+    if scale_dtype == "e8m0" and not force_scale_power_of_two:
+        raise ValueError("E8M0 scales need force_scale_power_of_two")
+    if scale_dtype == "bfloat16" and x.dtype != torch.bfloat16:
+        raise ValueError("bfloat16 scales need a bfloat16 input (scales come in the input dtype)")
+    nbytes = x.numel() * fmt.code_bits // 8
+    codes = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    sshape = list(x.shape)
+    sshape[ax] = -(-L // block_size)
+    sc = None
+    if scale_dtype != "bfloat16":
+        sc = torch.empty(sshape, dtype=_SCALE_DTYPES[scale_dtype], device=x.device)
+    s_in, _, _ = _mx_call(x, ax, block_size, quant_max, force_scale_power_of_two, None, fmt.desc(x.device),
+                          want_scale=scale_dtype == "bfloat16",
+                          scale_f32=sc if scale_dtype == "float32" else None,
+                          e8m0=sc if scale_dtype == "e8m0" else None,
+                          codes=codes, code_layout=0)
+    return (s_in if sc is None else sc), codes
+
+
+@_impl("dequantize_mx_packed")
+def dequantize_mx_packed(codes, scale, dtype, block_size, shape, out_dtype=torch.bfloat16):
+    _lib.require_device(codes, "dequantize_mx_packed")
+    fmt = parse_format(dtype)
+    n = math.prod(shape)
+    kind = {torch.float32: 0, torch.bfloat16: 1, torch.uint8: 2}.get(scale.dtype)
+    if kind is None:
+        raise ValueError(f"scale dtype {scale.dtype} not in float32/bfloat16/uint8(E8M0)")
+    dtab = fmt.tables(codes.device)["decode"]
+    out = torch.empty(list(shape), dtype=out_dtype, device=codes.device)
+    _lib.call("vqx_mx_decode", _lib.ptr(codes.contiguous()), fmt.code_bits, _lib.ptr(dtab), dtab.numel(),
+              _lib.ptr(scale.contiguous()), kind, n, block_size, _lib.ptr(out), _lib.dtype_tag(out_dtype),
+              _lib.stream_of(codes))
+    return out
+
+
+@_impl("codebook_encode")
+def codebook_encode(input, codebook):
+    """Per-row nearest-entry codes against sorted per-row codebooks [rows, K]."""
+    _lib.require_device(input, "codebook_encode")
+    x = input.contiguous()
+    rows = codebook.shape[0]
+    cb = codebook.to(device=x.device, dtype=torch.float32).contiguous()
+    if x.numel() % rows != 0:
+        raise ValueError("input rows must match codebook rows")
+    cols = x.numel() // rows
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    _lib.call("vqx_codebook_encode", _lib.ptr(x), _lib.dtype_tag(x.dtype), rows, cols, _lib.ptr(cb),
+              cb.shape[1], _lib.ptr(codes), _lib.stream_of(x))
+    return codes
+
+
+@_impl("codebook_decode")
+def codebook_decode(codes, codebook, dtype=torch.float32):
+    _lib.require_device(codes, "codebook_decode")
+    c = codes.contiguous()
+    rows = codebook.shape[0]
+    cb = codebook.to(device=c.device, dtype=torch.float32).contiguous()
+    cols = c.numel() // rows
+    out = torch.empty(c.shape, dtype=dtype, device=c.device)
+    _lib.call("vqx_codebook_decode", _lib.ptr(c), rows, cols, _lib.ptr(cb), cb.shape[1], _lib.ptr(out),
+              _lib.dtype_tag(dtype), _lib.stream_of(c))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# fake (meta) implementations for tracing
+# ---------------------------------------------------------------------------
+@torch.library.register_fake("quantized_ops::vmap")
+def _(input, qmap):
+    return torch.empty_like(input, memory_format=torch.contiguous_format)
+
+
+@torch.library.register_fake("quantized_ops::quantize")
+def _(input, scale, zero_point=None, axes=None, block_size=None, qmap=None, output_code=None):
+    return torch.empty_like(input, dtype=_compute_dtype(input, scale, zero_point))
+
+
+@torch.library.register_fake("quantized_ops::dequantize")
+def _(input, scale, zero_point=None, axes=None, block_size=None, input_qmap=None, output_qmap=None):
+    return torch.empty_like(input, dtype=_compute_dtype(input, scale, zero_point))
+
+
+@torch.library.register_fake("quantized_ops::calculate_mx_qparam")
+def _(input, axes, block_size, quant_max, force_scale_power_of_two=False, scale_qmap=None):
+    shape = list(input.shape)
+    for a in ([axes] if isinstance(axes, int) else axes):
+        shape[a] = -(-shape[a] // block_size)
+    return input.new_empty(shape)
+
+
+@torch.library.register_fake("quantized_ops::quantize_mx")
+def _(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False, scale_qmap=None,
+      output_code=None):
+    shape = list(input.shape)
+    for a in ([axes] if isinstance(axes, int) else axes):
+        shape[a] = -(-shape[a] // block_size)
+    return input.new_empty(shape), torch.empty_like(input, memory_format=torch.contiguous_format)
+
+
+@torch.library.register_fake("quantized_ops::linear_mx")
+def _(input, weight, bias=None, **kwargs):
+    return torch.nn.functional.linear(input, weight, bias)
+
+
+@torch.library.register_fake("quantized_ops::matmul_mx")
+def _(self, other, **kwargs):
+    return torch.matmul(self, other)
+
+
+@torch.library.register_fake("quantized_ops::fake_quant")
+def _(input, dtype, scale=None, mul_back=True, return_codes=False):
+    f = parse_format(dtype)
+    cdt = torch.uint8 if f.code_bits <= 8 else torch.int16
+    return torch.empty_like(input), input.new_empty(input.shape if return_codes else (0,), dtype=cdt)
+
+
+@torch.library.register_fake("quantized_ops::quantize_mx_packed")
+def _(input, dtype, axis, block_size, force_scale_power_of_two=True, quant_max=None, scale_dtype="e8m0"):
+    f = parse_format(dtype)
+    shape = list(input.shape)
+    shape[axis] = -(-shape[axis] // block_size)
+    return (input.new_empty(shape, dtype=_SCALE_DTYPES[scale_dtype]),
+            input.new_empty((input.numel() * f.code_bits // 8,), dtype=torch.uint8))
+
+
+@torch.library.register_fake("quantized_ops::dequantize_mx_packed")
+def _(codes, scale, dtype, block_size, shape, out_dtype=torch.bfloat16):
+    return codes.new_empty(list(shape), dtype=out_dtype)
+
+
+@torch.library.register_fake("quantized_ops::codebook_encode")
+def _(input, codebook):
+    return input.new_empty(input.shape, dtype=torch.uint8)
+
+
+@torch.library.register_fake("quantized_ops::codebook_decode")
+def _(codes, codebook, dtype=torch.float32):
+    return codes.new_empty(codes.shape, dtype=dtype)
