@@ -66,6 +66,9 @@ typedef struct vqx_format {
   const uint16_t* levels;      /* LEVELS: nlevels bf16 level patterns */
   const uint8_t* code_table;   /* LEVELS: 65536 codes, one per bf16 pattern */
   const uint16_t* value_table; /* TABLE: 65536 bf16 values, one per bf16 pattern */
+  const uint32_t* lut;         /* optional: table blob from vqx_build_lut (formats with
+                                  codes of at most 8 bits); NULL = closed form only */
+  int32_t lut_len;             /* that blob's entries per sign (blob word 4) */
 } vqx_format;
 
 /* Where element i of x finds its scale / zero point.  x is viewed as
@@ -139,6 +142,17 @@ int vqx_dequantize_mapped(const void* x, int32_t x_dtype, int64_t n, const uint1
  */
 int vqx_build_table(const vqx_format* fmt, uint16_t* values, uint16_t* codes,
                     vqx_stream_t stream);
+
+/* Bytes of the table blob vqx_build_lut writes. */
+int64_t vqx_lut_bytes(void);
+
+/*
+ * Compact code/value table of a format (codes of at most 8 bits) for the
+ * streaming kernels: blob word 0 = 1 if usable, word 4 = entries per sign
+ * (copy it to fmt->lut_len).  Built on the GPU from the closed-form encoder,
+ * so a kernel using it gives the same results.  blob: vqx_lut_bytes() bytes.
+ */
+int vqx_build_lut(const vqx_format* fmt, uint32_t* blob, vqx_stream_t stream);
 
 /*
  * Level-set tables for quantize_to_nf (src/vc/quantization/dtypes/normal_float.py:54-60,

@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared_symbols():
     text = open(os.path.join(ROOT, "include", "vqx.h")).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(vqx_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(vqx_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol(vqx):

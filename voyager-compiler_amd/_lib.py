@@ -33,6 +33,8 @@ class VqxFormat(ctypes.Structure):
         ("levels", ctypes.c_void_p),
         ("code_table", ctypes.c_void_p),
         ("value_table", ctypes.c_void_p),
+        ("lut", ctypes.c_void_p),
+        ("lut_len", ctypes.c_int32),
     ]
 
 
@@ -66,6 +68,8 @@ _SIGNATURES = {
     "vqx_dequantize_mapped": ([_P, _I32, _I64, _P, ctypes.POINTER(VqxScaleMap), _P, _P, _P],
                               ctypes.c_int),
     "vqx_build_table": ([ctypes.POINTER(VqxFormat), _P, _P, _P], ctypes.c_int),
+    "vqx_lut_bytes": ([], ctypes.c_int64),
+    "vqx_build_lut": ([ctypes.POINTER(VqxFormat), _P, _P], ctypes.c_int),
     "vqx_level_tables": ([_P, _I32, _I32, _P, _P, _P, _P, _P], ctypes.c_int),
     "vqx_mx_quantize": ([_P, _I32, _I64, _I64, _I64, _I64, ctypes.POINTER(VqxFormat), _I32, _I32,
                          _F, _P, _P, _P, _P, _P, _P, _P, _I32, _P], ctypes.c_int),

@@ -282,6 +282,178 @@ __global__ __launch_bounds__(256) void mx_block_kernel(const T* __restrict__ x, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// LUT fast path: bf16 input, blocks of 16*LPB along the last dim.
+// ---------------------------------------------------------------------------
+// RN_bf16(x / s) for bf16-valued x and s (s normal with a normal reciprocal):
+// q = x * rcp(s) is within 1.5 ulp32 of x / s, so its bf16 rounding is the
+// exact one unless q lies within a few ulp32 of a bf16 midpoint, where the
+// IEEE division decides.  (An exact quotient of two 8-bit significands is
+// either a bf16 midpoint itself or at least 2^-17 away from every midpoint,
+// so the fp32 division's own rounding never moves it across one.)
+__device__ __forceinline__ uint32_t div_bf16_fast(float x, float s, float r) {
+  float q = x * r;
+  uint32_t qb = f2u(q);
+  if ((qb & 0xFFFFu) - 0x7FFCu <= 8u) qb = f2u(x / s);
+  return f2bf(u2f(qb));
+}
+
+// Block scale of a bf16 block, specialised by mode (branch-free).
+template <bool ABSMAX>
+__device__ __forceinline__ float block_scale_bf16(uint32_t amax, const ScaleParams& sp) {
+  if constexpr (!ABSMAX) {
+    // e = floor(bf16 log2(amax)) - shift (amax 0 -> -126); 2**e in bf16 keeps
+    // 2^-133 .. 2^127 and rounds 2^-134 and below to 0, which becomes 1
+    int e = (amax == 0 ? -126 : log2floor_bf16(amax)) - sp.shift;
+    float sc = e > 127 ? __builtin_huge_valf() : (e >= -133 ? exp2i(e) : 1.0f);
+    sc = amax == 0x7F80u ? __builtin_huge_valf() : sc;
+    return amax > 0x7F80u ? 1.0f : sc;
+  } else {
+    float sc = bf2f(f2bf(bf2f(amax) / sp.quant_max));
+    if (sp.scale_qmap) sc = bf2f(f2bf(bf2f(sp.scale_qmap[f2bf(sc)])));
+    return sc > 0.0f ? sc : 1.0f;
+  }
+}
+
+// WANT: bit 0 = reference quantize() values, bit 1 = fake-quant values.
+template <int CB, int LPB, bool ABSMAX, int WANT>
+__global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict__ x, int64_t ngroups,
+                                                     ScaleParams sp, LutView lv, MxOut out) {
+  extern __shared__ uint32_t lds_lut[];
+  LutLds t = lut_to_lds(lv.blob, lv.len, lds_lut);
+  const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
+    uint32_t w[8];
+    {
+      const u32x4* q = reinterpret_cast<const u32x4*>(x + g * 16);
+      u32x4 a0 = ld_nt(q), a1 = ld_nt(q + 1);
+      w[0] = a0.x; w[1] = a0.y; w[2] = a0.z; w[3] = a0.w;
+      w[4] = a1.x; w[5] = a1.y; w[6] = a1.z; w[7] = a1.w;
+    }
+    uint32_t m2 = 0;  // two 16-bit magnitude maxima per word
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t a2 = w[j] & 0x7FFF7FFFu;
+      uint32_t lo = umax32(m2 & 0xFFFFu, a2 & 0xFFFFu), hi = umax32(m2 >> 16, a2 >> 16);
+      m2 = lo | (hi << 16);
+    }
+    uint32_t amax = umax32(m2 & 0xFFFFu, m2 >> 16);
+#pragma unroll
+    for (int off = 1; off < LPB; off <<= 1) amax = umax32(amax, (uint32_t)__shfl_xor((int)amax, off, 64));
+    float s = block_scale_bf16<ABSMAX>(amax, sp);
+    uint32_t sb = f2u(s);
+    uint32_t sE = (sb >> 23) & 0xFFu;
+    bool fast;
+    float rcp, sz;
+    if constexpr (!ABSMAX) {
+      // a power of two in [2^-100, 2^100]: x / s and v * s are exact
+      // scalings (quotients below bf16's normal range only reach the table's
+      // entry 0, as every format here has T0 above it); a quotient keeps its
+      // sign unless it rounds to a bf16 zero, i.e. unless |x| <= 2^-134 s
+      fast = (sb & 0x7FFFFFu) == 0 && sE >= 27 && sE <= 227 && amax < 0x7F80u && t.t0m1 >= 0x80u;
+      rcp = u2f((254u - sE) << 23);
+      int ze = (int)sE - 127 - 134;
+      sz = ze >= -149 ? exp2i(ze) : 0.0f;
+    } else {
+      fast = sE >= 2 && sE <= 252 && amax < 0x7F80u;
+      rcp = __builtin_amdgcn_rcpf(s);
+      sz = 0.0f;
+    }
+    uint32_t code[16], qv[16], fv[16];
+    if (fast) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
+        float xv = u2f(xb);
+        uint32_t idx;
+        if constexpr (!ABSMAX) {
+          uint32_t qb = f2u(xv * rcp);
+          uint32_t a = (qb >> 16) & 0x7FFFu;
+          uint32_t c = a < t.t0m1 ? t.t0m1 : a;
+          c = c > t.t1 ? t.t1 : c;
+          uint32_t neg = ((__builtin_fabsf(xv) > sz) | t.zsign) ? xb >> 31 : 0u;
+          idx = c - t.t0m1 + neg * t.len;
+        } else {
+          idx = lut_index(t, div_bf16_fast(xv, s, rcp));
+        }
+        uint32_t e = t.pos[idx];
+        code[j] = e >> 16;
+        uint32_t v = e & 0xFFFFu;
+        if constexpr (WANT & 1) qv[j] = v;
+        if constexpr (WANT & 2) fv[j] = ABSMAX ? f2bf(u2f(v << 16) * s) : (f2u(u2f(v << 16) * s) >> 16);
+      }
+    } else {
+      // scale 1 (NaN block), Inf, subnormal or extreme: exact division and
+      // the full table
+#pragma unroll 1
+      for (int j = 0; j < 16; ++j) {
+        uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
+        uint32_t h = f2bf(u2f(xb) / s);
+        uint32_t e = full[h];
+        code[j] = e >> 16;
+        uint32_t v = e & 0xFFFFu;
+        qv[j] = v;
+        fv[j] = f2bf(u2f(v << 16) * s);
+      }
+    }
+    if constexpr (WANT & 1) BT<uint16_t>::store16(static_cast<uint16_t*>(out.qvals) + g * 16, qv);
+    if constexpr (WANT & 2) BT<uint16_t>::store16(static_cast<uint16_t*>(out.fq) + g * 16, fv);
+    if constexpr (CB > 0) store_group_codes<CB>(static_cast<uint8_t*>(out.codes), g, code);
+    if ((threadIdx.x & (LPB - 1)) == 0) {
+      int64_t blk = g / LPB;
+      if (out.scale) BT<uint16_t>::put(static_cast<uint16_t*>(out.scale) + blk, f2bf(s));
+      if (out.scale_f32) out.scale_f32[blk] = s;
+      if (out.scale_e8m0) out.scale_e8m0[blk] = (uint8_t)e8m0_of(s);
+    }
+  }
+}
+
+template <int CB, int LPB, bool ABSMAX>
+static int launch_lut_want(const uint16_t* x, int64_t ngroups, const ScaleParams& sp, const LutView& lv,
+                           const MxOut& out, hipStream_t st) {
+  const int bs = 256;
+  unsigned grid = grid_for(ngroups, bs);
+  size_t lds = sizeof(uint32_t) * 2 * lv.len;
+  int want = (out.qvals ? 1 : 0) | (out.fq ? 2 : 0);
+  switch (want) {
+    case 0: hipLaunchKernelGGL((mx_lut_kernel<CB, LPB, ABSMAX, 0>), dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out); break;
+    case 1: hipLaunchKernelGGL((mx_lut_kernel<CB, LPB, ABSMAX, 1>), dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out); break;
+    case 2: hipLaunchKernelGGL((mx_lut_kernel<CB, LPB, ABSMAX, 2>), dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out); break;
+    default: hipLaunchKernelGGL((mx_lut_kernel<CB, LPB, ABSMAX, 3>), dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out); break;
+  }
+  return check_launch("mx_quantize(lut)");
+}
+
+template <int CB, bool ABSMAX>
+static int launch_lut_lpb(const uint16_t* x, int64_t ngroups, int lpb, const ScaleParams& sp,
+                          const LutView& lv, const MxOut& out, hipStream_t st) {
+  switch (lpb) {
+    case 1: return launch_lut_want<CB, 1, ABSMAX>(x, ngroups, sp, lv, out, st);
+    case 2: return launch_lut_want<CB, 2, ABSMAX>(x, ngroups, sp, lv, out, st);
+    case 4: return launch_lut_want<CB, 4, ABSMAX>(x, ngroups, sp, lv, out, st);
+    case 8: return launch_lut_want<CB, 8, ABSMAX>(x, ngroups, sp, lv, out, st);
+    default: return set_error(kErrInvalid, "block size %d not supported on the table path", lpb * 16);
+  }
+}
+
+static int launch_lut(const uint16_t* x, int64_t n, int lpb, int cb, const ScaleParams& sp, const LutView& lv,
+                      const MxOut& out, hipStream_t st) {
+  int64_t ngroups = n / 16;
+  bool absmax = sp.mode == 1;
+#define VQX_LUT_CB(C)                                                                        \
+  return absmax ? launch_lut_lpb<C, true>(x, ngroups, lpb, sp, lv, out, st)                  \
+                : launch_lut_lpb<C, false>(x, ngroups, lpb, sp, lv, out, st);
+  switch (cb) {
+    case 0: VQX_LUT_CB(0)
+    case 4: VQX_LUT_CB(4)
+    case 6: VQX_LUT_CB(6)
+    case 8: VQX_LUT_CB(8)
+    default: return set_error(kErrInvalid, "table path packs 4-, 6- or 8-bit codes, not %d", cb);
+  }
+#undef VQX_LUT_CB
+}
+
 template <typename T, typename Enc, int CB>
 static int launch_group(const T* x, int64_t n, int lpb, const ScaleParams& sp, const Enc& enc,
                         const MxOut& out, hipStream_t st) {
@@ -354,6 +526,20 @@ int mx_quantize(const void* x, int dtype, int64_t outer, int64_t L, int64_t inne
   if (code_layout < 0 || code_layout > 2) return set_error(kErrInvalid, "code layout must be 0, 1 or 2");
   if (out.scale_e8m0 && sp.mode != 0)
     return set_error(kErrInvalid, "E8M0 scales need power-of-two scaling");
+  {
+    int64_t n = outer * L * inner;
+    int64_t lpb = bs / 16;
+    bool packed = out.codes && code_layout == 0;
+    bool fast = dtype == kBF16 && fmt.lut && inner == 1 && bs % 16 == 0 && L % bs == 0 && lpb >= 1 &&
+                lpb <= 8 && (lpb & (lpb - 1)) == 0 && aligned(x, 16) &&
+                (!out.qvals || aligned(out.qvals, 16)) && (!out.fq || aligned(out.fq, 16)) &&
+                (!out.codes || aligned(out.codes, 16)) && (!out.codes || packed);
+    if (n == 0) return kOk;
+    if (fast) {
+      LutView lv{fmt.lut, fmt.lut_len};
+      return launch_lut((const uint16_t*)x, n, (int)lpb, packed ? fmt.code_bits : 0, sp, lv, out, st);
+    }
+  }
   return with_encoder(fmt, [&](auto enc) -> int {
     using E = decltype(enc);
     if (dtype == kBF16)

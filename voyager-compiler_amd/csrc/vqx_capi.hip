@@ -50,6 +50,10 @@ static int to_desc(const vqx_format* f, FormatDesc* d) {
   d->levels = f->levels;
   d->code_table = f->code_table;
   d->value_table = f->value_table;
+  d->lut = f->lut;
+  d->lut_len = f->lut_len;
+  if (d->lut && (d->lut_len < 1 || d->lut_len > kLutMaxLen))
+    return set_error(kErrInvalid, "lut_len %d outside [1, %d]", d->lut_len, kLutMaxLen);
   return kOk;
 }
 
@@ -127,6 +131,16 @@ int vqx_build_table(const vqx_format* fmt, uint16_t* values, uint16_t* codes, vq
   FormatDesc d;
   VQX_TRY(to_desc(fmt, &d));
   return build_table(d, values, codes, (hipStream_t)stream);
+}
+
+int64_t vqx_lut_bytes(void) { return kLutBytes; }
+
+int vqx_build_lut(const vqx_format* fmt, uint32_t* blob, vqx_stream_t stream) {
+  g_err[0] = 0;
+  FormatDesc d;
+  VQX_TRY(to_desc(fmt, &d));
+  if (!blob) return set_error(kErrInvalid, "build_lut: null blob");
+  return build_lut(d, blob, (hipStream_t)stream);
 }
 
 int vqx_level_tables(const float* levels, int32_t K, int32_t mode, uint8_t* index_table,

@@ -177,6 +177,52 @@ __global__ __launch_bounds__(256) void fq_vec_kernel(const T* __restrict__ x, T*
   }
 }
 
+// Table path of the per-tensor fake-quant: the format comes from the
+// compact LDS table (magnitudes >= S from the full table in global memory).
+template <typename T, int CB>
+__global__ __launch_bounds__(256) void fq_lut_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                     void* __restrict__ codes, int64_t n,
+                                                     const float* __restrict__ scale, bool mul, LutView lv) {
+  extern __shared__ uint32_t lds_lut[];
+  LutLds t = lut_to_lds(lv.blob, lv.len, lds_lut);
+  const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
+  constexpr bool kBf16 = std::is_same<T, uint16_t>::value;
+  float s = scale ? scale[0] : 1.0f;
+  s = to_dtype<T>(s);
+  const bool unit = s == 1.0f;
+  const int64_t nvec = n / 8;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < nvec; g += stride) {
+    float v[8];
+    uint32_t c[8];
+    IO<T>::load(x + g * 8, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t h;
+      if (unit)
+        h = kBf16 ? (f2u(v[j]) >> 16) : f2bf(v[j]);
+      else
+        h = f2bf(to_dtype<T>(v[j] / s));
+      uint32_t e = (h & 0x7FFFu) < t.s ? lut_entry(t, h) : full[h];
+      c[j] = e >> 16;
+      float q = u2f(e << 16);
+      v[j] = unit ? (kBf16 ? q : to_dtype<T>(q)) : (mul ? to_dtype<T>(to_dtype<T>(q) * s) : to_dtype<T>(q));
+    }
+    if (y) IO<T>::store(y + g * 8, v);
+    if constexpr (CB > 0) store_codes8<CB>(codes, g * 8, c);
+  }
+  int64_t i = nvec * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    float xv = IO<T>::get(x + i);
+    uint32_t h = unit ? (kBf16 ? (f2u(xv) >> 16) : f2bf(xv)) : f2bf(to_dtype<T>(xv / s));
+    uint32_t e = full[h];
+    float q = u2f(e << 16);
+    float r = unit ? (kBf16 ? q : to_dtype<T>(q)) : (mul ? to_dtype<T>(to_dtype<T>(q) * s) : to_dtype<T>(q));
+    if (y) IO<T>::put(y + i, r);
+    if constexpr (CB > 0) store_code1<CB>(codes, i, e >> 16);
+  }
+}
+
 // General path: any alignment, per-channel scales (channel of element i is
 // (i / inner) % C).
 template <typename T, typename Enc, int CB>
@@ -239,6 +285,18 @@ static int launch_fq_dtype(const void* x, int dtype, void* y, void* codes, int c
   }
 }
 
+template <typename T>
+static int launch_fq_lut(const T* x, T* y, void* codes, int code_bytes, int64_t n, const float* scale, bool mul,
+                         const LutView& lv, hipStream_t st) {
+  unsigned grid = grid_for(n / 8 + 1, 256);
+  size_t lds = sizeof(uint32_t) * 2 * lv.len;
+  if (code_bytes == 0)
+    hipLaunchKernelGGL((fq_lut_kernel<T, 0>), dim3(grid), dim3(256), lds, st, x, y, codes, n, scale, mul, lv);
+  else
+    hipLaunchKernelGGL((fq_lut_kernel<T, 1>), dim3(grid), dim3(256), lds, st, x, y, codes, n, scale, mul, lv);
+  return check_launch("fake_quant(lut)");
+}
+
 int fake_quant(const void* x, int dtype, int64_t n, const FormatDesc& fmt, const float* scale,
                int64_t scale_numel, int64_t scale_inner, bool mul, void* y, void* codes, int code_bytes,
                hipStream_t st) {
@@ -246,6 +304,17 @@ int fake_quant(const void* x, int dtype, int64_t n, const FormatDesc& fmt, const
   if (code_bytes != 0 && code_bytes != 1 && code_bytes != 2)
     return set_error(kErrInvalid, "code width must be 1 or 2 bytes");
   if (scale_numel > 1 && scale_inner < 1) return set_error(kErrInvalid, "scale_inner must be >= 1");
+  if (n == 0) return kOk;
+  if (fmt.lut && scale_numel <= 1 && code_bytes <= 1 && aligned(x, 16) && (!y || aligned(y, 16)) &&
+      (code_bytes == 0 || aligned(codes, 8))) {
+    LutView lv{fmt.lut, fmt.lut_len};
+    switch (dtype) {
+      case kF32: return launch_fq_lut((const float*)x, (float*)y, codes, code_bytes, n, scale, mul, lv, st);
+      case kBF16: return launch_fq_lut((const uint16_t*)x, (uint16_t*)y, codes, code_bytes, n, scale, mul, lv, st);
+      case kF16: return launch_fq_lut((const __half*)x, (__half*)y, codes, code_bytes, n, scale, mul, lv, st);
+      default: break;
+    }
+  }
   return with_encoder(fmt, [&](auto enc) {
     return launch_fq_dtype(x, dtype, y, codes, code_bytes, n, scale, scale_inner, scale_numel, mul, enc, st);
   });
@@ -389,6 +458,74 @@ int build_table(const FormatDesc& fmt, uint16_t* values, uint16_t* codes, hipStr
   return with_encoder(fmt, [&](auto enc) {
     hipLaunchKernelGGL((build_table_kernel<decltype(enc)>), dim3(256), dim3(256), 0, st, values, codes, enc);
     return check_launch("build_table");
+  });
+}
+
+// Compact LUT (vqx_lut.h): tabulate entries, find the flush and saturation
+// runs shared by both signs, copy the table between them.
+template <typename Enc>
+__global__ __launch_bounds__(256) void lut_full_kernel(uint32_t* full, Enc enc) {
+  uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= 65536u) return;
+  Result r = enc.encode(h);
+  full[h] = (r.value & 0xFFFFu) | (r.code << 16);
+}
+
+__global__ __launch_bounds__(256) void lut_bounds_kernel(const uint32_t* full, uint32_t S, uint32_t* hdr) {
+  uint32_t a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a < 1 || a >= S) return;
+  if (full[a] != full[1] || full[0x8000u | a] != full[0x8001u]) atomicMin(&hdr[kLutT0m1], a);
+  if (full[a] != full[S - 1] || full[0x8000u | a] != full[0x8000u | (S - 1)]) atomicMax(&hdr[kLutT1], a);
+}
+
+__global__ void lut_finalize_kernel(const uint32_t* full, uint32_t S, uint32_t* hdr) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  uint32_t first = hdr[kLutT0m1], last = hdr[kLutT1];
+  uint32_t t0m1 = first == 0xFFFFFFFFu ? S - 1 : first - 1;  // >= 1
+  if (full[0] != full[t0m1]) t0m1 = 0;  // +0 must share entry 0 with the run below T0
+  uint32_t t1 = last == 0 ? t0m1 : last + 1;
+  if (t1 > S - 1) t1 = S - 1;
+  if (t1 < t0m1) t1 = t0m1;
+  uint32_t len = t1 - t0m1 + 1;
+  hdr[kLutT0m1] = t0m1;
+  hdr[kLutT1] = t1;
+  hdr[kLutS] = S;
+  hdr[kLutLen] = len;
+  // -0 must encode like the tiny negatives or like +0
+  uint32_t zsign = full[0x8000u] == full[0x8000u | t0m1] ? 1u : 0u;
+  bool zok = zsign || full[0x8000u] == full[t0m1];
+  hdr[kLutZeroSign] = zsign;
+  hdr[kLutValid] = (len <= (uint32_t)kLutMaxLen && zok) ? 1u : 0u;
+}
+
+__global__ __launch_bounds__(256) void lut_copy_kernel(const uint32_t* full, uint32_t* blob) {
+  uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (!blob[kLutValid]) return;
+  uint32_t len = blob[kLutLen], t0m1 = blob[kLutT0m1];
+  if (i >= len) return;
+  blob[kLutHeaderWords + i] = full[t0m1 + i];
+  blob[kLutHeaderWords + len + i] = full[0x8000u | (t0m1 + i)];
+}
+
+__global__ void lut_init_kernel(uint32_t* hdr) {
+  if (threadIdx.x < kLutHeaderWords) hdr[threadIdx.x] = threadIdx.x == kLutT0m1 ? 0xFFFFFFFFu : 0u;
+}
+
+int build_lut(const FormatDesc& fmt, uint32_t* blob, hipStream_t st) {
+  if (fmt.code_bits > 8) return set_error(kErrInvalid, "tables hold codes of at most 8 bits");
+  // magnitudes from S up take the closed form: Inf/NaN, and the fp core's
+  // NaN region (bf16 log2 = 128)
+  uint32_t S = fmt.kind == kFmtFpCore ? 0x7F58u : 0x7F80u;
+  uint32_t* full = blob + kLutHeaderWords + 2 * kLutMaxLen;
+  FormatDesc d = fmt;
+  d.lut = nullptr;
+  return with_encoder(d, [&](auto enc) {
+    hipLaunchKernelGGL((lut_full_kernel<decltype(enc)>), dim3(256), dim3(256), 0, st, full, enc);
+    hipLaunchKernelGGL(lut_init_kernel, dim3(1), dim3(64), 0, st, blob);
+    hipLaunchKernelGGL(lut_bounds_kernel, dim3(128), dim3(256), 0, st, full, S, blob);
+    hipLaunchKernelGGL(lut_finalize_kernel, dim3(1), dim3(64), 0, st, full, S, blob);
+    hipLaunchKernelGGL(lut_copy_kernel, dim3(kLutMaxLen / 256), dim3(256), 0, st, full, blob);
+    return check_launch("build_lut");
   });
 }
 

@@ -22,6 +22,8 @@ struct FormatDesc {
   const uint16_t* levels;    // kFmtLevels: nlevels bf16 patterns
   const uint8_t* code_table; // kFmtLevels: 65536 codes, one byte each
   const uint16_t* value_table; // kFmtTable: 65536 bf16 values
+  const uint32_t* lut;         // compact LDS table blob (vqx_lut.h), or null
+  int32_t lut_len;             // entries per sign of that table
 };
 
 // kBits: the packed code width an encoder always produces (0 = depends on the

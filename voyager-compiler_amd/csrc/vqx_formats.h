@@ -88,31 +88,23 @@ VQX_HD float exp2i(int e) {
 // the result steps up are listed directly.  Every entry is checked against
 // torch's own bf16 log2 for all 2^16 patterns by the CPU test suite.
 VQX_HD uint32_t log2_step_threshold(int E) {
-  // b = -1 .. 6 -> threshold; index b + 1.  128 means "never".
-  const uint8_t kByBand[8] = {128, 128, 127, 126, 123, 118, 107, 88};
+  // thresholds for b = -1 .. 6 (128 = never), one byte each, b + 1 = byte index:
+  // 128, 128, 127, 126, 123, 118, 107, 88
+  const uint64_t kByBand = 0x586B767B7E7F8080ull;
   int p = E - 127;
-  int band;
-  if (p >= 0) {
-    uint32_t n = (uint32_t)p + 1u;
-    band = 31 - clz32(n);
-    if ((n & (n - 1u)) == 0) band -= 1;
-  } else if (p == -1) {
-    return 128;
-  } else {
-    uint32_t n = (uint32_t)(-p - 1);
-    band = 31 - clz32(n);
-  }
-  return kByBand[band + 1];
+  // n = p + 1 for p >= 0, -(p + 1) below; p == -1 gives n = 0 and band -1
+  uint32_t n = p >= 0 ? (uint32_t)p + 1u : (uint32_t)(-p - 1);
+  int band = 31 - clz32(n);
+  band -= (p >= 0 && (n & (n - 1u)) == 0) ? 1 : 0;
+  return (uint32_t)(kByBand >> (8 * (band + 1))) & 0xFFu;
 }
 
 // floor(bf16(log2(a))) for a positive finite bf16 magnitude pattern (1..0x7F7F).
 VQX_HD int log2floor_bf16(uint32_t mag) {
   uint32_t E = mag >> 7, m = mag & 0x7Fu;
-  if (E == 0) {
-    return -133 + (m >= 2) + (m >= 3) + (m >= 6) + (m >= 12) + (m >= 23) +
-           (m >= 54) + (m >= 108);
-  }
-  return (int)E - 127 + (m >= log2_step_threshold((int)E) ? 1 : 0);
+  int sub = -133 + (m >= 2) + (m >= 3) + (m >= 6) + (m >= 12) + (m >= 23) + (m >= 54) + (m >= 108);
+  int nrm = (int)E - 127 + (m >= log2_step_threshold((int)E) ? 1 : 0);
+  return E == 0 ? sub : nrm;
 }
 
 // Round-to-nearest-even of mant / 2^sh for sh >= 0 (sh may exceed 31).

@@ -3,6 +3,7 @@
 #pragma once
 
 #include "vqx_encoders.h"
+#include "vqx_lut.h"
 
 namespace vqx {
 
@@ -39,6 +40,7 @@ int fake_quant(const void* x, int dtype, int64_t n, const FormatDesc& fmt, const
                hipStream_t st);
 int lut_gather(const void* x, int dtype, int64_t n, const uint16_t* table, void* y, hipStream_t st);
 int build_table(const FormatDesc& fmt, uint16_t* values, uint16_t* codes, hipStream_t st);
+int build_lut(const FormatDesc& fmt, uint32_t* blob, hipStream_t st);
 int level_tables(const float* levels, int K, int mode, uint8_t* index_table, float* boundaries,
                  uint32_t* work, int* bad, hipStream_t st);
 

@@ -133,6 +133,16 @@ class Format:
                 t["boundaries"] = bnd
                 t["monotone"] = int(bad.item()) == 0
             desc = self._desc_from(t)
+            t["desc_closed"] = desc
+            if self.code_bits <= 8:
+                # compact code/value table for the streaming kernels
+                blob = torch.empty(int(_lib.load().vqx_lut_bytes()) // 4, dtype=torch.int32, device=device)
+                _lib.call("vqx_build_lut", _lib.ctypes.byref(desc), _lib.ptr(blob), sptr)
+                hdr = blob[:16].cpu()
+                if int(hdr[0]) == 1:
+                    t["lut"] = blob
+                    t["lut_len"] = int(hdr[4])
+                    desc = self._desc_from(t)
             vals = torch.empty(65536, dtype=torch.bfloat16, device=device)
             codes = torch.empty(65536, dtype=torch.int16, device=device)
             _lib.call("vqx_build_table", _lib.ctypes.byref(desc), _lib.ptr(vals), _lib.ptr(codes), sptr)
@@ -155,11 +165,16 @@ class Format:
             d.boundaries = t["boundaries"].data_ptr()
             d.levels = t["levels_bf16"].data_ptr()
             d.code_table = t["index_table"].data_ptr()
+        if "lut" in t:
+            d.lut = t["lut"].data_ptr()
+            d.lut_len = t["lut_len"]
         return d
 
-    def desc(self, device):
-        """ctypes ``vqx_format`` for kernels on ``device``."""
-        return self.tables(device)["desc"]
+    def desc(self, device, lut=True):
+        """ctypes ``vqx_format`` for kernels on ``device``; ``lut=False`` gives
+        the closed-form-only descriptor (the table path's cross-check)."""
+        t = self.tables(device)
+        return t["desc"] if lut else t["desc_closed"]
 
 
 _CACHE = {}
