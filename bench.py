@@ -169,6 +169,25 @@ def setup_c4(vqx, torch, L, K, decode=False):
         elements=n, bytes=algo, bound="hbm", dtype="u8->f32")
 
 
+def setup_c5(vqx, torch, L):
+    g = torch.Generator().manual_seed(4)
+    M, N, K = 2048, 11008, 4096
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).cuda()
+    Q = torch.ops.quantized_ops
+    sc, codes = Q.quantize_mx_packed(W, "nf4", -1, 64, False, 1.0, "float32")
+    del W
+    lv = vqx.parse_format("nf4").tables(A.device)["levels_bf16"]
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    st = L.stream_of(A)
+    fn = L.load().vqx_nf4_linear
+    args = (L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), M, N, K, st)
+    return (lambda: fn(*args)), dict(
+        name="C5 NF4-dequant linear: A bf16 [2048,4096] x W NF4 block-64 [11008,4096]^T -> bf16, fp32 accumulate",
+        elements=M * N, flops=2 * M * N * K, bytes=M * K * 2 + N * K // 2 + N * K // 64 * 4 + M * N * 2,
+        bound="mfma", dtype="bf16")
+
+
 CONFIGS = {
     "c2": lambda v, t, L: setup_c2(v, t, L),
     "c1": lambda v, t, L: setup_c1(v, t, L),
@@ -180,6 +199,7 @@ CONFIGS = {
     "c4_k16": lambda v, t, L: setup_c4(v, t, L, 16),
     "c4_k256": lambda v, t, L: setup_c4(v, t, L, 256),
     "c4_k16_decode": lambda v, t, L: setup_c4(v, t, L, 16, decode=True),
+    "c5": lambda v, t, L: setup_c5(v, t, L),
 }
 HEADLINE = "c2"
 
@@ -282,8 +302,15 @@ def main():
             "kernel_ms": ms, "region_ms_per_step": tm["region_ms"] / a.steps,
             "algorithmic_bytes": info["bytes"], "achieved_GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
             "dtype": info["dtype"]}
-        print(f"[bench] {k}: {ms * 1e3:.1f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)",
-              file=sys.stderr, flush=True)
+        if info["bound"] == "mfma":
+            tf = info["flops"] / (ms * 1e-3) / 1e12
+            results[k].update({"algorithmic_flops": info["flops"], "achieved_TFLOPs": tf,
+                               "mfma_frac": tf / BF16_PEAK_TFLOPS})
+            print(f"[bench] {k}: {ms * 1e3:.1f} us/launch, {tf:.0f} TFLOP/s ({tf / BF16_PEAK_TFLOPS:.1%} of bf16 "
+                  f"MFMA peak)", file=sys.stderr, flush=True)
+        else:
+            print(f"[bench] {k}: {ms * 1e3:.1f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)",
+                  file=sys.stderr, flush=True)
         if k == HEADLINE:
             info_head = info
         del launch

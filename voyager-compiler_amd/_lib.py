@@ -77,6 +77,7 @@ _SIGNATURES = {
     "vqx_decode_table": ([ctypes.POINTER(VqxFormat), _P, _I32, _P], ctypes.c_int),
     "vqx_codebook_encode": ([_P, _I32, _I64, _I64, _P, _I32, _P, _P], ctypes.c_int),
     "vqx_codebook_decode": ([_P, _I64, _I64, _P, _I32, _P, _I32, _P], ctypes.c_int),
+    "vqx_nf4_linear": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
 }
 
 _lib = None

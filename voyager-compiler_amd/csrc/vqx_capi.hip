@@ -200,4 +200,12 @@ int vqx_codebook_decode(const uint8_t* codes, int64_t rows, int64_t cols, const 
   return codebook_decode(codes, rows, cols, cb, K, out, out_dtype, (hipStream_t)stream);
 }
 
+int vqx_nf4_linear(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
+                   const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K,
+                   vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (!A || !codes || !scale || !levels || !out) return set_error(kErrInvalid, "nf4_linear: null buffer");
+  return nf4_gemm(A, codes, scale, levels, bias, out, M, N, K, (hipStream_t)stream);
+}
+
 }  // extern "C"

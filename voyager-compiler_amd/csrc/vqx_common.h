@@ -56,6 +56,33 @@ __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) {
 // Round-to-nearest-even fp32 -> bf16 pattern, every NaN to 0x7FC0.
 __device__ __forceinline__ uint32_t f2bf_dev(float f) { return f2bf(f); }
 
+// Exact fp16 <-> fp32 conversions in integer arithmetic (subnormals and signed
+// zeros kept, round to nearest even), independent of the device's fp16
+// denormal mode; torch's CPU conversions are the reference.
+__device__ __forceinline__ float h2f_exact(uint32_t hb) {
+  uint32_t s = (hb & 0x8000u) << 16;
+  uint32_t e = (hb >> 10) & 0x1Fu, m = hb & 0x3FFu;
+  uint32_t nrm = s | ((e + 112u) << 23) | (m << 13);
+  uint32_t inf = s | 0x7F800000u | (m << 13);
+  uint32_t sub = s | f2u((float)m * 0x1p-24f);  // m * 2^-24 is exact in fp32
+  return u2f(e == 0x1Fu ? inf : (e != 0 ? nrm : sub));
+}
+
+__device__ __forceinline__ uint32_t f2h_exact(float f) {
+  uint32_t b = f2u(f);
+  uint32_t s = (b >> 16) & 0x8000u;
+  uint32_t a = b & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return s | 0x7E00u;        // NaN
+  if (a >= 0x477FF000u) return s | 0x7C00u;       // rounds to >= 65520: Inf
+  if (a >= 0x38800000u) {                         // normal fp16 range
+    uint32_t r = a + 0xFFFu + ((a >> 13) & 1u);   // RNE at bit 13
+    return s | ((r >> 13) - (112u << 10));
+  }
+  // subnormal fp16: multiples of 2^-24; round |f| * 2^24 to an integer
+  float q = u2f(a) * 0x1p24f;                     // exact scaling
+  return s | (uint32_t)__builtin_rintf(q);
+}
+
 // Grid sizing: enough workgroups to cover the work, capped at a few per CU;
 // kernels loop grid-stride beyond that.
 inline unsigned grid_for(int64_t work_items, int per_block, int max_per_cu = 8) {

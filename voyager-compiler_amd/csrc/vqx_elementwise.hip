@@ -68,25 +68,23 @@ struct IO<__half> {
     uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      __half lo = __ushort_as_half((unsigned short)(w[j] & 0xFFFFu));
-      __half hi = __ushort_as_half((unsigned short)(w[j] >> 16));
-      v[2 * j] = __half2float(lo);
-      v[2 * j + 1] = __half2float(hi);
+      v[2 * j] = h2f_exact(w[j] & 0xFFFFu);
+      v[2 * j + 1] = h2f_exact(w[j] >> 16);
     }
   }
   __device__ static void store(__half* p, const float (&v)[8]) {
     uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t lo = __half_as_ushort(__float2half_rn(v[2 * j]));
-      uint32_t hi = __half_as_ushort(__float2half_rn(v[2 * j + 1]));
-      w[j] = lo | (hi << 16);
-    }
+    for (int j = 0; j < 4; ++j) w[j] = f2h_exact(v[2 * j]) | (f2h_exact(v[2 * j + 1]) << 16);
     u32x4 a = {w[0], w[1], w[2], w[3]};
     st_nt(reinterpret_cast<u32x4*>(p), a);
   }
-  __device__ static float get(const __half* p) { return __half2float(*p); }
-  __device__ static void put(__half* p, float v) { *p = __float2half_rn(v); }
+  __device__ static float get(const __half* p) {
+    return h2f_exact(*reinterpret_cast<const uint16_t*>(p));
+  }
+  __device__ static void put(__half* p, float v) {
+    *reinterpret_cast<uint16_t*>(p) = (uint16_t)f2h_exact(v);
+  }
 };
 
 // Rounding of a float to the input dtype, as torch stores an op result.
@@ -98,7 +96,7 @@ template <>
 __device__ __forceinline__ float to_dtype<uint16_t>(float v) { return bf2f(f2bf(v)); }
 template <>
 __device__ __forceinline__ float to_dtype<__half>(float v) {
-  return __half2float(__float2half_rn(v));
+  return h2f_exact(f2h_exact(v));
 }
 
 // One element of FakeQuantizeFunction.forward (fake_quantize.py:112-115):

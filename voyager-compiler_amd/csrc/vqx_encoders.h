@@ -36,8 +36,7 @@ struct EncIdentity {
 struct EncFp16 {
   static constexpr int kBits = 16;
   __device__ __forceinline__ Result encode(uint32_t h) const {
-    __half v = __float2half_rn(bf2f(h));
-    uint32_t b = f2bf(__half2float(v));
+    uint32_t b = f2bf(h2f_exact(f2h_exact(bf2f(h))));
     return Result{b, b};
   }
 };

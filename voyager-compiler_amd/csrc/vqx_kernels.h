@@ -59,4 +59,8 @@ int codebook_encode(const void* x, int dtype, int64_t rows, int64_t cols, const 
 int codebook_decode(const uint8_t* codes, int64_t rows, int64_t cols, const float* cb, int K, void* out,
                     int dtype, hipStream_t st);
 
+// vqx_nf4_gemm.hip
+int nf4_gemm(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
+             const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, hipStream_t st);
+
 }  // namespace vqx

@@ -67,6 +67,9 @@ _SCHEMAS = {
     "codebook_encode": "codebook_encode(Tensor self, Tensor codebook) -> Tensor",
     "codebook_decode": (
         "codebook_decode(Tensor codes, Tensor codebook, ScalarType dtype=float) -> Tensor"),
+    "linear_nf4": (
+        "linear_nf4(Tensor input, Tensor codes, Tensor scale, Tensor? bias=None, int block_size=64, "
+        'str dtype="nf4") -> Tensor'),
 }
 for _s in _SCHEMAS.values():
     quantized_ops_lib.define(_s)
@@ -536,6 +539,35 @@ def codebook_decode(codes, codebook, dtype=torch.float32):
     return out
 
 
+@_impl("linear_nf4")
+def linear_nf4(input, codes, scale, bias=None, block_size=64, dtype="nf4"):
+    """linear_mx for an NF4 block-64 weight stored packed (quantize_mx_packed
+    with fp32 scales): out = input . decode(codes, scale)^T + bias, the decode
+    fused into the bf16 MFMA product.  input bf16 [..., K]; codes uint8
+    [N * K / 2] or [N, K / 2]; scale fp32 [N, K / 64]."""
+    _lib.require_device(input, "linear_nf4")
+    if block_size != 64:
+        raise ValueError("linear_nf4 is built for 64-element scale blocks")
+    fmt = parse_format(dtype)
+    if not fmt.is_levels or fmt.nlevels != 16:
+        raise ValueError(f"linear_nf4 needs a 16-level NormalFloat format, not {dtype}")
+    if input.dtype != torch.bfloat16:
+        raise ValueError("linear_nf4 takes bfloat16 activations")
+    K = input.shape[-1]
+    x = input.reshape(-1, K).contiguous()
+    M = x.shape[0]
+    N = scale.shape[0]
+    if scale.shape[-1] * 64 != K or codes.numel() * 2 != N * K:
+        raise ValueError("codes / scale shapes do not match the input's K")
+    lv = fmt.tables(x.device)["levels_bf16"]
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    b = None if bias is None else bias.to(device=x.device, dtype=torch.bfloat16).contiguous()
+    _lib.call("vqx_nf4_linear", _lib.ptr(x), _lib.ptr(codes.contiguous()),
+              _lib.ptr(scale.to(torch.float32).contiguous()), _lib.ptr(lv), _lib.ptr(b), _lib.ptr(out),
+              M, N, K, _lib.stream_of(x))
+    return out.reshape(*input.shape[:-1], N)
+
+
 # ---------------------------------------------------------------------------
 # fake (meta) implementations for tracing
 # ---------------------------------------------------------------------------
@@ -610,3 +642,8 @@ def _(input, codebook):
 @torch.library.register_fake("quantized_ops::codebook_decode")
 def _(codes, codebook, dtype=torch.float32):
     return codes.new_empty(codes.shape, dtype=dtype)
+
+
+@torch.library.register_fake("quantized_ops::linear_nf4")
+def _(input, codes, scale, bias=None, block_size=64, dtype="nf4"):
+    return input.new_empty((*input.shape[:-1], scale.shape[0]), dtype=torch.bfloat16)
