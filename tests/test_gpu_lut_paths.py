@@ -35,6 +35,13 @@ def tricky_rows(cols=256):
     r[7, :] = -(2.0**-126)
     r[8, 0] = 1.0
     r[8, 1:] = -(2.0**-10) * torch.rand(cols - 1, generator=g)
+    # huge amax: absmax quotients of the small negatives run from fp32 normals
+    # through fp32 subnormals to zero (sign of the rounded zero)
+    r[9, :] = 0.0
+    r[9, 0] = 2.0**60
+    r[9, 1:60] = -(2.0 ** -torch.arange(70, 129).float())
+    r[9, 64] = 2.0**60
+    r[9, 65:124] = 2.0 ** -torch.arange(70, 129).float()
     return r.to(torch.bfloat16)
 
 
@@ -85,7 +92,12 @@ def test_fake_quant_lut_equals_closed_form(vqx, fmt, dt):
     f = vqx.parse_format(fmt)
     allp = torch.from_numpy(F.bf16_to_f32(F.ALL_BF16))
     g = torch.Generator().manual_seed(9)
-    x = torch.cat([allp, torch.randn(4099, generator=g) * 10]).to(dt).cuda()
+    # fp32 values around the -2^-134 boundary between rounding to -0 and to
+    # the smallest negative bf16 subnormal, and between bf16 neighbours
+    t = 2.0**-134
+    edge = torch.tensor([-t, -t * (1 + 2.0**-20), -t * (1 - 2.0**-20), -2 * t, -1e-45, t * (1 + 2.0**-20),
+                         -1.5 * 2.0**-126, 1.0 + 2.0**-8, -(1.0 + 3 * 2.0**-9), 3.0e38, -3.3e38, 3.39e38])
+    x = torch.cat([allp, torch.randn(4099, generator=g) * 10, edge]).to(dt).cuda()
     for scale in (None, torch.tensor([0.3], device="cuda"), torch.tensor([4.0], device="cuda")):
         outs = []
         for lut in (True, False):

@@ -315,73 +315,139 @@ __device__ __forceinline__ float block_scale_bf16(uint32_t amax, const ScalePara
   }
 }
 
+// Max over the LPB adjacent lanes of a block: DPP quad permutes for lane
+// distances 1 and 2, a shuffle beyond.
+template <int LPB>
+__device__ __forceinline__ uint32_t block_max(uint32_t v) {
+  if constexpr (LPB >= 2) v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  if constexpr (LPB >= 4) v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  if constexpr (LPB >= 8) v = umax32(v, (uint32_t)__shfl_xor((int)v, 4, 64));
+  return v;
+}
+
+// fp32 q within a few ulp of a bf16 rounding midpoint (see div_bf16_fast)
+__device__ __forceinline__ bool near_midpoint(float q) { return (f2u(q) & 0xFFFFu) - 0x7FFCu <= 8u; }
+
+typedef __attribute__((address_space(3))) const uint32_t lds_cu32;
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Power-of-two block scale of a bf16 block (block_scale<uint16_t> mode 0)
+// with the floor(bf16 log2) step thresholds read from an LDS byte table
+// indexed by the exponent field.
+__device__ __forceinline__ float block_scale_pow2_lds(uint32_t amax, int shift, const uint8_t* thr) {
+  uint32_t E = amax >> 7, m = amax & 0x7Fu;
+  int lf = (int)E - 127 + (m >= thr[E] ? 1 : 0);
+  if (E == 0) lf = amax == 0 ? -126 : log2floor_bf16(amax);  // zero or subnormal amax
+  int e = lf - shift;
+  float sc = e > 127 ? __builtin_huge_valf() : (e >= -133 ? exp2i(e) : 1.0f);
+  sc = amax == 0x7F80u ? __builtin_huge_valf() : sc;
+  return amax > 0x7F80u ? 1.0f : sc;
+}
+
 // WANT: bit 0 = reference quantize() values, bit 1 = fake-quant values.
+//
+// Fast path per element: the quotient (one multiply; for absmax scales a
+// reciprocal multiply whose rare near-midpoint cases are redone by IEEE
+// division for the whole group), its magnitude clamped into the table range
+// [T0 - 1, T1] with v_med3_f32 (clamping before the bf16 rounding equals
+// clamping after it, the bounds being bf16 values), one compare against a
+// uniform threshold for the sign, and one LDS read at an address formed from
+// the clamped quotient's bits, giving value and code together.
 template <int CB, int LPB, bool ABSMAX, int WANT>
 __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict__ x, int64_t ngroups,
                                                      ScaleParams sp, LutView lv, MxOut out) {
   extern __shared__ uint32_t lds_lut[];
+  __shared__ uint8_t thr8[256];
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // the first group's loads are in flight while the tables fill LDS
+  u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0};
+  if (g < ngroups) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(x + g * 16);
+    n0 = ld_nt(q);
+    n1 = ld_nt(q + 1);
+  }
+  if constexpr (!ABSMAX)
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) thr8[i] = (uint8_t)log2_step_threshold(i);
   LutLds t = lut_to_lds(lv.blob, lv.len, lds_lut);
   const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
-    uint32_t w[8];
-    {
-      const u32x4* q = reinterpret_cast<const u32x4*>(x + g * 16);
-      u32x4 a0 = ld_nt(q), a1 = ld_nt(q + 1);
-      w[0] = a0.x; w[1] = a0.y; w[2] = a0.z; w[3] = a0.w;
-      w[4] = a1.x; w[5] = a1.y; w[6] = a1.z; w[7] = a1.w;
+  // LDS byte addresses such that entry(h) = base + 4 h for h in [T0 - 1, T1]
+  const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - 4u * t.t0m1;
+  const uint32_t nb = pb + 4u * t.len;
+  const float lo = u2f(t.t0m1 << 16), hi = u2f(t.t1 << 16);
+  for (; g < ngroups; g += stride) {
+    uint32_t w[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+    if (g + stride < ngroups) {  // prefetch the next group
+      const u32x4* q = reinterpret_cast<const u32x4*>(x + (g + stride) * 16);
+      n0 = ld_nt(q);
+      n1 = ld_nt(q + 1);
     }
-    uint32_t m2 = 0;  // two 16-bit magnitude maxima per word
+    u16x2 m2 = {0, 0};  // magnitude maxima of the low and high halves
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      uint32_t a2 = w[j] & 0x7FFF7FFFu;
-      uint32_t lo = umax32(m2 & 0xFFFFu, a2 & 0xFFFFu), hi = umax32(m2 >> 16, a2 >> 16);
-      m2 = lo | (hi << 16);
-    }
-    uint32_t amax = umax32(m2 & 0xFFFFu, m2 >> 16);
-#pragma unroll
-    for (int off = 1; off < LPB; off <<= 1) amax = umax32(amax, (uint32_t)__shfl_xor((int)amax, off, 64));
-    float s = block_scale_bf16<ABSMAX>(amax, sp);
+    for (int j = 0; j < 8; ++j) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, w[j] & 0x7FFF7FFFu));
+    uint32_t amax = block_max<LPB>((uint32_t)(m2.x > m2.y ? m2.x : m2.y));
+    float s;
+    if constexpr (ABSMAX)
+      s = block_scale_bf16<true>(amax, sp);
+    else
+      s = block_scale_pow2_lds(amax, sp.shift, thr8);
     uint32_t sb = f2u(s);
     uint32_t sE = (sb >> 23) & 0xFFu;
+    const float amaxf = u2f(amax << 16);
     bool fast;
-    float rcp, sz;
+    float rcp;
+    uint32_t nthr;  // sign rule: the negative table iff (fp32 bits) > nthr
     if constexpr (!ABSMAX) {
       // a power of two in [2^-100, 2^100]: x / s and v * s are exact
       // scalings (quotients below bf16's normal range only reach the table's
-      // entry 0, as every format here has T0 above it); a quotient keeps its
-      // sign unless it rounds to a bf16 zero, i.e. unless |x| <= 2^-134 s
-      fast = (sb & 0x7FFFFFu) == 0 && sE >= 27 && sE <= 227 && amax < 0x7F80u && t.t0m1 >= 0x80u;
+      // entry 0, as T0 is above it), and the largest quotient stays below S;
+      // a quotient keeps its sign unless it rounds to a bf16 zero, i.e.
+      // unless |x| <= 2^-134 s: compared on x's bits
       rcp = u2f((254u - sE) << 23);
+      fast = (sb & 0x7FFFFFu) == 0 && sE >= 27 && sE <= 227 && amax < 0x7F80u && t.t0m1 >= 0x80u &&
+             (f2u(amaxf * rcp) >> 16) < t.s;
       int ze = (int)sE - 127 - 134;
-      sz = ze >= -149 ? exp2i(ze) : 0.0f;
+      float sz = ze >= -149 ? exp2i(ze) : 0.0f;
+      nthr = t.zsign ? 0x7FFFFFFFu : (0x80000000u | f2u(sz));
     } else {
-      fast = sE >= 2 && sE <= 252 && amax < 0x7F80u;
+      // the quotient q rounds to a bf16 below -0 iff q < -2^-134 (2^-134 is
+      // a midpoint, so q is exact there), or to -0 or below iff q is negative
       rcp = __builtin_amdgcn_rcpf(s);
-      sz = 0.0f;
+      fast = sE >= 2 && sE <= 252 && amax < 0x7F80u && t.t0m1 >= 0x80u &&
+             (f2u(amaxf * rcp) >> 16) + 1u < t.s;
+      nthr = t.zsign ? 0x7FFFFFFFu : 0x80008000u;
     }
-    uint32_t code[16], qv[16], fv[16];
+    uint32_t ent[16];
     if (fast) {
+      if constexpr (!ABSMAX) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
-        float xv = u2f(xb);
-        uint32_t idx;
-        if constexpr (!ABSMAX) {
-          uint32_t qb = f2u(xv * rcp);
-          uint32_t a = (qb >> 16) & 0x7FFFu;
-          uint32_t c = a < t.t0m1 ? t.t0m1 : a;
-          c = c > t.t1 ? t.t1 : c;
-          uint32_t neg = ((__builtin_fabsf(xv) > sz) | t.zsign) ? xb >> 31 : 0u;
-          idx = c - t.t0m1 + neg * t.len;
-        } else {
-          idx = lut_index(t, div_bf16_fast(xv, s, rcp));
+        for (int j = 0; j < 16; ++j) {
+          uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
+          float qc = __builtin_amdgcn_fmed3f(__builtin_fabsf(u2f(xb) * rcp), lo, hi);
+          ent[j] = *(lds_cu32*)(size_t)((xb > nthr ? nb : pb) + (f2u(qc) >> 14));
         }
-        uint32_t e = t.pos[idx];
-        code[j] = e >> 16;
-        uint32_t v = e & 0xFFFFu;
-        if constexpr (WANT & 1) qv[j] = v;
-        if constexpr (WANT & 2) fv[j] = ABSMAX ? f2bf(u2f(v << 16) * s) : (f2u(u2f(v << 16) * s) >> 16);
+      } else {
+        float q[16];
+        bool tie = false;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
+          q[j] = u2f(xb) * rcp;
+          tie |= near_midpoint(q[j]);
+        }
+        if (tie) {  // rare: redo the near-midpoint quotients by IEEE division
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
+            if (near_midpoint(q[j])) q[j] = u2f(xb) / s;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          // clamped magnitudes are normal and finite: hardware RNE is exact
+          uint32_t h = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(q[j]), lo, hi), 0.0f);
+          ent[j] = *(lds_cu32*)(size_t)((f2u(q[j]) > nthr ? nb : pb) + 4u * h);
+        }
       }
     } else {
       // scale 1 (NaN block), Inf, subnormal or extreme: exact division and
@@ -389,17 +455,27 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
 #pragma unroll 1
       for (int j = 0; j < 16; ++j) {
         uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
-        uint32_t h = f2bf(u2f(xb) / s);
-        uint32_t e = full[h];
-        code[j] = e >> 16;
-        uint32_t v = e & 0xFFFFu;
-        qv[j] = v;
-        fv[j] = f2bf(u2f(v << 16) * s);
+        ent[j] = full[f2bf(u2f(xb) / s)];
       }
     }
-    if constexpr (WANT & 1) BT<uint16_t>::store16(static_cast<uint16_t*>(out.qvals) + g * 16, qv);
-    if constexpr (WANT & 2) BT<uint16_t>::store16(static_cast<uint16_t*>(out.fq) + g * 16, fv);
-    if constexpr (CB > 0) store_group_codes<CB>(static_cast<uint8_t*>(out.codes), g, code);
+    if constexpr (WANT != 0) {
+      uint32_t qv[16], fv[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        uint32_t v = ent[j] & 0xFFFFu;
+        qv[j] = v;
+        // pow2 scales on the fast path multiply exactly
+        fv[j] = (ABSMAX || !fast) ? f2bf(u2f(v << 16) * s) : (f2u(u2f(v << 16) * s) >> 16);
+      }
+      if constexpr (WANT & 1) BT<uint16_t>::store16(static_cast<uint16_t*>(out.qvals) + g * 16, qv);
+      if constexpr (WANT & 2) BT<uint16_t>::store16(static_cast<uint16_t*>(out.fq) + g * 16, fv);
+    }
+    if constexpr (CB > 0) {
+      uint32_t code[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) code[j] = ent[j] >> 16;
+      store_group_codes<CB>(static_cast<uint8_t*>(out.codes), g, code);
+    }
     if ((threadIdx.x & (LPB - 1)) == 0) {
       int64_t blk = g / LPB;
       if (out.scale) BT<uint16_t>::put(static_cast<uint16_t*>(out.scale) + blk, f2bf(s));
@@ -409,20 +485,26 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
   }
 }
 
+template <int CB, int LPB, bool ABSMAX, int WANT>
+static int launch_lut_k(const uint16_t* x, int64_t ngroups, const ScaleParams& sp, const LutView& lv,
+                        const MxOut& out, hipStream_t st) {
+  const int bs = 256;
+  size_t lds = sizeof(uint32_t) * 2 * lv.len;
+  auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT>;
+  unsigned grid = persistent_grid((const void*)k, bs, lds, ngroups);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out);
+  return check_launch("mx_quantize(lut)");
+}
+
 template <int CB, int LPB, bool ABSMAX>
 static int launch_lut_want(const uint16_t* x, int64_t ngroups, const ScaleParams& sp, const LutView& lv,
                            const MxOut& out, hipStream_t st) {
-  const int bs = 256;
-  unsigned grid = grid_for(ngroups, bs);
-  size_t lds = sizeof(uint32_t) * 2 * lv.len;
-  int want = (out.qvals ? 1 : 0) | (out.fq ? 2 : 0);
-  switch (want) {
-    case 0: hipLaunchKernelGGL((mx_lut_kernel<CB, LPB, ABSMAX, 0>), dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out); break;
-    case 1: hipLaunchKernelGGL((mx_lut_kernel<CB, LPB, ABSMAX, 1>), dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out); break;
-    case 2: hipLaunchKernelGGL((mx_lut_kernel<CB, LPB, ABSMAX, 2>), dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out); break;
-    default: hipLaunchKernelGGL((mx_lut_kernel<CB, LPB, ABSMAX, 3>), dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out); break;
+  switch ((out.qvals ? 1 : 0) | (out.fq ? 2 : 0)) {
+    case 0: return launch_lut_k<CB, LPB, ABSMAX, 0>(x, ngroups, sp, lv, out, st);
+    case 1: return launch_lut_k<CB, LPB, ABSMAX, 1>(x, ngroups, sp, lv, out, st);
+    case 2: return launch_lut_k<CB, LPB, ABSMAX, 2>(x, ngroups, sp, lv, out, st);
+    default: return launch_lut_k<CB, LPB, ABSMAX, 3>(x, ngroups, sp, lv, out, st);
   }
-  return check_launch("mx_quantize(lut)");
 }
 
 template <int CB, bool ABSMAX>

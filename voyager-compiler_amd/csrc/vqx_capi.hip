@@ -38,6 +38,35 @@ int num_cus() {
   return cached_cus;
 }
 
+unsigned persistent_grid(const void* kernel, int block, size_t lds_bytes, int64_t work_items) {
+  // occupancy by (kernel, block, LDS), cached per thread and device
+  struct Entry {
+    const void* k;
+    int block, dev;
+    size_t lds;
+    int per_cu;
+  };
+  static thread_local Entry cache[32];
+  static thread_local int used = 0;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  int per_cu = 0;
+  for (int i = 0; i < used; ++i)
+    if (cache[i].k == kernel && cache[i].block == block && cache[i].lds == lds_bytes && cache[i].dev == dev)
+      per_cu = cache[i].per_cu;
+  if (per_cu == 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds_bytes) != hipSuccess ||
+        per_cu <= 0)
+      per_cu = 1;
+    Entry e{kernel, block, dev, lds_bytes, per_cu};
+    cache[used < 32 ? used++ : 31] = e;
+  }
+  int64_t need = (work_items + block - 1) / block;
+  int64_t cap = (int64_t)num_cus() * per_cu;
+  if (need < 1) need = 1;
+  return (unsigned)(need < cap ? need : cap);
+}
+
 static int to_desc(const vqx_format* f, FormatDesc* d) {
   if (!f) return set_error(kErrInvalid, "format descriptor is NULL");
   d->kind = f->kind;

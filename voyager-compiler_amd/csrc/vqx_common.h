@@ -56,6 +56,15 @@ __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) {
 // Round-to-nearest-even fp32 -> bf16 pattern, every NaN to 0x7FC0.
 __device__ __forceinline__ uint32_t f2bf_dev(float f) { return f2bf(f); }
 
+// Two fp32 -> bf16 (RNE, v_cvt_pk_bf16_f32), a in the low half.  Matches
+// f2bf for every non-NaN input.
+typedef __bf16 vqx_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float vqx_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  vqx_f32x2 f = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, vqx_bf16x2));
+}
+
 // Exact fp16 <-> fp32 conversions in integer arithmetic (subnormals and signed
 // zeros kept, round to nearest even), independent of the device's fp16
 // denormal mode; torch's CPU conversions are the reference.
@@ -91,6 +100,11 @@ inline unsigned grid_for(int64_t work_items, int per_block, int max_per_cu = 8) 
   if (need < 1) need = 1;
   return (unsigned)(need < cap ? need : cap);
 }
+
+// Persistent launch: as many workgroups as fit on the device at once (from
+// the kernel's register use and the dynamic LDS size), no more than the work
+// needs; the kernels loop grid-stride.
+unsigned persistent_grid(const void* kernel, int block, size_t lds_bytes, int64_t work_items);
 
 inline bool aligned(const void* p, unsigned a) {
   return ((uintptr_t)p & (a - 1)) == 0;

@@ -177,34 +177,72 @@ __global__ __launch_bounds__(256) void fq_vec_kernel(const T* __restrict__ x, T*
 
 // Table path of the per-tensor fake-quant: the format comes from the
 // compact LDS table (magnitudes >= S from the full table in global memory).
+typedef __attribute__((address_space(3))) const uint32_t lds_cu32;
+
+// Unit scale, per group of 8: when no magnitude reaches the table's special
+// threshold S, each element is its magnitude clamped into [T0 - 1, T1] with
+// v_med3_f32 (clamping before the bf16 rounding equals clamping after it, the
+// bounds being bf16 values), RNE to bf16, one compare against a uniform
+// threshold for the sign, and one LDS read giving value and code together.
+// Other groups, and every group under a non-unit scale, take the exact
+// per-element route (IEEE division, full table beyond S).
 template <typename T, int CB>
 __global__ __launch_bounds__(256) void fq_lut_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                      void* __restrict__ codes, int64_t n,
                                                      const float* __restrict__ scale, bool mul, LutView lv) {
   extern __shared__ uint32_t lds_lut[];
+  constexpr bool kBf16 = std::is_same<T, uint16_t>::value;
+  const int64_t nvec = n / 8;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  float nxt[8];
+  if (g < nvec) IO<T>::load(x + g * 8, nxt);  // in flight while the table fills LDS
   LutLds t = lut_to_lds(lv.blob, lv.len, lds_lut);
   const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
-  constexpr bool kBf16 = std::is_same<T, uint16_t>::value;
+  // LDS byte addresses such that entry(h) = base + 4 h for h in [T0 - 1, T1]
+  const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - 4u * t.t0m1;
+  const uint32_t nb = pb + 4u * t.len;
+  const float lo = u2f(t.t0m1 << 16), hi = u2f(t.t1 << 16);
+  const uint32_t big = (t.s - 1u) << 16;  // magnitudes (fp32 bits) from here: exact route
+  // x rounds to a bf16 below -0 iff x < -2^-134, to -0 or below iff x < 0
+  const uint32_t nthr = t.zsign ? 0x7FFFFFFFu : 0x80008000u;
   float s = scale ? scale[0] : 1.0f;
   s = to_dtype<T>(s);
   const bool unit = s == 1.0f;
-  const int64_t nvec = n / 8;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < nvec; g += stride) {
+  // a normal lower bound keeps the clamp and the rounding free of subnormals
+  const bool clamp_ok = unit && t.t0m1 >= 0x80u;
+  for (; g < nvec; g += stride) {
     float v[8];
     uint32_t c[8];
-    IO<T>::load(x + g * 8, v);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      uint32_t h;
-      if (unit)
-        h = kBf16 ? (f2u(v[j]) >> 16) : f2bf(v[j]);
-      else
-        h = f2bf(to_dtype<T>(v[j] / s));
-      uint32_t e = (h & 0x7FFFu) < t.s ? lut_entry(t, h) : full[h];
-      c[j] = e >> 16;
-      float q = u2f(e << 16);
-      v[j] = unit ? (kBf16 ? q : to_dtype<T>(q)) : (mul ? to_dtype<T>(to_dtype<T>(q) * s) : to_dtype<T>(q));
+    for (int j = 0; j < 8; ++j) v[j] = nxt[j];
+    if (g + stride < nvec) IO<T>::load(x + (g + stride) * 8, nxt);
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = umax32(m, f2u(v[j]) & 0x7FFFFFFFu);
+    if (clamp_ok && m < big) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float qc = __builtin_amdgcn_fmed3f(__builtin_fabsf(v[j]), lo, hi);
+        uint32_t h = kBf16 ? f2u(qc) >> 16 : pack_bf16x2(qc, 0.0f);
+        uint32_t e = *(lds_cu32*)(size_t)((f2u(v[j]) > nthr ? nb : pb) + 4u * h);
+        c[j] = e >> 16;
+        float q = u2f(e << 16);
+        v[j] = kBf16 ? q : to_dtype<T>(q);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t h;
+        if (unit)
+          h = kBf16 ? (f2u(v[j]) >> 16) : f2bf(v[j]);
+        else
+          h = f2bf(to_dtype<T>(v[j] / s));
+        uint32_t e = (h & 0x7FFFu) < t.s ? lut_entry(t, h) : full[h];
+        c[j] = e >> 16;
+        float q = u2f(e << 16);
+        v[j] = unit ? (kBf16 ? q : to_dtype<T>(q)) : (mul ? to_dtype<T>(to_dtype<T>(q) * s) : to_dtype<T>(q));
+      }
     }
     if (y) IO<T>::store(y + g * 8, v);
     if constexpr (CB > 0) store_codes8<CB>(codes, g * 8, c);
@@ -286,12 +324,16 @@ static int launch_fq_dtype(const void* x, int dtype, void* y, void* codes, int c
 template <typename T>
 static int launch_fq_lut(const T* x, T* y, void* codes, int code_bytes, int64_t n, const float* scale, bool mul,
                          const LutView& lv, hipStream_t st) {
-  unsigned grid = grid_for(n / 8 + 1, 256);
   size_t lds = sizeof(uint32_t) * 2 * lv.len;
-  if (code_bytes == 0)
-    hipLaunchKernelGGL((fq_lut_kernel<T, 0>), dim3(grid), dim3(256), lds, st, x, y, codes, n, scale, mul, lv);
-  else
-    hipLaunchKernelGGL((fq_lut_kernel<T, 1>), dim3(grid), dim3(256), lds, st, x, y, codes, n, scale, mul, lv);
+  if (code_bytes == 0) {
+    auto k = fq_lut_kernel<T, 0>;
+    unsigned grid = persistent_grid((const void*)k, 256, lds, n / 8 + 1);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, st, x, y, codes, n, scale, mul, lv);
+  } else {
+    auto k = fq_lut_kernel<T, 1>;
+    unsigned grid = persistent_grid((const void*)k, 256, lds, n / 8 + 1);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, st, x, y, codes, n, scale, mul, lv);
+  }
   return check_launch("fake_quant(lut)");
 }
 
@@ -571,11 +613,16 @@ __device__ __forceinline__ uint32_t key_bits(uint32_t key) {
 }
 
 // first[c] = least (order key of a) bf16 value whose index is c.
-__global__ __launch_bounds__(256) void level_first_kernel(const uint8_t* idx, uint32_t* first) {
+__global__ __launch_bounds__(256) void level_first_kernel(const uint8_t* idx, uint32_t* first, int K) {
+  // per-workgroup minima in LDS first, then one global atomic per level
+  __shared__ uint32_t lmin[256];
+  for (int k = threadIdx.x; k < K; k += blockDim.x) lmin[k] = 0xFFFFFFFFu;
+  __syncthreads();
   uint32_t h = blockIdx.x * blockDim.x + threadIdx.x;
-  if (h >= 65536u) return;
-  if ((h & 0x7FFFu) > 0x7F80u) return;  // NaN
-  atomicMin(&first[idx[h]], order_key(h << 16));
+  if (h < 65536u && (h & 0x7FFFu) <= 0x7F80u) atomicMin(&lmin[idx[h]], order_key(h << 16));
+  __syncthreads();
+  for (int k = threadIdx.x; k < K; k += blockDim.x)
+    if (lmin[k] != 0xFFFFFFFFu) atomicMin(&first[k], lmin[k]);
 }
 
 // boundaries[j-1] = min_{c >= j} first[c]  (suffix minimum), as fp32 values.
@@ -606,7 +653,7 @@ int level_tables(const float* levels, int K, int mode, uint8_t* index_table, flo
   if (hipMemsetAsync(work, 0xFF, sizeof(uint32_t) * K, st) != hipSuccess ||
       hipMemsetAsync(bad, 0, sizeof(int), st) != hipSuccess)
     return set_error(kErrLaunch, "hipMemsetAsync failed");
-  hipLaunchKernelGGL(level_first_kernel, dim3(256), dim3(256), 0, st, index_table, work);
+  hipLaunchKernelGGL(level_first_kernel, dim3(256), dim3(256), 0, st, index_table, work, K);
   hipLaunchKernelGGL(level_boundary_kernel, dim3(1), dim3(64), 0, st, work, K, boundaries);
   hipLaunchKernelGGL(level_verify_kernel, dim3(256), dim3(256), 0, st, index_table, boundaries, K, bad);
   return check_launch("level_tables");

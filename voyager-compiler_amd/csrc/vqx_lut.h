@@ -30,7 +30,7 @@ enum LutHeader : int {
   kLutHeaderWords = 16,
 };
 
-constexpr int kLutMaxLen = 8192;  // entries per sign
+constexpr int kLutMaxLen = 8192;  // entries per sign (64 KiB of LDS for both signs)
 // full table scratch (65536 entries) + header + two signed tables
 constexpr int64_t kLutBytes = (int64_t)(kLutHeaderWords + 2 * kLutMaxLen + 65536) * 4;
 
