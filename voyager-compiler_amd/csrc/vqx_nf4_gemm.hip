@@ -4,19 +4,22 @@
 // 319-326, fused into the product of :330-331).  bf16 MFMA
 // (v_mfma_f32_32x32x16_bf16), fp32 accumulation, bf16 output.
 //
-// Tiling: a workgroup of 256 threads (4 waves) computes a 256 x 128 tile of
-// out; wave w owns rows 64w .. 64w+63 and all 128 columns (2 x 4 MFMA tiles of
-// 32 x 32).  The K loop steps by 64 (one NF4 scale block).
-//  * A never touches LDS: each wave's rows are private to it, so its MFMA
-//    operands are loaded straight from global memory (one 16-byte load per
-//    lane per fragment), one k-step ahead in registers.
-//  * W is decoded once per workgroup into LDS (128 x 64 bf16 = 16 KiB per
-//    step, 16-byte chunks XOR-swizzled by row): each thread turns 32 codes per
-//    step into bf16 with a v_perm byte-table lookup of the levels, the fp32
-//    product with the block scale and RNE.  A ring of three LDS buffers lets
-//    the decode run two k-steps ahead of the MFMAs, so one barrier per step
-//    suffices and the next step's first fragments are already in registers
-//    when it starts.
+// Tiling: a workgroup of 512 threads (8 waves, two per SIMD) computes a
+// 256 x 128 tile of out; wave w owns the 64 x 64 block at rows 64 (w >> 1),
+// columns 64 (w & 1) (2 x 2 MFMA tiles of 32 x 32).  The K loop steps by 64
+// (one NF4 scale block) and is unrolled by 3 so every ring index below is
+// static.  Two waves per SIMD let one wave's decode VALU and memory
+// instructions issue while the other's MFMAs run.
+//  * A: a ring of three LDS stages filled two steps ahead of use: fully
+//    coalesced 16-byte loads (8 lanes per 128-byte row; wave w loads rows
+//    32 w .. 32 w + 31) into registers, written in the swizzled layout one
+//    step after the load.
+//  * W: decoded once per workgroup into a ring of three LDS buffers two
+//    steps ahead (128 x 64 bf16 per step; each thread 16 codes: v_perm
+//    byte-table lookup of the levels, fp32 product with the block scale,
+//    RNE).  One barrier per step publishes both rings.
+//  * Fragments of both operands are read from LDS one 16-deep k slice ahead
+//    of their MFMAs (16-byte chunks XOR-swizzled by row: conflict-free).
 //  * The MFMA takes the W fragment as its first operand, so each lane ends
 //    with four consecutive output columns per group: 8-byte stores.
 // Workgroups are ordered so each XCD runs whole 256-row slabs of A, which stay
@@ -33,12 +36,20 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBM = 256, kBN = 128, kBK = 64;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kWTile = kBN * kBK * 2;  // decoded W bytes per k-step
-constexpr int kWBufs = 3;
+constexpr int kATile = kBM * kBK * 2;  // A bytes per k-step
 
-// byte offset of 16-byte chunk c (0..7) of row r in a [rows][64] bf16 tile
-__device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) { return r * 128u + ((c ^ (r & 7u)) << 4); }
+// byte offset of 16-byte chunk c (0..7) of row r in a [rows][64] bf16 tile.
+// The chunk slot is c ^ (r & 7) ^ ((r >> 3) & 1): for a fixed c, any 8
+// aligned consecutive rows use 8 different slots (distinct 16-byte bank
+// groups within 128 bytes) and any 16 aligned consecutive rows use 16
+// different (row parity, slot) pairs (distinct bank groups within 256 bytes),
+// so a fragment read of 32 consecutive rows is conflict free whether LDS
+// serves 8 lanes over 32 banks or 16 lanes over 64 banks per cycle.
+__device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) {
+  return r * 128u + ((c ^ (r & 7u) ^ ((r >> 3) & 1u)) << 4);
+}
 
 // Decode 8 codes (one dword: byte i holds codes 2i (low nibble), 2i+1) into
 // four bf16 pairs in k order.  hl/hh: level high bytes for codes 0-7 / 8-15
@@ -48,11 +59,10 @@ struct LevelBytes {
   uint32_t l0, l1, l2, l3;  // low bytes
 };
 
-__device__ __forceinline__ void lookup4(uint32_t nib, const LevelBytes& lb, uint32_t& hi, uint32_t& lo) {
-  // nib: four 4-bit codes, one per byte.  v_perm picks bytes 0-7 of a pair of
-  // dwords; the code's bit 3 chooses between the 0-7 and 8-15 tables.
-  uint32_t sel = nib & 0x07070707u;
-  uint32_t m = ((nib >> 3) & 0x01010101u) * 0xFFu;
+__device__ __forceinline__ void lookup4(uint32_t sel, uint32_t m, const LevelBytes& lb, uint32_t& hi, uint32_t& lo) {
+  // sel: four 3-bit code bits 0-2, one per byte; m: 0xFF in the bytes whose
+  // code has bit 3 set.  v_perm picks bytes 0-7 of a pair of dwords; m
+  // chooses between the tables of codes 0-7 and 8-15.
   uint32_t ha = __builtin_amdgcn_perm(lb.h1, lb.h0, sel);
   uint32_t hb = __builtin_amdgcn_perm(lb.h3, lb.h2, sel);
   uint32_t la = __builtin_amdgcn_perm(lb.l1, lb.l0, sel);
@@ -61,11 +71,20 @@ __device__ __forceinline__ void lookup4(uint32_t nib, const LevelBytes& lb, uint
   lo = (lbb & m) | (la & ~m);
 }
 
+// Byte masks of bit 7 of each byte of y: v_perm selectors 8, 9, 10, 11
+// replicate the sign bit of bytes 1, 3, 5, 7 of the pair {y, y << 8}, i.e.
+// of bytes 0, 2, 1, 3 of y.
+__device__ __forceinline__ uint32_t byte_sign_mask(uint32_t y) {
+  return __builtin_amdgcn_perm(y, y << 8, 0x0B090A08u);
+}
+
 // 8 codes -> 4 dwords of bf16 pairs = bf16(level * s), k ascending.
 __device__ __forceinline__ void decode8(uint32_t w, float s, const LevelBytes& lb, uint32_t (&out)[4]) {
+  // byte b of w holds codes 2b (low nibble) and 2b + 1 (high nibble); bit 3
+  // of the even codes moves to bit 7 with w << 4, the odd ones' is there
   uint32_t he, le, ho, lo;
-  lookup4(w & 0x0F0F0F0Fu, lb, he, le);         // even k: codes 0, 2, 4, 6
-  lookup4((w >> 4) & 0x0F0F0F0Fu, lb, ho, lo);  // odd k:  codes 1, 3, 5, 7
+  lookup4(w & 0x07070707u, byte_sign_mask(w << 4), lb, he, le);         // even k: codes 0, 2, 4, 6
+  lookup4((w >> 4) & 0x07070707u, byte_sign_mask(w), lb, ho, lo);       // odd k:  codes 1, 3, 5, 7
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     // fp32 of the levels: level bf16 in the high half
@@ -90,10 +109,13 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
                                                              const uint16_t* __restrict__ levels,
                                                              const uint16_t* __restrict__ bias,
                                                              uint16_t* __restrict__ out, int M, int N, int K) {
-  __shared__ __attribute__((aligned(16))) uint8_t wl[kWBufs * kWTile];
+  __shared__ __attribute__((aligned(16))) uint8_t wl[3 * kWTile];
+  __shared__ __attribute__((aligned(16))) uint8_t al[3 * kATile];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int wm = wave >> 1;  // 64-row block
+  const int wn = wave & 1;   // 64-column block
   const int lr = lane & 31;  // fragment row within a 32-tile
   const int lk = lane >> 5;  // which 8-wide k group
 
@@ -127,145 +149,178 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
   const int nk = K / kBK;
   const int kb = K / 64;  // scale blocks per row
 
-  // A fragment (i, kk) of a step: lane (lr, lk) holds
-  // A[m0 + 64 wave + 32 i + lr][64 ks + 16 kk + 8 lk .. +8]; stored as a[2 kk + i].
-  const uint16_t* ap = A + (size_t)(m0 + wave * 64 + lr) * K + lk * 8;
-  const size_t a32 = (size_t)32 * K;
-  // W decode assignment: row wr, codes for k 32 wh .. 32 wh + 31 of a step
-  const int wr = tid >> 1, wh = tid & 1;
-  const uint8_t* wsrc = codes + (size_t)(n0 + wr) * (K / 2) + wh * 16;
+  // A staging: load q (0..3) of a step covers rows 32 wave + 8 q .. +7, lane
+  // L chunk L % 8 of row 32 wave + 8 q + L / 8
+  const uint16_t* asrc = A + (size_t)(m0 + wave * 32 + (lane >> 3)) * K + (lane & 7) * 8;
+  u32x4 areg[4];
+  auto load_a = [&](int ks) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      areg[q] = *reinterpret_cast<const u32x4*>(asrc + (size_t)(8 * q) * K + (size_t)ks * kBK);
+  };
+  auto store_a = [&](uint32_t stage) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<u32x4*>(al + stage + swz(wave * 32 + 8 * q + (lane >> 3), lane & 7)) = areg[q];
+  };
+  // W decode assignment: row wr, codes for k 16 wq .. 16 wq + 15 of a step
+  const int wr = tid >> 2, wq = tid & 3;
+  const uint8_t* wsrc = codes + (size_t)(n0 + wr) * (K / 2) + wq * 8;
   const float* ssrc = scale + (size_t)(n0 + wr) * kb;
 
-  auto load_a = [&](u32x4(&a)[8], int ks) {
-    const uint16_t* p = ap + (size_t)ks * kBK;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      a[2 * kk] = *reinterpret_cast<const u32x4*>(p + kk * 16);
-      a[2 * kk + 1] = *reinterpret_cast<const u32x4*>(p + a32 + kk * 16);
-    }
-  };
   auto decode_store = [&](uint32_t base, uint32_t w, float s, int j) {
     uint32_t o[4];
     decode8(w, s, lb, o);
     u32x4 v = {o[0], o[1], o[2], o[3]};
-    *reinterpret_cast<u32x4*>(wl + base + swz(wr, wh * 4 + j)) = v;
+    *reinterpret_cast<u32x4*>(wl + base + swz(wr, wq * 2 + j)) = v;
   };
-  auto read_b = [&](bf16x8(&b)[4], uint32_t base, int kk) {
+  auto read_b = [&](bf16x8(&b)[2], uint32_t base, int kk) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      b[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(wl + base + swz(j * 32 + lr, kk * 2 + lk)));
+    for (int j = 0; j < 2; ++j)
+      b[j] = __builtin_bit_cast(bf16x8,
+                                *reinterpret_cast<const u32x4*>(wl + base + swz(wn * 64 + j * 32 + lr, kk * 2 + lk)));
+  };
+  auto read_a = [&](bf16x8(&a)[2], uint32_t base, int kk) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      a[i] = __builtin_bit_cast(bf16x8,
+                                *reinterpret_cast<const u32x4*>(al + base + swz(wm * 64 + i * 32 + lr, kk * 2 + lk)));
   };
 
-  f32x16 acc[2][4];
+  f32x16 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  auto mma = [&](const bf16x8(&b)[4], const u32x4(&a)[8], int kk) {
-    bf16x8 a0 = __builtin_bit_cast(bf16x8, a[2 * kk]);
-    bf16x8 a1 = __builtin_bit_cast(bf16x8, a[2 * kk + 1]);
+  auto mma = [&](const bf16x8(&b)[2], const bf16x8(&a)[2]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[j], a0, acc[0][j], 0, 0, 0);
-      acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[j], a1, acc[1][j], 0, 0, 0);
+    for (int j = 0; j < 2; ++j) {
+      acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[j], a[0], acc[0][j], 0, 0, 0);
+      acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b[j], a[1], acc[1][j], 0, 0, 0);
     }
   };
 
-  // codes in flight: wc/ws hold the codes of step ks + 2 while step ks runs
-  u32x4 wc;
-  float ws;
-  // prologue: W of steps 0 and 1 decoded into buffers 0 and 1, A of step 0
-  // and the codes of step 2 in flight, fragments of step 0, kk 0 read
-  u32x4 a0[8], a1[8];
-  bf16x8 bA[4], bB[4];
-  load_a(a0, 0);
+  // codes in flight, one slot per step mod 3: step ks decodes the codes of
+  // step ks + 2 from its slot and, once they are consumed, reloads the slot
+  // with those of step ks + 5 (no register copies, so no early waits)
+  u32x2 wc0 = {0, 0}, wc1 = {0, 0}, wc2 = {0, 0};
+  float ws0 = 0.0f, ws1 = 0.0f, ws2 = 0.0f;
+  auto load_codes = [&](u32x2& c, float& sc, int ks) {
+    c = *reinterpret_cast<const u32x2*>(wsrc + (size_t)ks * (kBK / 2));
+    sc = ssrc[ks];
+  };
+
+  // prologue: A of steps 0 and 1 staged and of step 2 in registers, W of
+  // steps 0 and 1 decoded, the codes of steps 2..4 in flight, fragments of
+  // step 0, first slice, read
+  load_a(0);
+  store_a(0);
+  if (nk > 1) {
+    load_a(1);
+    store_a(kATile);
+  }
+  if (nk > 2) load_a(2);
   {
-    u32x4 c0 = *reinterpret_cast<const u32x4*>(wsrc);
-    float s0 = ssrc[0];
-    u32x4 c1 = c0;
-    float s1 = s0;
-    if (nk > 1) {
-      c1 = *reinterpret_cast<const u32x4*>(wsrc + kBK / 2);
-      s1 = ssrc[1];
-    }
-    if (nk > 2) {
-      wc = *reinterpret_cast<const u32x4*>(wsrc + 2 * (kBK / 2));
-      ws = ssrc[2];
-    }
+    u32x2 c0, c1 = {0, 0};
+    float s0, s1 = 0.0f;
+    load_codes(c0, s0, 0);
+    if (nk > 1) load_codes(c1, s1, 1);
+    if (nk > 2) load_codes(wc0, ws0, 2);
+    if (nk > 3) load_codes(wc1, ws1, 3);
+    if (nk > 4) load_codes(wc2, ws2, 4);
     decode_store(0, c0.x, s0, 0);
     decode_store(0, c0.y, s0, 1);
-    decode_store(0, c0.z, s0, 2);
-    decode_store(0, c0.w, s0, 3);
     if (nk > 1) {
       decode_store(kWTile, c1.x, s1, 0);
       decode_store(kWTile, c1.y, s1, 1);
-      decode_store(kWTile, c1.z, s1, 2);
-      decode_store(kWTile, c1.w, s1, 3);
     }
   }
   lds_barrier();
+  bf16x8 bA[2], bB[2], aA[2], aB[2];
   read_b(bA, 0, 0);
+  read_a(aA, 0, 0);
 
-  // One k-step.  On entry bA holds the kk 0 fragments of step ks and acur its
-  // A fragments; on exit bA holds the kk 0 fragments of step ks + 1 and anxt
-  // its A fragments.  full: ks + 3 < nk, so every prefetch and decode is live
-  // and the step compiles without branches.
-  auto step = [&](auto full, int ks, int buf, const u32x4(&acur)[8], u32x4(&anxt)[8]) {
+  // One k-step; T = ks % 3 selects the ring slots.  On entry bA/aA hold the
+  // kk 0 fragments of step ks; on exit those of step ks + 1.  full:
+  // ks + 5 < nk, so every prefetch and decode is live and the step compiles
+  // without branches.
+  //
+  // Issue order: each kk first sends the LDS reads of the next kk's
+  // fragments, then a scheduling fence, then its 4 MFMAs alternating with
+  // the VALU of the decode (kk 0 and 2) or the A staging (kk 1) or the code
+  // loads (kk 3); the fences keep the compiler from sinking the fragment
+  // reads next to their MFMAs.
+  auto step = [&](auto full, auto tt, int ks, u32x2& wc, float& ws) {
     constexpr bool kFull = decltype(full)::value;
-    const uint32_t cur = buf * kWTile;
-    const uint32_t nxt = (buf == kWBufs - 1 ? 0 : buf + 1) * kWTile;
-    const uint32_t dec = (buf == 0 ? kWBufs - 1 : buf - 1) * kWTile;  // (ks + 2) % 3
+    constexpr int T = decltype(tt)::value;
+    constexpr uint32_t a_cur = T * kATile, a_nxt = ((T + 1) % 3) * kATile, a_new = ((T + 2) % 3) * kATile;
+    constexpr uint32_t w_cur = T * kWTile, w_nxt = ((T + 1) % 3) * kWTile, w_new = ((T + 2) % 3) * kWTile;
     const bool more = kFull || ks + 1 < nk;
-    const bool do_dec = kFull || ks + 2 < nk;
-    if (more) load_a(anxt, ks + 1);
-    const uint32_t w0 = wc.x, w1 = wc.y, w2 = wc.z, w3 = wc.w;
+    const bool ahead2 = kFull || ks + 2 < nk;
+    const uint32_t w0 = wc.x, w1 = wc.y;
     const float s = ws;
-    if (kFull || ks + 3 < nk) {
-      wc = *reinterpret_cast<const u32x4*>(wsrc + (size_t)(ks + 3) * (kBK / 2));
-      ws = ssrc[ks + 3];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      bf16x8(&bcur)[2] = (kk & 1) ? bB : bA;
+      bf16x8(&bnext)[2] = (kk & 1) ? bA : bB;
+      bf16x8(&acur)[2] = (kk & 1) ? aB : aA;
+      bf16x8(&anext)[2] = (kk & 1) ? aA : aB;
+      if (kk < 3) {
+        read_b(bnext, w_cur, kk + 1);
+        read_a(anext, a_cur, kk + 1);
+      } else if (more) {
+        read_b(bnext, w_nxt, 0);
+        read_a(anext, a_nxt, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (kk == 0 && ahead2) decode_store(w_new, w0, s, 0);
+      if (kk == 2 && ahead2) decode_store(w_new, w1, s, 1);
+      mma(bcur, acur);
+      if (kk == 1) {
+        if (ahead2) store_a(a_new);  // A of step ks + 2, loaded during step ks - 1
+        __builtin_amdgcn_sched_barrier(0);
+        if (kFull || ks + 3 < nk) load_a(ks + 3);
+      }
+      if (kk == 3 && (kFull || ks + 5 < nk)) load_codes(wc, ws, ks + 5);
+      if constexpr (kFull) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    read_b(bB, cur, 1);
-    if (do_dec) decode_store(dec, w0, s, 0);
-    mma(bA, acur, 0);
-    read_b(bA, cur, 2);
-    if (do_dec) decode_store(dec, w1, s, 1);
-    mma(bB, acur, 1);
-    read_b(bB, cur, 3);
-    if (do_dec) decode_store(dec, w2, s, 2);
-    mma(bA, acur, 2);
-    if (more) read_b(bA, nxt, 0);
-    if (do_dec) decode_store(dec, w3, s, 3);
-    mma(bB, acur, 3);
     lds_barrier();
   };
   const std::integral_constant<bool, true> kAll;
   const std::integral_constant<bool, false> kChecked;
+  const std::integral_constant<int, 0> k0;
+  const std::integral_constant<int, 1> k1;
+  const std::integral_constant<int, 2> k2;
 
-  int buf = 0;
   int ks = 0;
-  for (; ks + 4 < nk; ks += 2) {
-    step(kAll, ks, buf, a0, a1);
-    buf = buf == kWBufs - 1 ? 0 : buf + 1;
-    step(kAll, ks + 1, buf, a1, a0);
-    buf = buf == kWBufs - 1 ? 0 : buf + 1;
+  for (; ks + 7 < nk; ks += 3) {
+    step(kAll, k0, ks, wc0, ws0);
+    step(kAll, k1, ks + 1, wc1, ws1);
+    step(kAll, k2, ks + 2, wc2, ws2);
   }
-  for (; ks < nk; ks += 2) {
-    step(kChecked, ks, buf, a0, a1);
-    buf = buf == kWBufs - 1 ? 0 : buf + 1;
-    if (ks + 1 < nk) step(kChecked, ks + 1, buf, a1, a0);
-    buf = buf == kWBufs - 1 ? 0 : buf + 1;
+  for (; ks < nk; ks += 3) {
+    step(kChecked, k0, ks, wc0, ws0);
+    if (ks + 1 < nk) step(kChecked, k1, ks + 1, wc1, ws1);
+    if (ks + 2 < nk) step(kChecked, k2, ks + 2, wc2, ws2);
   }
 
   // epilogue: lane holds output row m = lr of each A fragment and columns
   // 8 g + 4 lk .. +3 (g = 0..3) of each W fragment, in acc[i][j][4 g .. 4 g + 3]
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < 2; ++j) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int n = n0 + j * 32 + 8 * g + 4 * lk;
+      const int n = n0 + wn * 64 + j * 32 + 8 * g + 4 * lk;
       float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
       if (bias) {
         u32x2 bb = *reinterpret_cast<const u32x2*>(bias + n);
@@ -276,7 +331,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int m = m0 + wave * 64 + i * 32 + lr;
+        const int m = m0 + wm * 64 + i * 32 + lr;
         u32x2 o = {pack_bf16x2(acc[i][j][4 * g] + b0, acc[i][j][4 * g + 1] + b1),
                    pack_bf16x2(acc[i][j][4 * g + 2] + b2, acc[i][j][4 * g + 3] + b3)};
         *reinterpret_cast<u32x2*>(out + (size_t)m * N + n) = o;
