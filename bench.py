@@ -5,11 +5,15 @@
 A step is one pass of a hot-path kernel over one batch of synthetic, seeded
 input already resident in HBM.  The headline (``value``) is BASELINE.json
 NF4 block-64 encode of a bf16 4096x11008 weight (C2), in
-quantized elements per second; every other config is reported in
-``configs``.  Kernel time is measured with HIP events on the launch stream
-(the kernels launch on torch's current stream, so torch.cuda.Event sees
-them).  ``cpu_baseline`` times the CPU oracle (a restatement of the
-reference's PyTorch CPU path) on this host's cores.
+quantized elements per second over the whole timed region (K back-to-back
+launches between two synchronisations); every other config is reported in
+``configs``.  ``roofline.achieved`` divides the algorithmic bytes of a launch
+by the kernel's average launch duration, from HIP events around each launch
+on the launch stream (the kernels launch on torch's current stream, so
+torch.cuda.Event sees them); ``roofline.traffic`` is the HBM bytes per launch
+measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/
+hbm_traffic.json).  ``cpu_baseline`` times the CPU oracle (a restatement of
+the reference's PyTorch CPU path) on this host's cores.
 """
 
 import argparse
@@ -35,6 +39,9 @@ def parse():
     ap.add_argument("--only", default=None, help="comma list of config keys to run")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain device-to-device copy of 512 MiB (5 times), the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     return ap.parse_args()
 
 
@@ -205,25 +212,31 @@ HEADLINE = "c2"
 
 
 def time_config(torch, launch, steps, warmup):
+    """Warm up, then time (1) the whole region of `steps` back-to-back launches
+    between two synchronisations (events only at its ends) and (2), in a
+    second pass, each launch on its own between HIP events on the launch
+    stream."""
     for _ in range(warmup):
         rc = launch()
         if rc != 0:
             raise RuntimeError(f"launch failed: {rc}")
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     w0 = time.perf_counter()
     t0.record()
+    for _ in range(steps):
+        launch()
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     for i in range(steps):
         starts[i].record()
         launch()
         ends[i].record()
-    t1.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - w0
     per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     return {"kernel_ms_avg": statistics.fmean(per), "kernel_ms_median": statistics.median(per),
             "region_ms": t0.elapsed_time(t1), "wall_s": wall}
@@ -274,8 +287,53 @@ def _cpu_model():
     return "unknown"
 
 
+# Kernel that dominates each config's launch (rocprofv3 names it this way).
+DOMINANT = {
+    "c1": "fq_lut_kernel<float, 1>",
+    "c2": "mx_lut_kernel<4, 4, true, 0>",
+    "c2_decode": "decode_group_kernel<unsigned short, 4, 4>",
+    "c3_e4m3": "mx_lut_kernel<8, 2, false, 0>",
+    "c3_e3m2": "mx_lut_kernel<6, 2, false, 0>",
+    "c3_e2m1": "mx_lut_kernel<4, 2, false, 0>",
+    "c3_e4m3_fq": "mx_lut_kernel<0, 2, false, 2>",
+    "c4_k16": "cb_encode_kernel<float>",
+    "c4_k256": "cb_encode_kernel<float>",
+    "c4_k16_decode": "cb_decode_kernel<float>",
+    "c5": "nf4_gemm_kernel",
+}
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+
+
+def measured_traffic(key):
+    """HBM bytes per launch of a config's dominant kernel, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes summarised in profiles/hbm_traffic.json
+    (already scaled by the copy-kernel calibration), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t["configs"][key]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
+
+
+def calibrate_copy():
+    import torch
+
+    n = 512 << 20
+    x = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "launches": 5}))
+
+
 def main():
     a = parse()
+    if a.calibrate_copy:
+        calibrate_copy()
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "bench.py runs on one GPU only: this build has no multi-GPU path "
                                    f"(asked for --gpus {a.gpus})"}))
@@ -297,9 +355,11 @@ def main():
         tm = time_config(torch, launch, a.steps, a.warmup)
         ms = tm["kernel_ms_avg"]
         gbs = info["bytes"] / (ms * 1e-3) / 1e9
+        region = tm["region_ms"] / a.steps
         results[k] = {
-            "workload": info["name"], "elements_per_s": info["elements"] / (ms * 1e-3),
-            "kernel_ms": ms, "region_ms_per_step": tm["region_ms"] / a.steps,
+            "workload": info["name"], "elements_per_s": info["elements"] / (region * 1e-3),
+            "kernel_ms": ms, "region_ms_per_step": region, "kernel": DOMINANT.get(k),
+            "hbm_traffic_bytes": measured_traffic(k),
             "algorithmic_bytes": info["bytes"], "achieved_GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
             "dtype": info["dtype"]}
         if info["bound"] == "mfma":
@@ -335,8 +395,8 @@ def main():
         "data": "synthetic (seeded, BASELINE.json configs)",
         "config": {"workload": head["workload"], "block_size": 64, "format": "nf4", "shape": [4096, 11008]},
         "roofline": {"bound": "hbm", "achieved": head["achieved_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["hbm_frac"], "traffic": None,
-                     "kernel": "mx_group_kernel<bf16, EncLevels, 4, 4>",
+                     "frac": head["hbm_frac"], "traffic": head["hbm_traffic_bytes"],
+                     "kernel": DOMINANT[HEADLINE],
                      "algorithmic_bytes_per_launch": head["algorithmic_bytes"],
                      "kernel_ms_avg": head["kernel_ms"]},
         "cpu_baseline": cpu,

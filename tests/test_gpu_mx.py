@@ -58,6 +58,26 @@ def test_pow2_scale_every_amax(vqx, qmax):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("qmax", [448.0, 6.0, 1.0])
+def test_pow2_scale_fp32_input(vqx, qmax):
+    # fp32 amax: the reference takes floor(log2) in fp32 (torch CPU log2 of
+    # float32), which steps up near the top of each binade; cover the top 64
+    # mantissas of every binade, random mantissas and subnormals
+    g = torch.Generator().manual_seed(7)
+    E = torch.arange(1, 255, dtype=torch.int64)
+    top = (E.unsqueeze(1) << 23) | (0x7FFFFF - torch.arange(64)).unsqueeze(0)
+    rnd = (E.unsqueeze(1) << 23) | torch.randint(0, 1 << 23, (E.numel(), 16), generator=g)
+    sub = torch.cat([torch.tensor([1, 2, 3, 0x400000, 0x7FFFFF]), torch.randint(1, 1 << 23, (64,), generator=g)])
+    bits = torch.cat([top.reshape(-1), rnd.reshape(-1), sub]).to(torch.int32)
+    a = bits.view(torch.float32)
+    x = torch.zeros(a.numel(), 32, dtype=torch.float32)
+    x[:, 3] = a
+    x[:, 9] = -a * 0.25
+    got = Q.calculate_mx_qparam(x.cuda(), [-1], 32, qmax, True, None)
+    assert_bitexact(got.cpu(), R.calculate_mx_qparam(x, [-1], 32, qmax, True), f"fp32 pow2 scales qmax={qmax}")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("qmax", [1.0, 31.0, 448.0])
 def test_absmax_scale_every_amax(vqx, qmax):
     a = torch.arange(0, 0x7F81, 3, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
