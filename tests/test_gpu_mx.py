@@ -67,7 +67,10 @@ def test_pow2_scale_fp32_input(vqx, qmax):
     E = torch.arange(1, 255, dtype=torch.int64)
     top = (E.unsqueeze(1) << 23) | (0x7FFFFF - torch.arange(64)).unsqueeze(0)
     rnd = (E.unsqueeze(1) << 23) | torch.randint(0, 1 << 23, (E.numel(), 16), generator=g)
-    sub = torch.cat([torch.tensor([1, 2, 3, 0x400000, 0x7FFFFF]), torch.randint(1, 1 << 23, (64,), generator=g)])
+    # subnormals: the top 24 mantissas below each power of two from 2^17 up
+    # (where the log rounds up), a few more, and random ones
+    tops = torch.cat([(1 << (k + 1)) - 1 - torch.arange(24) for k in range(16, 23)])
+    sub = torch.cat([torch.tensor([1, 2, 3, 0x400000, 0x7FFFFF]), tops, torch.randint(1, 1 << 23, (64,), generator=g)])
     bits = torch.cat([top.reshape(-1), rnd.reshape(-1), sub]).to(torch.int32)
     a = bits.view(torch.float32)
     x = torch.zeros(a.numel(), 32, dtype=torch.float32)
@@ -163,6 +166,16 @@ def test_packed_mx_codes_e8m0_and_decode(vqx, dtype, qmax):
     # decode(codes, E8M0) = the reference's fake-quant values
     dq = Q.dequantize_mx_packed(codes, sc, dtype, 32, list(x.shape), torch.bfloat16)
     assert_bitexact(dq.cpu(), wq * R.expand(ws, wq.shape, 32), f"{dtype} decode")
+    # fp32 output: the power-of-two products are exact, so equal to the bf16 ones
+    dq32 = Q.dequantize_mx_packed(codes, sc, dtype, 32, list(x.shape), torch.float32)
+    assert_bitexact(dq32.cpu(), (wq * R.expand(ws, wq.shape, 32)).float(), f"{dtype} decode fp32")
+    # a size that leaves a tail past the last whole 1024-element wave step
+    xt = c3_input(3, 2080)
+    sct, codest = Q.quantize_mx_packed(xt.cuda(), dtype, -1, 32, True, qmax, "e8m0")
+    wst, wqt = R.quantize_mx(xt, oracle_qmap(dtype), [-1], 32, qmax, True)
+    for odt in (torch.bfloat16, torch.float32):
+        dqt = Q.dequantize_mx_packed(codest, sct, dtype, 32, list(xt.shape), odt)
+        assert_bitexact(dqt.cpu(), (wqt * R.expand(wst, wqt.shape, 32)).to(odt), f"{dtype} decode tail {odt}")
     # bf16 / fp32 scale outputs carry the reference scale exactly
     sb, codes2 = Q.quantize_mx_packed(x.cuda(), dtype, -1, 32, True, qmax, "bfloat16")
     assert_bitexact(sb.cpu(), ws, "bf16 scales")

@@ -81,7 +81,15 @@ struct BT<float> {
 // 2^23 (2^(1 - u/2) - 1), u the fp32 spacing next to the integer above.
 __device__ __forceinline__ int log2floor_f32(uint32_t mag) {
   uint32_t E = mag >> 23, m = mag & 0x7FFFFFu;
-  if (E == 0) return (31 - clz32(m)) - 149;  // subnormal amax: floor of the exact log
+  if (E == 0) {
+    // subnormal amax m * 2^-149, 2^k <= m < 2^(k+1): the fp32 log rounds up
+    // to k - 148 for the top J mantissas of the range (J by k = 17..22, from
+    // torch's CPU log2 over every subnormal; none below k = 17)
+    const int k = 31 - clz32(m);
+    const uint32_t kSubTop[6] = {1, 2, 5, 11, 11, 22};
+    const uint32_t J = k >= 17 ? kSubTop[k - 17] : 0u;
+    return k - 149 + (J != 0 && m >= (2u << k) - J ? 1 : 0);
+  }
   int p = (int)E - 127;
   int band;
   if (p >= 0) {
@@ -646,6 +654,54 @@ __device__ __forceinline__ float load_scale(const void* s, int kind, int64_t i) 
   return e == 0xFFu ? __builtin_huge_valf() : (e == 0 ? u2f(0x00400000u) : u2f(e << 23));
 }
 
+// Decode of packed codes: out = round(table[code] * scale[block]).
+// 4- and 8-bit codes take a lane-interleaved layout: a wave handles 1024
+// elements per step as chunks of 16 output bytes per lane (E = 8 bf16 or 4
+// fp32 elements), chunk q of lane L at element 64 E q + E L, so every load
+// and store instruction of the wave covers one contiguous span; each chunk
+// lies inside one block (block sizes are multiples of 16).  6-bit codes and
+// any elements past the last whole 1024 take 16-element groups per thread.
+template <typename T, int CB>
+__device__ __forceinline__ void decode_chunks(const uint8_t* __restrict__ codes, const void* scale, int scale_kind,
+                                              const uint16_t* tab, T* __restrict__ out, int64_t base, int lane,
+                                              int64_t bs) {
+  constexpr int E = 16 / (int)sizeof(T);  // elements per 16-byte output chunk
+  constexpr int Q = 16 / E;               // chunks per lane per step
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int64_t e = base + (int64_t)q * 64 * E + (int64_t)lane * E;
+    uint32_t c[E];
+    if constexpr (CB == 4 && E == 8) {
+      uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(codes + e / 2));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = (w >> (4 * j)) & 0xFu;
+    } else if constexpr (CB == 4) {  // E == 4
+      uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(codes + e / 2));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = (w >> (4 * j)) & 0xFu;
+    } else if constexpr (E == 8) {  // CB == 8
+      u32x2 w = ld_nt(reinterpret_cast<const u32x2*>(codes + e));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = ((j < 4 ? w.x : w.y) >> (8 * (j & 3))) & 0xFFu;
+    } else {  // CB == 8, E == 4
+      uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(codes + e));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = (w >> (8 * j)) & 0xFFu;
+    }
+    const float s = load_scale(scale, scale_kind, e / bs);
+    if constexpr (E == 8) {
+      uint32_t o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(tab[c[j]]) * s);
+      u32x4 v = {o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+      st_nt(reinterpret_cast<u32x4*>(out + e), v);
+    } else {
+      f32x4 v = {bf2f(tab[c[0]]) * s, bf2f(tab[c[1]]) * s, bf2f(tab[c[2]]) * s, bf2f(tab[c[3]]) * s};
+      st_nt(reinterpret_cast<f32x4*>(out + e), v);
+    }
+  }
+}
+
 template <typename T, int CB, int LPB>
 __global__ __launch_bounds__(256) void decode_group_kernel(const uint8_t* __restrict__ codes,
                                                            const void* __restrict__ scale, int scale_kind,
@@ -655,7 +711,16 @@ __global__ __launch_bounds__(256) void decode_group_kernel(const uint8_t* __rest
   for (int i = threadIdx.x; i < ntab && i < (1 << (CB > 8 ? 8 : CB)); i += blockDim.x) tab[i] = dtab[i];
   __syncthreads();
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
+  int64_t g0 = 0;  // first group left to the per-thread loop
+  if constexpr (CB == 4 || CB == 8) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nsteps = ngroups / 64;  // whole 1024-element wave steps
+    const int64_t wstride = stride / 64;
+    for (int64_t w = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64; w < nsteps; w += wstride)
+      decode_chunks<T, CB>(codes, scale, scale_kind, tab, out, w * 1024, lane, 16 * LPB);
+    g0 = nsteps * 64;
+  }
+  for (int64_t g = g0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
     uint32_t c[16];
     if constexpr (CB == 4) {
       u32x2 w = ld_nt(reinterpret_cast<const u32x2*>(codes + g * 8));

@@ -192,11 +192,40 @@ __global__ __launch_bounds__(256) void fq_lut_kernel(const T* __restrict__ x, T*
                                                      const float* __restrict__ scale, bool mul, LutView lv) {
   extern __shared__ uint32_t lds_lut[];
   constexpr bool kBf16 = std::is_same<T, uint16_t>::value;
+  constexpr bool kF32 = std::is_same<T, float>::value;
   const int64_t nvec = n / 8;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int lane = threadIdx.x & 63;
   int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // Element offsets of thread group gg's two 4-element halves.  fp32 is
+  // lane-interleaved within a whole wave (lane L: 4 L and 256 + 4 L of the
+  // wave's 512 elements), so each 16-byte load / store instruction of the
+  // wave covers one contiguous span; 2-byte types already do (one 16-byte
+  // access per lane).
+  auto halves = [&](int64_t gg, int64_t& e0, int64_t& e1) {
+    e0 = gg * 8;
+    e1 = e0 + 4;
+    if constexpr (kF32) {
+      const int64_t w0 = gg - lane;
+      if (w0 + 64 <= nvec) {
+        e0 = w0 * 8 + lane * 4;
+        e1 = e0 + 256;
+      }
+    }
+  };
+  auto load8 = [&](int64_t gg, float (&v)[8]) {
+    if constexpr (kF32) {
+      int64_t e0, e1;
+      halves(gg, e0, e1);
+      f32x4 a = ld_nt(reinterpret_cast<const f32x4*>(x + e0)), b = ld_nt(reinterpret_cast<const f32x4*>(x + e1));
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+      IO<T>::load(x + gg * 8, v);
+    }
+  };
   float nxt[8];
-  if (g < nvec) IO<T>::load(x + g * 8, nxt);  // in flight while the table fills LDS
+  if (g < nvec) load8(g, nxt);  // in flight while the table fills LDS
   LutLds t = lut_to_lds(lv.blob, lv.len, lds_lut);
   const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
   // LDS byte addresses such that entry(h) = base + 4 h for h in [T0 - 1, T1]
@@ -216,7 +245,7 @@ __global__ __launch_bounds__(256) void fq_lut_kernel(const T* __restrict__ x, T*
     uint32_t c[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = nxt[j];
-    if (g + stride < nvec) IO<T>::load(x + (g + stride) * 8, nxt);
+    if (g + stride < nvec) load8(g + stride, nxt);
     uint32_t m = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) m = umax32(m, f2u(v[j]) & 0x7FFFFFFFu);
@@ -244,8 +273,28 @@ __global__ __launch_bounds__(256) void fq_lut_kernel(const T* __restrict__ x, T*
         v[j] = unit ? (kBf16 ? q : to_dtype<T>(q)) : (mul ? to_dtype<T>(to_dtype<T>(q) * s) : to_dtype<T>(q));
       }
     }
-    if (y) IO<T>::store(y + g * 8, v);
-    if constexpr (CB > 0) store_codes8<CB>(codes, g * 8, c);
+    if constexpr (kF32) {
+      int64_t e0, e1;
+      halves(g, e0, e1);
+      if (y) {
+        st_nt(reinterpret_cast<f32x4*>(y + e0), f32x4{v[0], v[1], v[2], v[3]});
+        st_nt(reinterpret_cast<f32x4*>(y + e1), f32x4{v[4], v[5], v[6], v[7]});
+      }
+      if constexpr (CB == 1) {
+        uint8_t* cb8 = static_cast<uint8_t*>(codes);
+        __builtin_nontemporal_store((c[0] & 0xFF) | ((c[1] & 0xFF) << 8) | ((c[2] & 0xFF) << 16) | (c[3] << 24),
+                                    reinterpret_cast<uint32_t*>(cb8 + e0));
+        __builtin_nontemporal_store((c[4] & 0xFF) | ((c[5] & 0xFF) << 8) | ((c[6] & 0xFF) << 16) | (c[7] << 24),
+                                    reinterpret_cast<uint32_t*>(cb8 + e1));
+      } else if constexpr (CB == 2) {
+        uint16_t* cb16 = static_cast<uint16_t*>(codes);
+        st_nt(reinterpret_cast<u32x2*>(cb16 + e0), u32x2{(c[0] & 0xFFFF) | (c[1] << 16), (c[2] & 0xFFFF) | (c[3] << 16)});
+        st_nt(reinterpret_cast<u32x2*>(cb16 + e1), u32x2{(c[4] & 0xFFFF) | (c[5] << 16), (c[6] & 0xFFFF) | (c[7] << 16)});
+      }
+    } else {
+      if (y) IO<T>::store(y + g * 8, v);
+      if constexpr (CB > 0) store_codes8<CB>(codes, g * 8, c);
+    }
   }
   int64_t i = nvec * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) {
