@@ -49,3 +49,37 @@ def test_codebook_bf16_input(vqx):
     cb = c4_codebooks(64, 16)
     codes = Q.codebook_encode(x.cuda(), cb.cuda())
     assert torch.equal(codes.cpu().long(), R.codebook_encode_rows(x.float(), cb))
+
+
+def random_codebooks(rows, K, g):
+    """Sorted rows with repeated entries, including runs at the top (which
+    leave the later decision thresholds empty) and at the bottom."""
+    cb = torch.sort(torch.randn(rows, K, generator=g), dim=1).values
+    if K >= 3:
+        for r in range(0, rows, 7):
+            n = 1 + r % (K - 1)
+            cb[r, K - n:] = cb[r, K - n]        # top run
+        for r in range(3, rows, 11):
+            n = 1 + r % (K - 1)
+            cb[r, :n] = cb[r, n - 1]            # bottom run
+    return cb
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [1, 2, 3, 5, 17, 100, 129, 255, 256])
+@pytest.mark.parametrize("rows,cols", [(3000, 16), (40, 1040), (9, 2064)])
+def test_codebook_sizes_and_shapes(vqx, K, rows, cols):
+    """Every search depth (codebook sizes 1 .. 256), rows beyond the resident
+    grid, row lengths below, at and past the 1024-element chunk, fp32 and
+    bf16 outputs."""
+    g = torch.Generator().manual_seed(1000 * K + cols)
+    cb = random_codebooks(rows, K, g)
+    x = torch.randn(rows, cols, generator=g) * 1.5
+    n = min(K, cols)
+    x[0, :n] = cb[0, :n]
+    codes = Q.codebook_encode(x.cuda(), cb.cuda())
+    want = R.codebook_encode_rows(x, cb)
+    assert torch.equal(codes.cpu().long(), want)
+    for dt in (torch.float32, torch.bfloat16):
+        dec = Q.codebook_decode(codes, cb.cuda(), dt)
+        assert torch.equal(dec.cpu().float(), R.codebook_decode_rows(want, cb))

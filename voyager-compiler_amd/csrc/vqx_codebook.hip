@@ -74,84 +74,174 @@ __device__ uint32_t code_threshold(const float* cb, int K, int i) {
 // elements taken as 4 sub-chunks of 64 x 4, so each load / store instruction
 // of the wave covers one contiguous span.
 constexpr int kCbChunk = 1024;  // elements per wave chunk
+constexpr int kCbMaxK = 256;    // entries per row, one per thread of the workgroup
 
-// Per-channel encode: one workgroup per row (grid-stride over rows); the
-// row's sorted thresholds (padded with ~0 to a power of two P) in LDS; per
-// element the bf16 key and a branch-free search of log2(P) steps.
+// Node of sorted threshold j (0-based) in the breadth-first (Eytzinger) layout
+// of a complete search tree with 2^L - 1 nodes: node 1 is the root, the
+// children of node i are 2i and 2i + 1.  The in-order rank j + 1 =
+// (2m + 1) 2^h puts it at height h, i.e. depth L - 1 - h, m-th from the left.
+__device__ __forceinline__ uint32_t eytzinger_node(uint32_t j, int L) {
+  const uint32_t r = j + 1;
+  const int h = __builtin_ctz(r);
+  return (1u << (L - 1 - h)) + (r >> (h + 1));
+}
+
 template <typename T>
-__global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
-                                                        const float* __restrict__ cb, int K, int P,
-                                                        uint8_t* __restrict__ codes) {
-  extern __shared__ float s_cb[];               // K fp32 entries, then P uint32 thresholds
-  uint32_t* s_t = reinterpret_cast<uint32_t*>(s_cb + K);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    __syncthreads();
-    for (int k = threadIdx.x; k < K; k += blockDim.x) s_cb[k] = cb[r * K + k];
-    __syncthreads();
-    for (int k = threadIdx.x; k < P; k += blockDim.x) s_t[k] = k < K - 1 ? code_threshold(s_cb, K, k) : 0xFFFFFFFFu;
-    __syncthreads();
-    const T* xr = x + r * cols;
-    uint8_t* cr = codes + r * cols;
-    auto encode = [&](float v) -> uint32_t {
-      uint32_t key = bf16_key(f2bf(v));
-      uint32_t pos = 0;
-      for (int step = P >> 1; step > 0; step >>= 1) pos += s_t[pos + step - 1] <= key ? step : 0;
-      return v != v ? 0u : pos;
-    };
-    int64_t full = cols / kCbChunk * kCbChunk;
-    for (int64_t base = (int64_t)wave * kCbChunk; base < full; base += (int64_t)nwaves * kCbChunk) {
-      float v[16];
+__device__ __forceinline__ void load_chunk(const T* xr, int64_t base, int lane, float (&v)[16]) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t e = base + q * 256 + lane * 4;
-        if constexpr (std::is_same<T, float>::value) {
-          f32x4 a = ld_nt(reinterpret_cast<const f32x4*>(xr + e));
-          v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
-        } else {
-          u32x2 a = ld_nt(reinterpret_cast<const u32x2*>(xr + e));
-          v[4 * q] = u2f(a.x << 16); v[4 * q + 1] = u2f(a.x & 0xFFFF0000u);
-          v[4 * q + 2] = u2f(a.y << 16); v[4 * q + 3] = u2f(a.y & 0xFFFF0000u);
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t c0 = encode(v[4 * q]), c1 = encode(v[4 * q + 1]), c2 = encode(v[4 * q + 2]),
-                 c3 = encode(v[4 * q + 3]);
-        __builtin_nontemporal_store(c0 | (c1 << 8) | (c2 << 16) | (c3 << 24),
-                                    reinterpret_cast<uint32_t*>(cr + base + q * 256 + lane * 4));
-      }
-    }
-    for (int64_t i = full + threadIdx.x; i < cols; i += blockDim.x) {
-      float xv = std::is_same<T, float>::value ? (float)xr[i] : u2f((uint32_t)((const uint16_t*)xr)[i] << 16);
-      cr[i] = (uint8_t)encode(xv);
+  for (int q = 0; q < 4; ++q) {
+    const int64_t e = base + q * 256 + lane * 4;
+    if constexpr (std::is_same<T, float>::value) {
+      f32x4 a = ld_nt(reinterpret_cast<const f32x4*>(xr + e));
+      v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
+    } else {
+      u32x2 a = ld_nt(reinterpret_cast<const u32x2*>(xr + e));
+      v[4 * q] = u2f(a.x << 16); v[4 * q + 1] = u2f(a.x & 0xFFFF0000u);
+      v[4 * q + 2] = u2f(a.y << 16); v[4 * q + 3] = u2f(a.y & 0xFFFF0000u);
     }
   }
 }
 
+// Wave-level LDS hand-off: the wave's own LDS writes are complete and visible
+// to all its lanes before any lane reads past this point.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Per-channel encode.  Each wave works through its own rows (row gw, gw + nw,
+// ... for global wave gw of nw) with no workgroup barriers; the items it
+// streams are the 1024-element chunks of those rows in order, in two register
+// buffers used in turn: the next item's load is issued before the current one
+// is encoded, also across a row boundary, so loads stay in flight while a
+// row's search table is built.  The table: the row's K - 1 decision
+// thresholds, padded with ~0 to 2^LOGP - 1, in breadth-first order in the
+// wave's LDS slice, so each level of the search reads one contiguous run of
+// nodes (distinct banks down to 64 nodes); the LOGP-step search is unrolled,
+// letting a lane's 16 searches overlap.  Row elements past the last whole
+// chunk are encoded one per lane.
+template <typename T, int LOGP>
+__global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
+                                                        const float* __restrict__ cb, int K,
+                                                        uint8_t* __restrict__ codes) {
+  constexpr int P = 1 << LOGP;
+  constexpr int kSlice = P > 1 ? P : 2;
+  __shared__ float s_cbw[4][kCbMaxK];
+  __shared__ uint32_t s_tw[4][kSlice];  // node i at s_t[i], i = 1 .. P - 1
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float* s_cb = s_cbw[wave];
+  uint32_t* s_t = s_tw[wave];
+  const int64_t gw = (int64_t)blockIdx.x * 4 + wave, nw = (int64_t)gridDim.x * 4;
+  const int64_t nchunk = cols / kCbChunk, full = nchunk * kCbChunk;
+  auto encode = [&](float v) -> uint32_t {
+    const uint32_t key = bf16_key(f2bf(v));
+    uint32_t i = 1;
+#pragma unroll
+    for (int l = 0; l < LOGP; ++l) i = 2 * i + (s_t[i] <= key ? 1u : 0u);
+    return v != v ? 0u : i - (uint32_t)P;
+  };
+  auto load_cb = [&](int64_t r, float (&c)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c[j] = (r < rows && lane + 64 * j < K) ? cb[r * K + lane + 64 * j] : 0.0f;
+  };
+  float cbn[4];
+  load_cb(gw, cbn);
+  int64_t r = gw, c = 0;  // current item: chunk c of row r
+  // one item: encode chunk (r, c) from cur after loading the next item into nxt
+  auto step = [&](const float (&cur)[16], float (&nxt)[16]) {
+    if (c == 0) {  // new row: its table from the prefetched codebook
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j < K) s_cb[lane + 64 * j] = cbn[j];
+      wave_lds_sync();
+      for (int j = lane; j < P - 1; j += 64)
+        s_t[eytzinger_node(j, LOGP)] = j < K - 1 ? code_threshold(s_cb, K, j) : 0xFFFFFFFFu;
+      load_cb(r + nw, cbn);
+      wave_lds_sync();
+    }
+    const bool last = c + 1 >= nchunk;
+    const int64_t rn = last ? r + nw : r, cn = last ? 0 : c + 1;
+    if (nchunk > 0) {
+      // past the wave's last item: reload the current one (a valid address)
+      const bool more = rn < rows;
+      load_chunk(x + (more ? rn : r) * cols, (more ? cn : c) * kCbChunk, lane, nxt);
+      uint8_t* cr = codes + r * cols + c * kCbChunk;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t c0 = encode(cur[4 * q]), c1 = encode(cur[4 * q + 1]), c2 = encode(cur[4 * q + 2]),
+                 c3 = encode(cur[4 * q + 3]);
+        __builtin_nontemporal_store(c0 | (c1 << 8) | (c2 << 16) | (c3 << 24),
+                                    reinterpret_cast<uint32_t*>(cr + q * 256 + lane * 4));
+      }
+    }
+    if (last) {  // row done: its tail
+      const T* xr = x + r * cols;
+      for (int64_t i = full + lane; i < cols; i += 64) {
+        float xv = std::is_same<T, float>::value ? (float)xr[i] : u2f((uint32_t)((const uint16_t*)xr)[i] << 16);
+        codes[r * cols + i] = (uint8_t)encode(xv);
+      }
+      wave_lds_sync();  // all lanes are done with this row's table
+    }
+    r = rn;
+    c = cn;
+  };
+  float va[16], vb[16];
+  if (r < rows && nchunk > 0) load_chunk(x + r * cols, 0, lane, va);
+  while (r < rows) {
+    step(va, vb);
+    if (r >= rows) break;
+    step(vb, va);
+  }
+}
+
+// Per-channel decode, organised like the encode: each wave streams the
+// 1024-element chunks of its own rows through two register buffers, the next
+// chunk's codes loaded before the current one is written out, the row's table
+// (bf16 of each entry) in the wave's LDS slice.
 template <typename T>
 __global__ __launch_bounds__(256) void cb_decode_kernel(const uint8_t* __restrict__ codes, int64_t rows,
                                                         int64_t cols, const float* __restrict__ cb, int K,
                                                         T* __restrict__ out) {
-  extern __shared__ float s_cb[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-    __syncthreads();
-    for (int k = threadIdx.x; k < K; k += blockDim.x) s_cb[k] = bf2f(f2bf(cb[r * K + k]));
-    __syncthreads();
-    const uint8_t* cr = codes + r * cols;
-    T* orow = out + r * cols;
-    auto value = [&](uint32_t c) { return s_cb[c < (uint32_t)K ? c : K - 1]; };
-    int64_t full = cols / kCbChunk * kCbChunk;
-    for (int64_t base = (int64_t)wave * kCbChunk; base < full; base += (int64_t)nwaves * kCbChunk) {
-      uint32_t w[4];
+  __shared__ float s_cbw[4][kCbMaxK];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float* s_cb = s_cbw[wave];
+  const int64_t gw = (int64_t)blockIdx.x * 4 + wave, nw = (int64_t)gridDim.x * 4;
+  const int64_t nchunk = cols / kCbChunk, full = nchunk * kCbChunk;
+  auto value = [&](uint32_t c) { return s_cb[c < (uint32_t)K ? c : K - 1]; };
+  auto load_cb = [&](int64_t r, float (&c)[4]) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) w[q] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(cr + base + q * 256 + lane * 4));
+    for (int j = 0; j < 4; ++j) c[j] = (r < rows && lane + 64 * j < K) ? cb[r * K + lane + 64 * j] : 0.0f;
+  };
+  auto load = [&](const uint8_t* p, uint32_t(&d)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) d[q] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p + q * 256 + lane * 4));
+  };
+  float cbn[4];
+  load_cb(gw, cbn);
+  int64_t r = gw, c = 0;
+  auto step = [&](const uint32_t(&cur)[4], uint32_t(&nxt)[4]) {
+    if (c == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (lane + 64 * j < K) s_cb[lane + 64 * j] = bf2f(f2bf(cbn[j]));
+      load_cb(r + nw, cbn);
+      wave_lds_sync();
+    }
+    const bool last = c + 1 >= nchunk;
+    const int64_t rn = last ? r + nw : r, cn = last ? 0 : c + 1;
+    if (nchunk > 0) {
+      const bool more = rn < rows;
+      load(codes + (more ? rn : r) * cols + (more ? cn : c) * kCbChunk, nxt);
+      T* orow = out + r * cols + c * kCbChunk;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float v0 = value(w[q] & 0xFFu), v1 = value((w[q] >> 8) & 0xFFu), v2 = value((w[q] >> 16) & 0xFFu),
-              v3 = value(w[q] >> 24);
-        const int64_t e = base + q * 256 + lane * 4;
+        float v0 = value(cur[q] & 0xFFu), v1 = value((cur[q] >> 8) & 0xFFu), v2 = value((cur[q] >> 16) & 0xFFu),
+              v3 = value(cur[q] >> 24);
+        const int e = q * 256 + lane * 4;
         if constexpr (std::is_same<T, float>::value) {
           st_nt(reinterpret_cast<f32x4*>(orow + e), f32x4{v0, v1, v2, v3});
         } else {
@@ -160,31 +250,58 @@ __global__ __launch_bounds__(256) void cb_decode_kernel(const uint8_t* __restric
         }
       }
     }
-    for (int64_t i = full + threadIdx.x; i < cols; i += blockDim.x) {
-      float v = value(cr[i]);
-      if constexpr (std::is_same<T, float>::value) orow[i] = v;
-      else ((uint16_t*)orow)[i] = (uint16_t)(f2u(v) >> 16);
+    if (last) {
+      const uint8_t* cr = codes + r * cols;
+      T* orow = out + r * cols;
+      for (int64_t i = full + lane; i < cols; i += 64) {
+        float v = value(cr[i]);
+        if constexpr (std::is_same<T, float>::value) orow[i] = v;
+        else ((uint16_t*)orow)[i] = (uint16_t)(f2u(v) >> 16);
+      }
+      wave_lds_sync();
     }
+    r = rn;
+    c = cn;
+  };
+  uint32_t wa[4], wb[4];
+  if (r < rows && nchunk > 0) load(codes + r * cols, wa);
+  while (r < rows) {
+    step(wa, wb);
+    if (r >= rows) break;
+    step(wb, wa);
   }
+}
+
+// one wave per row, as many as fit on the device at once
+template <typename T>
+static void launch_encode(int logp, hipStream_t st, const T* x, int64_t rows, int64_t cols, const float* cb,
+                          int K, uint8_t* codes) {
+#define VQX_CB_CASE(L)                                                                                    \
+  case L:                                                                                                 \
+    hipLaunchKernelGGL((cb_encode_kernel<T, L>),                                                          \
+                       dim3(persistent_grid((const void*)cb_encode_kernel<T, L>, 256, 0, rows * 64)), dim3(256), \
+                       0, st, x, rows, cols, cb, K, codes);                                               \
+    break;
+  switch (logp) {
+    VQX_CB_CASE(0) VQX_CB_CASE(1) VQX_CB_CASE(2) VQX_CB_CASE(3) VQX_CB_CASE(4)
+    VQX_CB_CASE(5) VQX_CB_CASE(6) VQX_CB_CASE(7) default: VQX_CB_CASE(8)
+  }
+#undef VQX_CB_CASE
 }
 
 int codebook_encode(const void* x, int dtype, int64_t rows, int64_t cols, const float* cb, int K,
                     uint8_t* codes, hipStream_t st) {
-  if (K < 1 || K > 256) return set_error(kErrInvalid, "codebook size %d outside [1,256]", K);
+  if (K < 1 || K > kCbMaxK) return set_error(kErrInvalid, "codebook size %d outside [1,%d]", K, kCbMaxK);
   if (rows < 0 || cols < 0) return set_error(kErrInvalid, "negative shape");
   if (rows == 0 || cols == 0) return kOk;
   if (!aligned(x, 16) || !aligned(codes, 16) || (cols % 16) != 0)
     return set_error(kErrInvalid, "codebook encode needs 16-byte aligned rows (cols %% 16 == 0)");
-  unsigned grid = (unsigned)(rows < (int64_t)num_cus() * 8 ? rows : (int64_t)num_cus() * 8);
-  int P = 1;
-  while (P < K) P <<= 1;  // K - 1 thresholds padded to a power of two >= K (codes up to P - 1)
-  size_t lds = sizeof(float) * K + sizeof(uint32_t) * P;
+  int logp = 0;
+  while ((1 << logp) < K) ++logp;  // K - 1 thresholds padded to 2^logp - 1 nodes (codes up to 2^logp - 1)
   if (dtype == kF32)
-    hipLaunchKernelGGL((cb_encode_kernel<float>), dim3(grid), dim3(256), lds, st, (const float*)x, rows, cols,
-                       cb, K, P, codes);
+    launch_encode<float>(logp, st, (const float*)x, rows, cols, cb, K, codes);
   else if (dtype == kBF16)
-    hipLaunchKernelGGL((cb_encode_kernel<uint16_t>), dim3(grid), dim3(256), lds, st, (const uint16_t*)x,
-                       rows, cols, cb, K, P, codes);
+    launch_encode<uint16_t>(logp, st, (const uint16_t*)x, rows, cols, cb, K, codes);
   else
     return set_error(kErrInvalid, "codebook input dtype %d not supported", dtype);
   return check_launch("codebook_encode");
@@ -192,19 +309,19 @@ int codebook_encode(const void* x, int dtype, int64_t rows, int64_t cols, const 
 
 int codebook_decode(const uint8_t* codes, int64_t rows, int64_t cols, const float* cb, int K, void* out,
                     int dtype, hipStream_t st) {
-  if (K < 1 || K > 256) return set_error(kErrInvalid, "codebook size %d outside [1,256]", K);
+  if (K < 1 || K > kCbMaxK) return set_error(kErrInvalid, "codebook size %d outside [1,%d]", K, kCbMaxK);
   if (rows < 0 || cols < 0) return set_error(kErrInvalid, "negative shape");
   if (rows == 0 || cols == 0) return kOk;
   if (!aligned(out, 16) || !aligned(codes, 16) || (cols % 16) != 0)
     return set_error(kErrInvalid, "codebook decode needs 16-byte aligned rows (cols %% 16 == 0)");
-  unsigned grid = (unsigned)(rows < (int64_t)num_cus() * 8 ? rows : (int64_t)num_cus() * 8);
-  size_t lds = sizeof(float) * K;
+  const int64_t work = rows * 64;  // one wave per row
   if (dtype == kF32)
-    hipLaunchKernelGGL((cb_decode_kernel<float>), dim3(grid), dim3(256), lds, st, codes, rows, cols, cb, K,
-                       (float*)out);
+    hipLaunchKernelGGL((cb_decode_kernel<float>), dim3(persistent_grid((const void*)cb_decode_kernel<float>, 256, 0, work)),
+                       dim3(256), 0, st, codes, rows, cols, cb, K, (float*)out);
   else if (dtype == kBF16)
-    hipLaunchKernelGGL((cb_decode_kernel<uint16_t>), dim3(grid), dim3(256), lds, st, codes, rows, cols, cb,
-                       K, (uint16_t*)out);
+    hipLaunchKernelGGL((cb_decode_kernel<uint16_t>),
+                       dim3(persistent_grid((const void*)cb_decode_kernel<uint16_t>, 256, 0, work)), dim3(256), 0, st,
+                       codes, rows, cols, cb, K, (uint16_t*)out);
   else
     return set_error(kErrInvalid, "codebook output dtype %d not supported", dtype);
   return check_launch("codebook_decode");
