@@ -53,7 +53,9 @@ def test_codebook_bf16_input(vqx):
 
 def random_codebooks(rows, K, g):
     """Sorted rows with repeated entries, including runs at the top (which
-    leave the later decision thresholds empty) and at the bottom."""
+    leave the later decision thresholds empty) and at the bottom; rows with
+    entries one fp32 ulp apart, and rows spanning 40 binades, where rounded
+    distances tie (encoded by the exact per-element search)."""
     cb = torch.sort(torch.randn(rows, K, generator=g), dim=1).values
     if K >= 3:
         for r in range(0, rows, 7):
@@ -62,6 +64,13 @@ def random_codebooks(rows, K, g):
         for r in range(3, rows, 11):
             n = 1 + r % (K - 1)
             cb[r, :n] = cb[r, n - 1]            # bottom run
+    if K >= 2:
+        for r in range(5, rows, 13):
+            cb[r, 1] = torch.nextafter(cb[r, 0], torch.tensor(float("inf")))
+            cb[r] = torch.sort(cb[r]).values
+        for r in range(6, rows, 17):
+            mag = torch.exp(torch.empty(K).uniform_(-20, 20, generator=g))
+            cb[r] = torch.sort(torch.randn(K, generator=g) * mag).values
     return cb
 
 
@@ -83,3 +92,29 @@ def test_codebook_sizes_and_shapes(vqx, K, rows, cols):
     for dt in (torch.float32, torch.bfloat16):
         dec = Q.codebook_decode(codes, cb.cuda(), dt)
         assert torch.equal(dec.cpu().float(), R.codebook_decode_rows(want, cb))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [2, 16, 256])
+def test_codebook_subnormals_and_signed_zeros(vqx, K):
+    """Codebooks whose entries straddle zero at subnormal magnitudes, and
+    inputs that round to bf16 subnormals, signed zeros, huge values and
+    NaNs: the fp32 -> bf16 rounding of the input and the threshold
+    comparisons must stay exact down to the smallest subnormal."""
+    g = torch.Generator().manual_seed(77 + K)
+    rows, cols = 24, 2048
+    tiny = 2.0 ** -130
+    base = torch.sort(torch.randn(rows, K, generator=g), dim=1).values
+    cb = base * tiny                                  # all entries subnormal
+    cb[rows // 2:] = base[rows // 2:]                 # ordinary rows for contrast
+    cb[1] = torch.linspace(-3 * tiny, 3 * tiny, K)    # evenly spaced across zero
+    x = torch.randn(rows, cols, generator=g) * tiny * 4
+    x[:, :8] = torch.tensor([0.0, -0.0, tiny, -tiny, 2.0 ** -149, -(2.0 ** -149), 3e38, -3e38])
+    x[:, 8] = float("nan")
+    # fp32 values just around bf16 rounding boundaries among subnormals
+    m = torch.randint(0, 1 << 23, (rows, 64), generator=g, dtype=torch.int64)
+    x[:, 64:128] = (m | 0x8000).to(torch.int32).view(torch.float32)
+    x[:, 128:192] = -((m & ~0xFFFF) | 0x8000).to(torch.int32).view(torch.float32)
+    codes = Q.codebook_encode(x.cuda(), cb.cuda())
+    want = R.codebook_encode_rows(x, cb)
+    assert torch.equal(codes.cpu().long(), want)

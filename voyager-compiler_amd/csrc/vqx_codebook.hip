@@ -40,29 +40,62 @@ __device__ __forceinline__ uint32_t nearest_sorted(const float* cb, int K, float
 __device__ __forceinline__ uint32_t bf16_key(uint32_t h) { return (h & 0x8000u) ? (h ^ 0xFFFFu) : (h | 0x8000u); }
 __device__ __forceinline__ uint32_t key_bf16(uint32_t k) { return (k & 0x8000u) ? (k & 0x7FFFu) : (k ^ 0xFFFFu); }
 
-// The code of a bf16 value under the row's codebook is non-decreasing in the
-// value, so it is the number of decision thresholds at or below its key:
-// t[i] = the smallest key whose code exceeds i (i = 0 .. K-2).  With a =
-// cb[i] and b the first later entry above a (duplicates of a never win: the
-// lowest index does), code(v) > i exactly when fp32 |b - v| < |v - a|, i.e.
-// fl(b - v) < fl(v - a), also outside [a, b] (and for the clamped values
-// beyond the codebook's ends); that predicate is monotone in v, so t[i] is a
-// binary search over the bf16 keys around [a, b].  No later entry above a:
-// no threshold (0x10000, above every key).
-__device__ uint32_t code_threshold(const float* cb, int K, int i) {
+// Decision thresholds.  With v clamped into [c[0], c[K-1]] and d_j =
+// |fl(v - c_j)| the reference's distance to entry j, the code is the first
+// index of the smallest d_j.  If every two distinct neighbouring entries differ
+// by at least four ulps of the row's range R = c[K-1] - c[0] (no two distinct
+// entries on one side of v can then round to equal distances), the code is
+// non-decreasing in v and exceeds i exactly when d_b < d_a, with a = c[i] and
+// b the first later entry above a (duplicates of a never win: the lowest index
+// does).  That predicate is false up to a, true from b on and monotone in
+// between, so the code is the number of thresholds at or below the value's
+// key, t[i] = the smallest key with d_b < d_a, found by binary search over the
+// bf16 keys.  No later entry above a: no threshold (0x10000, above every
+// key).  A row that fails the gap condition (entries closer than the fp32
+// resolution of its distances, where rounded distances tie and the code need
+// not be monotone) is encoded by nearest_sorted instead.
+
+// Smallest gap between distinct entries under which the threshold search is
+// exact (+Inf when the range is not finite: every pair fails).
+__device__ __forceinline__ float exact_gap(float lo, float hi) {
+  const float r = hi - lo;
+  if (!(r < __builtin_huge_valf())) return __builtin_huge_valf();
+  const uint32_t e = f2u(r) >> 23;  // r >= 0: biased exponent
+  const float ulp = e > 23 ? u2f((e - 23) << 23) : u2f(1u << (e > 0 ? e - 1 : 0));
+  return 4.0f * ulp;
+}
+
+// Threshold i of the row; clears ok when the pair (a, b) is closer than gap.
+__device__ uint32_t code_threshold(const float* cb, int K, int i, float gap, bool& ok) {
   const float a = cb[i];
   int j = i + 1;
   while (j < K && !(cb[j] > a)) ++j;
   if (j == K) return 0x10000u;
   const float b = cb[j];
+  if (!(b - a >= gap)) ok = false;
+  const float vmin = cb[0], vmax = cb[K - 1];
   auto closer_to_b = [&](int k) {
     float v = bf2f(key_bf16((uint32_t)k));
-    return (b - v) < (v - a);
+    v = v < vmin ? vmin : (v > vmax ? vmax : v);
+    return __builtin_fabsf(b - v) < __builtin_fabsf(v - a);
   };
-  // closer_to_b(lo) is false (lo is below a), closer_to_b(hi) true (above b)
-  int lo = (int)bf16_key(f2bf(a)) - 2, hi = (int)bf16_key(f2bf(b)) + 2;
-  lo = lo < 0x7F ? 0x7F : lo;        // -Inf
-  hi = hi > 0xFF80 ? 0xFF80 : hi;    // +Inf
+  // Invariant: closer_to_b(lo) is false, closer_to_b(hi) true.  The switch
+  // usually sits within a key or two of the midpoint, so a bracket of the
+  // midpoint's key is tried first (it checks itself); where fp32 absorption
+  // moves the switch away from the midpoint (entries of opposite signs close
+  // to zero) the bracket fails and the search covers [a, b]: lo below a
+  // (or -Inf), hi above b (or +Inf, which clamps to c[K-1] >= b).
+  const int km = (int)bf16_key(f2bf(0.5f * a + 0.5f * b));
+  int lo, hi;
+  if (km - 2 >= 0x7F && km + 2 <= 0xFF80 && !closer_to_b(km - 2) && closer_to_b(km + 2)) {
+    lo = km - 2;
+    hi = km + 2;
+  } else {
+    lo = (int)bf16_key(f2bf(a)) - 2;
+    hi = (int)bf16_key(f2bf(b)) + 2;
+    lo = lo < 0x7F ? 0x7F : lo;      // -Inf
+    hi = hi > 0xFF80 ? 0xFF80 : hi;  // +Inf
+  }
   while (lo + 1 < hi) {
     int mid = (lo + hi) >> 1;
     if (closer_to_b(mid)) hi = mid; else lo = mid;
@@ -76,14 +109,36 @@ __device__ uint32_t code_threshold(const float* cb, int K, int i) {
 constexpr int kCbChunk = 1024;  // elements per wave chunk
 constexpr int kCbMaxK = 256;    // entries per row, one per thread of the workgroup
 
-// Node of sorted threshold j (0-based) in the breadth-first (Eytzinger) layout
-// of a complete search tree with 2^L - 1 nodes: node 1 is the root, the
-// children of node i are 2i and 2i + 1.  The in-order rank j + 1 =
-// (2m + 1) 2^h puts it at height h, i.e. depth L - 1 - h, m-th from the left.
-__device__ __forceinline__ uint32_t eytzinger_node(uint32_t j, int L) {
+// Search tree of the decision thresholds.  A row with 2^L - 1 thresholds
+// (L = 0 .. 8) uses the top of a breadth-first (Eytzinger) tree of 255 slots:
+// slot n has children 2n and 2n + 1, the root sits at slot 2^(8 - L), and L
+// steps n -> 2n + (threshold(n) <= v) end at slot 256 + code, so the code is
+// the low byte of the final slot.  Sorted threshold j has in-order rank
+// j + 1 = (2m + 1) 2^h: height h, m-th of its level, slot 2^(7 - h) + m.
+// Each level's slots are contiguous, so a level's reads hit distinct LDS
+// banks down to 64 slots.
+__device__ __forceinline__ uint32_t tree_slot(uint32_t j) {
   const uint32_t r = j + 1;
   const int h = __builtin_ctz(r);
-  return (1u << (L - 1 - h)) + (r >> (h + 1));
+  return (1u << (7 - h)) + (r >> (h + 1));
+}
+
+// Threshold key as a value for fp32 comparisons with the bf16 input value:
+// keys order like values except that -0 sits just below +0, and no threshold
+// separates -0 from +0 (both are at the same distance from every entry), so
+// key(t) <= key(v) is t <= v; "no threshold" is NaN, below nothing, and a NaN
+// input is below every threshold (code 0, the reference's NaN code).
+__device__ __forceinline__ float threshold_value(uint32_t key) {
+  return key > 0xFFFFu ? u2f(0x7FC00000u) : bf2f(key_bf16(key));
+}
+
+typedef __attribute__((address_space(3))) const float lds_cf32;
+__device__ __forceinline__ float lds_f32(uint32_t byte_addr) { return *(lds_cf32*)(size_t)byte_addr; }
+
+// Low bytes of four words, packed a | b << 8 | c << 16 | d << 24.
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_amdgcn_perm(__builtin_amdgcn_perm(d, c, 0x0C0C0400u), __builtin_amdgcn_perm(b, a, 0x0C0C0400u),
+                               0x05040100u);
 }
 
 template <typename T>
@@ -116,32 +171,44 @@ __device__ __forceinline__ void wave_lds_sync() {
 // streams are the 1024-element chunks of those rows in order, in two register
 // buffers used in turn: the next item's load is issued before the current one
 // is encoded, also across a row boundary, so loads stay in flight while a
-// row's search table is built.  The table: the row's K - 1 decision
-// thresholds, padded with ~0 to 2^LOGP - 1, in breadth-first order in the
-// wave's LDS slice, so each level of the search reads one contiguous run of
-// nodes (distinct banks down to 64 nodes); the LOGP-step search is unrolled,
-// letting a lane's 16 searches overlap.  Row elements past the last whole
-// chunk are encoded one per lane.
+// row's search tree is built.  The tree (see tree_slot) holds the row's K - 1
+// decision thresholds, padded with "no threshold" to 2^LOGP - 1, in the
+// wave's 1 KiB LDS slice.  The search walks LDS byte addresses A = B + 4n
+// (B: the slice, 1 KiB aligned): a step is A -> 2A - B + 4c, the root level
+// compares against a register copy, and the last step yields
+// A / 2 + c = B / 2 + 256 + code, whose low byte is the code.  fp32 inputs
+// are rounded to bf16 two at a time (v_cvt_pk_bf16_f32: round to nearest
+// even, NaN kept, subnormals kept under the kernel's f32 denormal mode).
 template <typename T, int LOGP>
 __global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
                                                         const float* __restrict__ cb, int K,
                                                         uint8_t* __restrict__ codes) {
-  constexpr int P = 1 << LOGP;
-  constexpr int kSlice = P > 1 ? P : 2;
+  constexpr uint32_t kRoot = 1u << (8 - LOGP);
+  __shared__ __attribute__((aligned(1024))) float s_tw[4][256];  // slot n of wave w at s_tw[w][n]
   __shared__ float s_cbw[4][kCbMaxK];
-  __shared__ uint32_t s_tw[4][kSlice];  // node i at s_t[i], i = 1 .. P - 1
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   float* s_cb = s_cbw[wave];
-  uint32_t* s_t = s_tw[wave];
+  float* s_t = s_tw[wave];
+  const uint32_t B = (uint32_t)(size_t)(lds_cf32*)s_t;
+  const uint32_t kStep0 = 0u - B, kStep1 = 4u - B;               // 2A + these: A -> B + 4(2n + c)
+  const uint32_t kLeft = B + 8u * kRoot, kRight = B + 8u * kRoot + 4u;  // A after the root level
   const int64_t gw = (int64_t)blockIdx.x * 4 + wave, nw = (int64_t)gridDim.x * 4;
   const int64_t nchunk = cols / kCbChunk, full = nchunk * kCbChunk;
-  auto encode = [&](float v) -> uint32_t {
-    const uint32_t key = bf16_key(f2bf(v));
-    uint32_t i = 1;
+  float root = 0.0f;
+  bool tree = true;  // the row's tree is exact (else nearest_sorted)
+  // a word whose low byte is the code of bf16 value f
+  auto search = [&](float f) -> uint32_t {
+    if constexpr (LOGP == 0) {
+      return 0u;
+    } else if constexpr (LOGP == 1) {
+      return root <= f ? 1u : 0u;
+    } else {
+      uint32_t A = root <= f ? kRight : kLeft;
 #pragma unroll
-    for (int l = 0; l < LOGP; ++l) i = 2 * i + (s_t[i] <= key ? 1u : 0u);
-    return v != v ? 0u : i - (uint32_t)P;
+      for (int l = 1; l < LOGP - 1; ++l) A = (A << 1) + (lds_f32(A) <= f ? kStep1 : kStep0);
+      return (A >> 1) + (lds_f32(A) <= f ? 1u : 0u);
+    }
   };
   auto load_cb = [&](int64_t r, float (&c)[4]) {
 #pragma unroll
@@ -152,15 +219,19 @@ __global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x,
   int64_t r = gw, c = 0;  // current item: chunk c of row r
   // one item: encode chunk (r, c) from cur after loading the next item into nxt
   auto step = [&](const float (&cur)[16], float (&nxt)[16]) {
-    if (c == 0) {  // new row: its table from the prefetched codebook
+    if (c == 0) {  // new row: its tree from the prefetched codebook
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (lane + 64 * j < K) s_cb[lane + 64 * j] = cbn[j];
       wave_lds_sync();
-      for (int j = lane; j < P - 1; j += 64)
-        s_t[eytzinger_node(j, LOGP)] = j < K - 1 ? code_threshold(s_cb, K, j) : 0xFFFFFFFFu;
+      const float gap = exact_gap(s_cb[0], s_cb[K - 1]);
+      bool ok = true;
+      for (int j = lane; j < (1 << LOGP) - 1; j += 64)
+        s_t[tree_slot(j)] = threshold_value(j < K - 1 ? code_threshold(s_cb, K, j, gap, ok) : 0x10000u);
+      tree = __builtin_amdgcn_ballot_w64(!ok) == 0;
       load_cb(r + nw, cbn);
       wave_lds_sync();
+      if constexpr (LOGP > 0) root = s_t[kRoot];
     }
     const bool last = c + 1 >= nchunk;
     const int64_t rn = last ? r + nw : r, cn = last ? 0 : c + 1;
@@ -171,19 +242,32 @@ __global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x,
       uint8_t* cr = codes + r * cols + c * kCbChunk;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        uint32_t c0 = encode(cur[4 * q]), c1 = encode(cur[4 * q + 1]), c2 = encode(cur[4 * q + 2]),
-                 c3 = encode(cur[4 * q + 3]);
-        __builtin_nontemporal_store(c0 | (c1 << 8) | (c2 << 16) | (c3 << 24),
-                                    reinterpret_cast<uint32_t*>(cr + q * 256 + lane * 4));
+        float f[4];
+        if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+          for (int k = 0; k < 4; k += 2) {
+            const uint32_t p = pack_bf16x2(cur[4 * q + k], cur[4 * q + k + 1]);
+            f[k] = u2f(p << 16);
+            f[k + 1] = u2f(p & 0xFFFF0000u);
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) f[k] = cur[4 * q + k];  // bf16 values already
+        }
+        const uint32_t w = tree ? pack_low_bytes(search(f[0]), search(f[1]), search(f[2]), search(f[3]))
+                                : pack_low_bytes(nearest_sorted(s_cb, K, f[0]), nearest_sorted(s_cb, K, f[1]),
+                                                 nearest_sorted(s_cb, K, f[2]), nearest_sorted(s_cb, K, f[3]));
+        __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(cr + q * 256 + lane * 4));
       }
     }
     if (last) {  // row done: its tail
       const T* xr = x + r * cols;
       for (int64_t i = full + lane; i < cols; i += 64) {
-        float xv = std::is_same<T, float>::value ? (float)xr[i] : u2f((uint32_t)((const uint16_t*)xr)[i] << 16);
-        codes[r * cols + i] = (uint8_t)encode(xv);
+        float xv = std::is_same<T, float>::value ? u2f(pack_bf16x2((float)xr[i], 0.0f) << 16)
+                                                 : u2f((uint32_t)((const uint16_t*)xr)[i] << 16);
+        codes[r * cols + i] = (uint8_t)(tree ? search(xv) : nearest_sorted(s_cb, K, xv));
       }
-      wave_lds_sync();  // all lanes are done with this row's table
+      wave_lds_sync();  // all lanes are done with this row's tree
     }
     r = rn;
     c = cn;
