@@ -290,14 +290,14 @@ def _cpu_model():
 # Kernel that dominates each config's launch (rocprofv3 names it this way).
 DOMINANT = {
     "c1": "fq_lut_kernel<float, 1>",
-    "c2": "mx_lut_kernel<4, 4, true, 0>",
+    "c2": "mx_lut_kernel<4, 4, true, 0, true>",
     "c2_decode": "decode_group_kernel<unsigned short, 4, 4>",
-    "c3_e4m3": "mx_lut_kernel<8, 2, false, 0>",
-    "c3_e3m2": "mx_lut_kernel<6, 2, false, 0>",
-    "c3_e2m1": "mx_lut_kernel<4, 2, false, 0>",
-    "c3_e4m3_fq": "mx_lut_kernel<0, 2, false, 2>",
-    "c4_k16": "cb_encode_kernel<float>",
-    "c4_k256": "cb_encode_kernel<float>",
+    "c3_e4m3": "mx_lut_kernel<8, 2, false, 0, true>",
+    "c3_e3m2": "mx_lut_kernel<6, 2, false, 0, false>",
+    "c3_e2m1": "mx_lut_kernel<4, 2, false, 0, true>",
+    "c3_e4m3_fq": "mx_lut_kernel<0, 2, false, 2, false>",
+    "c4_k16": "cb_encode_kernel<float, 4>",
+    "c4_k256": "cb_encode_kernel<float, 8>",
     "c4_k16_decode": "cb_decode_kernel<float>",
     "c5": "nf4_gemm_kernel",
 }

@@ -353,17 +353,21 @@ __device__ __forceinline__ float block_scale_pow2_lds(uint32_t amax, int shift, 
 }
 
 // WANT: bit 0 = reference quantize() values, bit 1 = fake-quant values.
+// CT: packed codes only (WANT 0, CB 4 or 8), read from the codes-only LDS
+// table (lut_codes_to_lds) and packed with ORs and byte permutes.
 //
 // Fast path per element: the quotient (one multiply; for absmax scales a
 // reciprocal multiply whose rare near-midpoint cases are redone by IEEE
 // division for the whole group), its magnitude clamped into the table range
 // [T0 - 1, T1] with v_med3_f32 (clamping before the bf16 rounding equals
 // clamping after it, the bounds being bf16 values), one compare against a
-// uniform threshold for the sign, and one LDS read at an address formed from
-// the clamped quotient's bits, giving value and code together.
-template <int CB, int LPB, bool ABSMAX, int WANT>
+// uniform threshold picking the sign's table base, and one LDS read at that
+// base plus the clamped quotient's bf16 bits, scaled to the entry size.
+template <int CB, int LPB, bool ABSMAX, int WANT, bool CT>
 __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict__ x, int64_t ngroups,
                                                      ScaleParams sp, LutView lv, MxOut out) {
+  static_assert(!CT || (WANT == 0 && (CB == 4 || CB == 8)), "code tables serve packed 4- or 8-bit codes only");
+  constexpr int SH = (CT && CB == 4) ? 3 : 2;  // log2 of the LDS bytes per magnitude
   extern __shared__ uint32_t lds_lut[];
   __shared__ uint8_t thr8[256];
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -377,12 +381,19 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
   }
   if constexpr (!ABSMAX)
     for (int i = threadIdx.x; i < 256; i += blockDim.x) thr8[i] = (uint8_t)log2_step_threshold(i);
-  LutLds t = lut_to_lds(lv.blob, lv.len, lds_lut);
+  LutLds t;
+  if constexpr (CT)
+    t = lut_codes_to_lds<CB>(lv.blob, lv.len, lds_lut);
+  else
+    t = lut_to_lds(lv.blob, lv.len, lds_lut);
   const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
-  // LDS byte addresses such that entry(h) = base + 4 h for h in [T0 - 1, T1]
-  const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - 4u * t.t0m1;
-  const uint32_t nb = pb + 4u * t.len;
+  // LDS byte addresses such that entry(h) = base + (h << SH) for h in [T0 - 1, T1]
+  const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - (t.t0m1 << SH);
+  const uint32_t nb = pb + (t.len << SH);
   const float lo = u2f(t.t0m1 << 16), hi = u2f(t.t1 << 16);
+  // absmax: a power-of-two quant_max divides exactly as a multiply
+  const bool qmax_pow2 = (f2u(sp.quant_max) & 0x807FFFFFu) == 0 && ((f2u(sp.quant_max) >> 23) - 1u) < 253u;
+  const float qmax_rcp = u2f((254u - (f2u(sp.quant_max) >> 23)) << 23);
   for (; g < ngroups; g += stride) {
     uint32_t w[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
     if (g + stride < ngroups) {  // prefetch the next group
@@ -395,10 +406,16 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
     for (int j = 0; j < 8; ++j) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, w[j] & 0x7FFF7FFFu));
     uint32_t amax = block_max<LPB>((uint32_t)(m2.x > m2.y ? m2.x : m2.y));
     float s;
-    if constexpr (ABSMAX)
-      s = block_scale_bf16<true>(amax, sp);
-    else
+    if constexpr (ABSMAX) {
+      if (qmax_pow2 && !sp.scale_qmap) {
+        const float sc = bf2f(f2bf(u2f(amax << 16) * qmax_rcp));
+        s = sc > 0.0f ? sc : 1.0f;
+      } else {
+        s = block_scale_bf16<true>(amax, sp);
+      }
+    } else {
       s = block_scale_pow2_lds(amax, sp.shift, thr8);
+    }
     uint32_t sb = f2u(s);
     uint32_t sE = (sb >> 23) & 0xFFu;
     const float amaxf = u2f(amax << 16);
@@ -427,23 +444,24 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
     }
     uint32_t ent[16];
     if (fast) {
+      uint32_t addr[16];
       if constexpr (!ABSMAX) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
           float qc = __builtin_amdgcn_fmed3f(__builtin_fabsf(u2f(xb) * rcp), lo, hi);
-          ent[j] = *(lds_cu32*)(size_t)((xb > nthr ? nb : pb) + (f2u(qc) >> 14));
+          addr[j] = (xb > nthr ? nb : pb) + (f2u(qc) >> (16 - SH));  // qc is a bf16 value
         }
       } else {
         float q[16];
-        bool tie = false;
+        uint32_t near = 0xFFFFFFFFu;  // min over the group of (low 16 bits of q) - 0x7FFC
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
           q[j] = u2f(xb) * rcp;
-          tie |= near_midpoint(q[j]);
+          near = umin32(near, (f2u(q[j]) & 0xFFFFu) - 0x7FFCu);
         }
-        if (tie) {  // rare: redo the near-midpoint quotients by IEEE division
+        if (near <= 8u) {  // rare: redo the near-midpoint quotients by IEEE division
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
@@ -454,16 +472,20 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
         for (int j = 0; j < 16; ++j) {
           // clamped magnitudes are normal and finite: hardware RNE is exact
           uint32_t h = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(q[j]), lo, hi), 0.0f);
-          ent[j] = *(lds_cu32*)(size_t)((f2u(q[j]) > nthr ? nb : pb) + 4u * h);
+          addr[j] = (f2u(q[j]) > nthr ? nb : pb) + (h << SH);
         }
       }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ent[j] = *(lds_cu32*)(size_t)(addr[j] + ((CT && CB == 4 && (j & 1)) ? 4u : 0u));
     } else {
       // scale 1 (NaN block), Inf, subnormal or extreme: exact division and
       // the full table
 #pragma unroll 1
       for (int j = 0; j < 16; ++j) {
         uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
-        ent[j] = full[f2bf(u2f(xb) / s)];
+        uint32_t e = full[f2bf(u2f(xb) / s)];
+        if constexpr (CT) e = (CB == 4 && (j & 1)) ? (e >> 16) << 4 : e >> 16;
+        ent[j] = e;
       }
     }
     if constexpr (WANT != 0) {
@@ -478,7 +500,18 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
       if constexpr (WANT & 1) BT<uint16_t>::store16(static_cast<uint16_t*>(out.qvals) + g * 16, qv);
       if constexpr (WANT & 2) BT<uint16_t>::store16(static_cast<uint16_t*>(out.fq) + g * 16, fv);
     }
-    if constexpr (CB > 0) {
+    if constexpr (CT && CB == 4) {
+      uint32_t b[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) b[k] = ent[2 * k] | ent[2 * k + 1];
+      u32x2 cw = {pack_low_bytes(b[0], b[1], b[2], b[3]), pack_low_bytes(b[4], b[5], b[6], b[7])};
+      st_nt(reinterpret_cast<u32x2*>(static_cast<uint8_t*>(out.codes) + g * 8), cw);
+    } else if constexpr (CT) {
+      u32x4 cw = {pack_low_bytes(ent[0], ent[1], ent[2], ent[3]), pack_low_bytes(ent[4], ent[5], ent[6], ent[7]),
+                  pack_low_bytes(ent[8], ent[9], ent[10], ent[11]),
+                  pack_low_bytes(ent[12], ent[13], ent[14], ent[15])};
+      st_nt(reinterpret_cast<u32x4*>(static_cast<uint8_t*>(out.codes) + g * 16), cw);
+    } else if constexpr (CB > 0) {
       uint32_t code[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) code[j] = ent[j] >> 16;
@@ -497,10 +530,19 @@ template <int CB, int LPB, bool ABSMAX, int WANT>
 static int launch_lut_k(const uint16_t* x, int64_t ngroups, const ScaleParams& sp, const LutView& lv,
                         const MxOut& out, hipStream_t st) {
   const int bs = 256;
-  size_t lds = sizeof(uint32_t) * 2 * lv.len;
-  auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT>;
-  unsigned grid = persistent_grid((const void*)k, bs, lds, ngroups);
-  hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out);
+  // codes-only outputs use the code table where it fits in 64 KiB
+  constexpr bool kCodes = WANT == 0 && (CB == 4 || CB == 8);
+  if (kCodes && (int64_t)lv.len * (CB == 4 ? 16 : 8) <= 65536) {
+    auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT, kCodes>;
+    size_t lds = (size_t)lv.len * (CB == 4 ? 16 : 8);
+    unsigned grid = persistent_grid((const void*)k, bs, lds, ngroups);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out);
+  } else {
+    auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT, false>;
+    size_t lds = sizeof(uint32_t) * 2 * lv.len;
+    unsigned grid = persistent_grid((const void*)k, bs, lds, ngroups);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out);
+  }
   return check_launch("mx_quantize(lut)");
 }
 

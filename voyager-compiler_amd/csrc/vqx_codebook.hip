@@ -135,12 +135,6 @@ __device__ __forceinline__ float threshold_value(uint32_t key) {
 typedef __attribute__((address_space(3))) const float lds_cf32;
 __device__ __forceinline__ float lds_f32(uint32_t byte_addr) { return *(lds_cf32*)(size_t)byte_addr; }
 
-// Low bytes of four words, packed a | b << 8 | c << 16 | d << 24.
-__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  return __builtin_amdgcn_perm(__builtin_amdgcn_perm(d, c, 0x0C0C0400u), __builtin_amdgcn_perm(b, a, 0x0C0C0400u),
-                               0x05040100u);
-}
-
 template <typename T>
 __device__ __forceinline__ void load_chunk(const T* xr, int64_t base, int lane, float (&v)[16]) {
 #pragma unroll

@@ -52,6 +52,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) {
   return a > b ? a : b;
 }
+__device__ __forceinline__ uint32_t umin32(uint32_t a, uint32_t b) {
+  return a < b ? a : b;
+}
 
 // Round-to-nearest-even fp32 -> bf16 pattern, every NaN to 0x7FC0.
 __device__ __forceinline__ uint32_t f2bf_dev(float f) { return f2bf(f); }
@@ -63,6 +66,12 @@ typedef float vqx_f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   vqx_f32x2 f = {a, b};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, vqx_bf16x2));
+}
+
+// Low bytes of four words, packed a | b << 8 | c << 16 | d << 24 (three v_perm).
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_amdgcn_perm(__builtin_amdgcn_perm(d, c, 0x0C0C0400u), __builtin_amdgcn_perm(b, a, 0x0C0C0400u),
+                               0x05040100u);
 }
 
 // Exact fp16 <-> fp32 conversions in integer arithmetic (subnormals and signed

@@ -62,6 +62,35 @@ __device__ __forceinline__ LutLds lut_to_lds(const uint32_t* blob, int len, uint
   return v;
 }
 
+// Codes-only copy of the two signed tables into LDS, for kernels that write
+// packed codes and nothing else: CB 8 keeps one word per magnitude (the
+// code); CB 4 keeps two, the code and the code shifted into the high nibble,
+// so a byte of two codes is the OR of an even and an odd element's words.
+// Call with all threads of the workgroup; includes the barrier.
+template <int CB>
+__device__ __forceinline__ LutLds lut_codes_to_lds(const uint32_t* blob, int len, uint32_t* lds) {
+  static_assert(CB == 4 || CB == 8, "code tables hold 4- or 8-bit codes");
+  const uint32_t* src = blob + kLutHeaderWords;
+  for (int i = threadIdx.x; i < 2 * len; i += blockDim.x) {
+    const uint32_t c = src[i] >> 16;
+    if constexpr (CB == 4) {
+      lds[2 * i] = c;
+      lds[2 * i + 1] = c << 4;
+    } else {
+      lds[i] = c;
+    }
+  }
+  __syncthreads();
+  LutLds v;
+  v.pos = lds;
+  v.len = (uint32_t)len;
+  v.t0m1 = blob[kLutT0m1];
+  v.t1 = blob[kLutT1];
+  v.s = blob[kLutS];
+  v.zsign = blob[kLutZeroSign];
+  return v;
+}
+
 // Entry for a bf16 pattern whose magnitude is below S.
 __device__ __forceinline__ uint32_t lut_index(const LutLds& t, uint32_t h) {
   uint32_t a = h & 0x7FFFu;
