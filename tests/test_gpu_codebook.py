@@ -118,3 +118,20 @@ def test_codebook_subnormals_and_signed_zeros(vqx, K):
     codes = Q.codebook_encode(x.cuda(), cb.cuda())
     want = R.codebook_encode_rows(x, cb)
     assert torch.equal(codes.cpu().long(), want)
+
+
+@pytest.mark.gpu
+def test_codebook_tied_distances_row_all_patterns(vqx):
+    """A row whose entries span 40 binades: values near 258 are equally far
+    (in fp32) from several entries, so the decision-threshold count would be
+    wrong there; the kernel must notice and encode the row exactly.  Every
+    bf16 pattern is encoded, next to an ordinary row."""
+    wide = torch.tensor([-4.5617120e+08, -1.7806498e+04, -4.6088116e+02, -4.8019073e+01, -4.9426060e-02,
+                         -6.8074833e-03, -2.1707090e-03, -9.7630935e-04, -5.2784779e-04, -8.3647523e-05,
+                         -2.4869628e-06, -1.9292422e-07, -5.5566971e-08, 4.8861853e-06, 1.9638399e-05,
+                         4.0374794e-05, 7.8944244e+02], dtype=torch.float32)
+    cb = torch.stack([wide, torch.linspace(-2, 2, 17)])
+    pats = (torch.arange(0x10000, dtype=torch.int32) << 16).view(torch.float32)
+    x = torch.stack([pats, pats])
+    codes = Q.codebook_encode(x.cuda(), cb.cuda())
+    assert torch.equal(codes.cpu().long(), R.codebook_encode_rows(x, cb))

@@ -354,7 +354,7 @@ __device__ __forceinline__ float block_scale_pow2_lds(uint32_t amax, int shift, 
 
 // WANT: bit 0 = reference quantize() values, bit 1 = fake-quant values.
 // CT: packed codes only (WANT 0, CB 4 or 8), read from the codes-only LDS
-// table (lut_codes_to_lds) and packed with ORs and byte permutes.
+// tables (lut_codes_to_lds) and packed with ORs and byte permutes.
 //
 // Fast path per element: the quotient (one multiply; for absmax scales a
 // reciprocal multiply whose rare near-midpoint cases are redone by IEEE
@@ -367,7 +367,6 @@ template <int CB, int LPB, bool ABSMAX, int WANT, bool CT>
 __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict__ x, int64_t ngroups,
                                                      ScaleParams sp, LutView lv, MxOut out) {
   static_assert(!CT || (WANT == 0 && (CB == 4 || CB == 8)), "code tables serve packed 4- or 8-bit codes only");
-  constexpr int SH = (CT && CB == 4) ? 3 : 2;  // log2 of the LDS bytes per magnitude
   extern __shared__ uint32_t lds_lut[];
   __shared__ uint8_t thr8[256];
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -387,9 +386,11 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
   else
     t = lut_to_lds(lv.blob, lv.len, lds_lut);
   const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
-  // LDS byte addresses such that entry(h) = base + (h << SH) for h in [T0 - 1, T1]
-  const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - (t.t0m1 << SH);
-  const uint32_t nb = pb + (t.len << SH);
+  // LDS byte addresses such that entry(h) = base + 4 h for h in [T0 - 1, T1];
+  // nb passes through readfirstlane so that the compiler keeps the per-element
+  // form select(pb, nb) + 4 h (one v_cndmask, one v_lshl_add)
+  const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - 4u * t.t0m1;
+  const uint32_t nb = __builtin_amdgcn_readfirstlane(pb + 4u * t.len);
   const float lo = u2f(t.t0m1 << 16), hi = u2f(t.t1 << 16);
   // absmax: a power-of-two quant_max divides exactly as a multiply
   const bool qmax_pow2 = (f2u(sp.quant_max) & 0x807FFFFFu) == 0 && ((f2u(sp.quant_max) >> 23) - 1u) < 253u;
@@ -450,7 +451,7 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
         for (int j = 0; j < 16; ++j) {
           uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
           float qc = __builtin_amdgcn_fmed3f(__builtin_fabsf(u2f(xb) * rcp), lo, hi);
-          addr[j] = (xb > nthr ? nb : pb) + (f2u(qc) >> (16 - SH));  // qc is a bf16 value
+          addr[j] = (xb > nthr ? nb : pb) + (f2u(qc) >> 14);  // qc is a bf16 value
         }
       } else {
         float q[16];
@@ -472,11 +473,12 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
         for (int j = 0; j < 16; ++j) {
           // clamped magnitudes are normal and finite: hardware RNE is exact
           uint32_t h = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(q[j]), lo, hi), 0.0f);
-          addr[j] = (f2u(q[j]) > nthr ? nb : pb) + (h << SH);
+          addr[j] = (f2u(q[j]) > nthr ? nb : pb) + 4u * h;
         }
       }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) ent[j] = *(lds_cu32*)(size_t)(addr[j] + ((CT && CB == 4 && (j & 1)) ? 4u : 0u));
+      for (int j = 0; j < 16; ++j)
+        ent[j] = *(lds_cu32*)(size_t)(addr[j] + ((CT && CB == 4 && (j & 1)) ? (uint32_t)kCodeCopy2 : 0u));
     } else {
       // scale 1 (NaN block), Inf, subnormal or extreme: exact division and
       // the full table
@@ -530,11 +532,11 @@ template <int CB, int LPB, bool ABSMAX, int WANT>
 static int launch_lut_k(const uint16_t* x, int64_t ngroups, const ScaleParams& sp, const LutView& lv,
                         const MxOut& out, hipStream_t st) {
   const int bs = 256;
-  // codes-only outputs use the code table where it fits in 64 KiB
+  // codes-only outputs use the code tables where they fit
   constexpr bool kCodes = WANT == 0 && (CB == 4 || CB == 8);
-  if (kCodes && (int64_t)lv.len * (CB == 4 ? 16 : 8) <= 65536) {
+  if (kCodes && (CB == 8 || (int64_t)lv.len * 8 <= kCodeCopy2)) {
     auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT, kCodes>;
-    size_t lds = (size_t)lv.len * (CB == 4 ? 16 : 8);
+    size_t lds = CB == 4 ? kCodeCopy2 + (size_t)lv.len * 8 : (size_t)lv.len * 8;
     unsigned grid = persistent_grid((const void*)k, bs, lds, ngroups);
     hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out);
   } else {

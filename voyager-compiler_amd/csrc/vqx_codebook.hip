@@ -52,8 +52,9 @@ __device__ __forceinline__ uint32_t key_bf16(uint32_t k) { return (k & 0x8000u) 
 // key, t[i] = the smallest key with d_b < d_a, found by binary search over the
 // bf16 keys.  No later entry above a: no threshold (0x10000, above every
 // key).  A row that fails the gap condition (entries closer than the fp32
-// resolution of its distances, where rounded distances tie and the code need
-// not be monotone) is encoded by nearest_sorted instead.
+// resolution of its distances, where several entries round to the same
+// distance and counting pairwise decisions misses the first of them) is
+// encoded by nearest_sorted instead.
 
 // Smallest gap between distinct entries under which the threshold search is
 // exact (+Inf when the range is not finite: every pair fails).
@@ -165,7 +166,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 // streams are the 1024-element chunks of those rows in order, in two register
 // buffers used in turn: the next item's load is issued before the current one
 // is encoded, also across a row boundary, so loads stay in flight while a
-// row's search tree is built.  The tree (see tree_slot) holds the row's K - 1
+// row's search tree is built.  Rows and chunks are wave-uniform (the wave
+// index goes through readfirstlane), so the loop's branches are scalar.  The tree (see tree_slot) holds the row's K - 1
 // decision thresholds, padded with "no threshold" to 2^LOGP - 1, in the
 // wave's 1 KiB LDS slice.  The search walks LDS byte addresses A = B + 4n
 // (B: the slice, 1 KiB aligned): a step is A -> 2A - B + 4c, the root level
@@ -230,9 +232,7 @@ __global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x,
     const bool last = c + 1 >= nchunk;
     const int64_t rn = last ? r + nw : r, cn = last ? 0 : c + 1;
     if (nchunk > 0) {
-      // past the wave's last item: reload the current one (a valid address)
-      const bool more = rn < rows;
-      load_chunk(x + (more ? rn : r) * cols, (more ? cn : c) * kCbChunk, lane, nxt);
+      if (rn < rows) load_chunk(x + rn * cols, cn * kCbChunk, lane, nxt);  // wave-uniform branch
       uint8_t* cr = codes + r * cols + c * kCbChunk;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -312,8 +312,7 @@ __global__ __launch_bounds__(256) void cb_decode_kernel(const uint8_t* __restric
     const bool last = c + 1 >= nchunk;
     const int64_t rn = last ? r + nw : r, cn = last ? 0 : c + 1;
     if (nchunk > 0) {
-      const bool more = rn < rows;
-      load(codes + (more ? rn : r) * cols + (more ? cn : c) * kCbChunk, nxt);
+      if (rn < rows) load(codes + rn * cols + cn * kCbChunk, nxt);  // wave-uniform branch
       T* orow = out + r * cols + c * kCbChunk;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
