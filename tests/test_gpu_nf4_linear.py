@@ -28,7 +28,8 @@ def decode_reference(codes_u8, scale_f32, N, K):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (256, 256, 512), (512, 384, 1024), (2048, 11008, 4096)])
+@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (256, 128, 128), (256, 128, 192), (256, 256, 320),
+                                   (256, 256, 512), (512, 384, 1024), (2048, 11008, 4096)])
 def test_nf4_linear_matches_reference(vqx, M, N, K):
     g = torch.Generator().manual_seed(M + N + K)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16)
