@@ -39,6 +39,10 @@ def parse():
     ap.add_argument("--only", default=None, help="comma list of config keys to run")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="only measure what HBM sustains on this box for each traffic mix, with 1 GiB working sets "
+                         "(beyond the 256 MiB MALL): torch's own copy, fill and read kernels, and the C3 e4m3 "
+                         "kernel on a 1 GiB input")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device-to-device copy of 512 MiB (5 times), the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -325,6 +329,51 @@ def measured_traffic(key):
         return None
 
 
+def hbm_ceiling(steps, warmup):
+    """HBM bandwidth by traffic mix with 1 GiB working sets, which the 256 MiB
+    MALL cannot hold: write only (torch fill_), 1:1 (torch copy_), and two
+    passes of this library's MX kernel over a bf16 16384x32768 input: E8M0
+    scales only (read-mostly: 2 B read, 1/32 B written per element) and the
+    C3 e4m3 quantize (2:1 read:write).  One JSON line."""
+    import torch
+
+    import __graft_entry__
+
+    n = 1 << 28  # 1 GiB of fp32
+    a = torch.empty(n, dtype=torch.float32, device="cuda").uniform_()
+    b = torch.empty_like(a)
+    res = {}
+
+    def run(name, fn, nbytes):
+        tm = time_config(torch, lambda: (fn(), 0)[1], steps, warmup)
+        ms = tm["kernel_ms_avg"]
+        res[name] = {"bytes": nbytes, "ms": ms, "GBps": nbytes / (ms * 1e-3) / 1e9,
+                     "frac_of_8TBps": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        print(f"[bench] hbm ceiling {name}: {ms * 1e3:.1f} us, {res[name]['GBps']:.0f} GB/s", file=sys.stderr,
+              flush=True)
+
+    run("write_1GiB (torch fill_)", lambda: b.fill_(1.0), 4 * n)
+    run("copy_1GiB_to_1GiB (torch copy_)", lambda: b.copy_(a), 8 * n)
+    del a, b
+    torch.cuda.empty_cache()
+    vqx = __graft_entry__.load_package()
+    L = vqx._lib
+    rows, cols = 16384, 32768
+    x = torch.empty(rows, cols, dtype=torch.bfloat16, device="cuda").normal_()
+    fmt = vqx.parse_format("fp8_e4m3")
+    desc = fmt.desc(x.device)
+    codes = torch.empty(rows * cols, dtype=torch.uint8, device="cuda")
+    e8 = torch.empty(rows, cols // 32, dtype=torch.uint8, device="cuda")
+    fn = L.load().vqx_mx_quantize
+    sargs = (L.ptr(x), L.BF16, rows, cols, 1, 32, L.ctypes.byref(desc), 0, 8, L.ctypes.c_float(448.0), None,
+             None, None, L.ptr(e8), None, None, None, 0, L.stream_of(x))
+    run("read_mostly_1GiB (vqx MX scales only)", lambda: fn(*sargs), rows * cols * 2 + e8.numel())
+    args = (L.ptr(x), L.BF16, rows, cols, 1, 32, L.ctypes.byref(desc), 0, 8, L.ctypes.c_float(448.0), None, None,
+            None, L.ptr(e8), None, None, L.ptr(codes), 0, L.stream_of(x))
+    run("c3_e4m3_kernel_1GiB_input", lambda: fn(*args), rows * cols * 3 + e8.numel())
+    print(json.dumps({"hbm_ceiling": res, "note": "1 GiB working sets, beyond the 256 MiB MALL"}))
+
+
 def calibrate_copy():
     import torch
 
@@ -342,6 +391,9 @@ def main():
     a = parse()
     if a.calibrate_copy:
         calibrate_copy()
+        return
+    if a.hbm_ceiling:
+        hbm_ceiling(a.steps, a.warmup)
         return
     if a.gpus != 1:
         print(json.dumps({"error": "bench.py runs on one GPU only: this build has no multi-GPU path "

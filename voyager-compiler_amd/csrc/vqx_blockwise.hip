@@ -337,6 +337,7 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v) {
 __device__ __forceinline__ bool near_midpoint(float q) { return (f2u(q) & 0xFFFFu) - 0x7FFCu <= 8u; }
 
 typedef __attribute__((address_space(3))) const uint32_t lds_cu32;
+typedef __attribute__((address_space(3))) const uint8_t lds_cu8;
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // Power-of-two block scale of a bf16 block (block_scale<uint16_t> mode 0)
@@ -386,11 +387,13 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
   else
     t = lut_to_lds(lv.blob, lv.len, lds_lut);
   const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
-  // LDS byte addresses such that entry(h) = base + 4 h for h in [T0 - 1, T1];
-  // nb passes through readfirstlane so that the compiler keeps the per-element
-  // form select(pb, nb) + 4 h (one v_cndmask, one v_lshl_add)
-  const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - 4u * t.t0m1;
-  const uint32_t nb = __builtin_amdgcn_readfirstlane(pb + 4u * t.len);
+  // LDS byte addresses such that entry(h) = base + ES h for h in [T0 - 1, T1]
+  // (ES = 4 bytes per entry, 1 for the code tables); nb passes through
+  // readfirstlane so that the compiler keeps the per-element form
+  // select(pb, nb) + ES h
+  constexpr uint32_t ES = CT ? 1u : 4u;
+  const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - ES * t.t0m1;
+  const uint32_t nb = __builtin_amdgcn_readfirstlane(pb + ES * t.len);
   const float lo = u2f(t.t0m1 << 16), hi = u2f(t.t1 << 16);
   // absmax: a power-of-two quant_max divides exactly as a multiply
   const bool qmax_pow2 = (f2u(sp.quant_max) & 0x807FFFFFu) == 0 && ((f2u(sp.quant_max) >> 23) - 1u) < 253u;
@@ -451,7 +454,7 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
         for (int j = 0; j < 16; ++j) {
           uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
           float qc = __builtin_amdgcn_fmed3f(__builtin_fabsf(u2f(xb) * rcp), lo, hi);
-          addr[j] = (xb > nthr ? nb : pb) + (f2u(qc) >> 14);  // qc is a bf16 value
+          addr[j] = (xb > nthr ? nb : pb) + ES * (f2u(qc) >> 16);  // qc is a bf16 value
         }
       } else {
         float q[16];
@@ -473,12 +476,16 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
         for (int j = 0; j < 16; ++j) {
           // clamped magnitudes are normal and finite: hardware RNE is exact
           uint32_t h = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(q[j]), lo, hi), 0.0f);
-          addr[j] = (f2u(q[j]) > nthr ? nb : pb) + 4u * h;
+          addr[j] = (f2u(q[j]) > nthr ? nb : pb) + ES * h;
         }
       }
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        ent[j] = *(lds_cu32*)(size_t)(addr[j] + ((CT && CB == 4 && (j & 1)) ? (uint32_t)kCodeCopy2 : 0u));
+      for (int j = 0; j < 16; ++j) {
+        if constexpr (CT)
+          ent[j] = *(lds_cu8*)(size_t)(addr[j] + ((CB == 4 && (j & 1)) ? (uint32_t)kCodeCopy2 : 0u));
+        else
+          ent[j] = *(lds_cu32*)(size_t)addr[j];
+      }
     } else {
       // scale 1 (NaN block), Inf, subnormal or extreme: exact division and
       // the full table
@@ -534,9 +541,9 @@ static int launch_lut_k(const uint16_t* x, int64_t ngroups, const ScaleParams& s
   const int bs = 256;
   // codes-only outputs use the code tables where they fit
   constexpr bool kCodes = WANT == 0 && (CB == 4 || CB == 8);
-  if (kCodes && (CB == 8 || (int64_t)lv.len * 8 <= kCodeCopy2)) {
+  if (kCodes && (CB == 8 || (int64_t)lv.len * 2 <= kCodeCopy2)) {
     auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT, kCodes>;
-    size_t lds = CB == 4 ? kCodeCopy2 + (size_t)lv.len * 8 : (size_t)lv.len * 8;
+    size_t lds = CB == 4 ? kCodeCopy2 + (size_t)lv.len * 2 : (size_t)lv.len * 2;
     unsigned grid = persistent_grid((const void*)k, bs, lds, ngroups);
     hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out);
   } else {

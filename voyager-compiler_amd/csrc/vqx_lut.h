@@ -63,20 +63,22 @@ __device__ __forceinline__ LutLds lut_to_lds(const uint32_t* blob, int len, uint
 }
 
 // Codes-only copy of the two signed tables into LDS, for kernels that write
-// packed codes and nothing else: one word per magnitude holding the code;
-// CB 4 adds a second copy kCodeCopy2 bytes further on holding the code shifted
-// into the high nibble, so a byte of two codes is the OR of an even and an odd
-// element's words (read at the same address plus an immediate offset).
+// packed codes and nothing else: one byte per magnitude holding the code, so
+// an entry's address is the table base plus the bf16 bits themselves; CB 4
+// adds a second copy kCodeCopy2 bytes further on holding the code shifted into
+// the high nibble, so a byte of two codes is the OR of an even and an odd
+// element's entries (read at the same address plus an immediate offset).
 // Call with all threads of the workgroup; includes the barrier.
-constexpr int kCodeCopy2 = 8192;  // CB 4 needs 2 * len * 4 <= kCodeCopy2
+constexpr int kCodeCopy2 = 4096;  // CB 4 needs 2 * len <= kCodeCopy2
 template <int CB>
 __device__ __forceinline__ LutLds lut_codes_to_lds(const uint32_t* blob, int len, uint32_t* lds) {
   static_assert(CB == 4 || CB == 8, "code tables hold 4- or 8-bit codes");
   const uint32_t* src = blob + kLutHeaderWords;
+  uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
   for (int i = threadIdx.x; i < 2 * len; i += blockDim.x) {
     const uint32_t c = src[i] >> 16;
-    lds[i] = c;
-    if constexpr (CB == 4) lds[kCodeCopy2 / 4 + i] = c << 4;
+    l8[i] = (uint8_t)c;
+    if constexpr (CB == 4) l8[kCodeCopy2 + i] = (uint8_t)(c << 4);
   }
   __syncthreads();
   LutLds v;
