@@ -196,6 +196,21 @@ int vqx_mx_decode(const uint8_t* codes, int32_t code_bits, const uint16_t* decod
                   int32_t ntab, const void* scale, int32_t scale_kind, int64_t n,
                   int64_t block_size, void* out, int32_t out_dtype, vqx_stream_t stream);
 
+/*
+ * GroupWiseAffineFakeQuantFunction.forward
+ * (src/vc/quantization/fake_quantize.py:162-211), the group_wise_affine
+ * qscheme's fake-quant (e.g. uint2 KV caches).  x viewed as [outer, L, inner]
+ * with blocks of block_size along L (a short last block is zero-padded, as
+ * mx_utils.py:62-108 pads it).  Per block: sf = (max - min) / (quant_max -
+ * quant_min), 1 where not > 0; zp = -min / sf + quant_min; both through
+ * scale_qmap when given; y = (clamp(round(x / sf + zp), quant_min, quant_max)
+ * - zp) * sf, every step rounded to x's dtype (BF16 or F32) as torch does.
+ * scale_out / zero_point_out (optional): [outer, ceil(L/bs), inner] in x's dtype.
+ */
+int vqx_gwa_fake_quant(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                       int64_t block_size, float quant_min, float quant_max, const uint16_t* scale_qmap,
+                       void* scale_out, void* zero_point_out, void* y, vqx_stream_t stream);
+
 /* decode_table[code] = value of the format, for codes < ntab. */
 int vqx_decode_table(const vqx_format* fmt, uint16_t* decode_table, int32_t ntab,
                      vqx_stream_t stream);

@@ -25,6 +25,7 @@ __all__ = [
     "calculate_mx_qparam",
     "quantize_mx",
     "mx_fake_quantize",
+    "group_wise_affine_fake_quant",
     "fake_quantize_per_tensor",
     "codebook_encode_rows",
     "codebook_decode_rows",
@@ -59,7 +60,7 @@ def expand(t, shape, block_size):
         if t.shape[d] != shape[d]:
             t = torch.repeat_interleave(t, block_size, d)
     if list(t.shape) != list(shape):
-        t = t[[slice(0, x) for x in shape]]
+        t = t[tuple(slice(0, x) for x in shape)]
     return t
 
 
@@ -135,6 +136,27 @@ def mx_fake_quantize(x, qmap, axes, block_size, quant_max, force_scale_power_of_
     """MXFakeQuantizeFunction.forward (src/vc/quantization/fake_quantize.py:143-153)."""
     sf, q = quantize_mx(x, qmap, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap)
     return sf, q * expand(sf, q.shape, block_size)
+
+
+def group_wise_affine_fake_quant(x, axes, block_size, quant_min, quant_max, scale_qmap=None):
+    """GroupWiseAffineFakeQuantFunction.forward (src/vc/quantization/
+    fake_quantize.py:162-211), one axis: block min / max of the zero-padded
+    blocks, sf, zp, optional scale_qmap, then the affine fake-quant, every op
+    on x's dtype.  Returns (scale, zero_point, y)."""
+    axis = axes[0] if isinstance(axes, (list, tuple)) else axes
+    xb, axis = _to_blocks(x, axis, block_size)
+    mn = torch.amin(xb, dim=axis + 1)
+    mx = torch.amax(xb, dim=axis + 1)
+    sf = (mx - mn) / (quant_max - quant_min)
+    sf = torch.where(sf > 0.0, sf, 1.0)
+    zp = -mn / sf + quant_min
+    if scale_qmap is not None:
+        sf = vmap(sf, scale_qmap)
+        zp = vmap(zp, scale_qmap)
+    sfe = expand(sf, x.shape, block_size)
+    zpe = expand(zp, x.shape, block_size)
+    q = torch.clamp(torch.round(x / sfe + zpe), quant_min, quant_max)
+    return sf, zp, (q - zpe) * sfe
 
 
 def fake_quantize_per_tensor(x, qmap, scale):

@@ -1,0 +1,82 @@
+"""GPU parity of the group-wise affine fake-quant (GroupWiseAffineFakeQuantFunction,
+src/vc/quantization/fake_quantize.py:162-216) against the CPU oracle, bit for
+bit: scale, zero point and output, bf16 and fp32 inputs, blocks along any
+axis, short (zero-padded) last blocks, NaN / Inf, scale_qmap, and the
+FakeQuantize module's group_wise_affine path."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as F
+from oracle import reference_ops as R
+
+
+def same(a, b):
+    """Bit equality with NaN as a class."""
+    a, b = a.cpu(), b.cpu()
+    if a.shape != b.shape or a.dtype != b.dtype:
+        return False
+    nan = torch.isnan(a) & torch.isnan(b)
+    ai = a.view(torch.int16 if a.dtype == torch.bfloat16 else torch.int32)
+    bi = b.view(torch.int16 if b.dtype == torch.bfloat16 else torch.int32)
+    return bool(((ai == bi) | nan).all())
+
+
+def gwa_inputs(shape, dt, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=g) * torch.exp(torch.randn(*shape, generator=g))
+    return x.to(dt)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape,axis,bs", [((64, 256), -1, 64), ((8, 100), -1, 32), ((4, 37, 6), 1, 8),
+                                           ((33, 5), 0, 16), ((3, 7), -1, 64)])
+@pytest.mark.parametrize("qrange", [(0, 3), (-8, 7), (0, 255)])
+def test_gwa_fake_quant_matches_oracle(vqx, dt, shape, axis, bs, qrange):
+    from importlib import import_module
+
+    qops = import_module(vqx.__name__ + ".ops.quantized")
+    x = gwa_inputs(shape, dt, seed=sum(shape) + bs)
+    qmin, qmax = qrange
+    sf, zp, y = qops.gwa_fake_quantize(x.cuda(), axis, bs, qmin, qmax)
+    rsf, rzp, ry = R.group_wise_affine_fake_quant(x, axis, bs, qmin, qmax)
+    assert same(sf, rsf) and same(zp, rzp), "scale / zero point"
+    assert same(y, ry), f"{int((y.cpu() != ry).sum())} outputs differ"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_gwa_special_values_and_scale_qmap(vqx, dt):
+    from importlib import import_module
+
+    qops = import_module(vqx.__name__ + ".ops.quantized")
+    x = gwa_inputs((12, 64), dt, seed=5)
+    x[0, 3] = float("nan")
+    x[1, 0] = float("inf")
+    x[2, 5] = -float("inf")
+    x[3] = 2.5                                   # constant block: sf -> 1
+    x[4, :32] = 0.0
+    x[5] = torch.linspace(-1e-30, 1e-30, 64).to(dt)   # tiny range
+    for sq in (None, R.table_tensor(F.quantization_table("fp8_e5m3"))):
+        sf, zp, y = qops.gwa_fake_quantize(x.cuda(), -1, 32, 0, 3, None if sq is None else sq.cuda())
+        rsf, rzp, ry = R.group_wise_affine_fake_quant(x, -1, 32, 0, 3, sq)
+        assert same(sf, rsf) and same(zp, rzp) and same(y, ry)
+
+
+@pytest.mark.gpu
+def test_gwa_fakequantize_module(vqx):
+    """FusedAmaxObsFakeQuantize with qscheme group_wise_affine (uint2 KV-cache
+    style, fake_quantize.py:409-420): output and the scale / zero_point buffers."""
+    fq_mod = vqx.quantization.FusedAmaxObsFakeQuantize
+    m = fq_mod("uint2", qscheme=vqx.quantization.QScheme.GROUP_WISE_AFFINE, quant_min=0, quant_max=3,
+               ch_axis=-1, block_size=64, device="cuda")
+    x = gwa_inputs((2, 8, 128), torch.bfloat16, seed=9)
+    y = m(x.cuda())
+    rsf, rzp, ry = R.group_wise_affine_fake_quant(x, -1, 64, 0, 3)
+    assert same(y, ry)
+    assert torch.equal(m.scale.cpu(), rsf.float()) and torch.equal(m.zero_point.cpu(), rzp.float())
+    xg = x.cuda().requires_grad_(True)
+    m(xg).sum().backward()
+    assert torch.equal(xg.grad, torch.ones_like(xg))

@@ -212,3 +212,85 @@ def test_oracle_vmap_chunks_and_dtypes():
     y = R.vmap(x, t, chunk_size=1 << 20)
     h = F.f32_to_bf16(x.numpy())
     assert np.array_equal(y.numpy().view(np.uint32), F.bf16_to_f32(F.posit_table(8, 1)[h]).view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# group-wise affine fake-quant (fake_quantize.py:162-211)
+# ---------------------------------------------------------------------------
+GWA = R.group_wise_affine_fake_quant
+
+
+def test_gwa_identity_on_the_grid():
+    """Blocks whose min is 0 and max is qmax - qmin hold sf = 1, zp = 0, so
+    integer inputs come back unchanged (a wrong sign in zp, a dropped qmin
+    or a swapped min / max would move them)."""
+    x = torch.tensor([[0.0, 1.0, 2.0, 3.0, 3.0, 0.0, 1.0, 2.0]])
+    sf, zp, y = GWA(x, -1, 4, 0, 3)
+    assert torch.equal(sf, torch.ones(1, 2)) and torch.equal(zp, torch.zeros(1, 2))
+    assert torch.equal(y, x)
+    x2 = torch.tensor([[-8.0, -3.0, 0.0, 7.0]])
+    sf, zp, y = GWA(x2, -1, 4, -8, 7)  # int4: sf = 15 / 15 = 1, zp = 8 - 8 = 0
+    assert torch.equal(sf, torch.ones(1, 1)) and torch.equal(zp, torch.zeros(1, 1)) and torch.equal(y, x2)
+
+
+def test_gwa_constant_block_and_shift():
+    """A constant block has max - min = 0, so sf becomes 1 and zp = qmin - c:
+    the block is reproduced exactly; shifting a grid block by an integer
+    shifts only zp."""
+    x = torch.full((1, 4), 5.0)
+    sf, zp, y = GWA(x, -1, 4, 0, 3)
+    assert sf.item() == 1.0 and zp.item() == -5.0 and torch.equal(y, x)
+    base = torch.tensor([[0.0, 1.0, 2.0, 3.0]])
+    sf, zp, y = GWA(base + 10.0, -1, 4, 0, 3)
+    assert sf.item() == 1.0 and zp.item() == -10.0 and torch.equal(y, base + 10.0)
+
+
+def test_gwa_short_block_is_zero_padded():
+    """mx_utils.py:62-108 pads a short last block with zeros before min / max:
+    the result equals that of the explicitly padded tensor, trimmed."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.rand(3, 10, generator=g) + 2.0          # all positive: the padding zero becomes the min
+    xp = torch.cat([x, torch.zeros(3, 2)], dim=1)
+    for dt in (torch.float32, torch.bfloat16):
+        sf, zp, y = GWA(x.to(dt), -1, 4, 0, 3)
+        sfp, zpp, yp = GWA(xp.to(dt), -1, 4, 0, 3)
+        assert torch.equal(sf, sfp) and torch.equal(zp, zpp) and torch.equal(y, yp[:, :10])
+        assert (zp[:, -1] == 0).all()                  # min = 0 in the padded block
+
+
+def test_gwa_levels_and_error_bound():
+    """Each block's outputs take at most qmax - qmin + 1 distinct values, and
+    in fp32 every output is within sf / 2 (plus rounding) of its input."""
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(16, 256, generator=g)
+    for qmin, qmax in ((0, 3), (-8, 7), (0, 255)):
+        sf, zp, y = GWA(x, 1, 64, qmin, qmax)
+        for b in range(4):
+            yb = y[:, 64 * b:64 * (b + 1)]
+            for r in range(16):
+                assert yb[r].unique().numel() <= qmax - qmin + 1
+        err = (y - x).abs()
+        bound = R.expand(sf, x.shape, 64) * (0.5 + 1e-4)
+        assert (err <= bound).all()
+
+
+def test_gwa_matches_a_per_block_loop():
+    """The vectorised oracle against a per-block scalar loop over another axis
+    (blocks along dim 0 of a 3-d tensor), bf16 arithmetic step by step."""
+    g = torch.Generator().manual_seed(13)
+    x = (torch.randn(10, 3, 5, generator=g) * 4).to(torch.bfloat16)
+    sf, zp, y = GWA(x, 0, 4, 0, 3)
+    bf = torch.bfloat16
+    for j in range(3):
+        for k in range(5):
+            for b in range(3):                            # blocks of rows 0-3, 4-7, 8-9 (+2 zero rows)
+                col = x[4 * b:4 * b + 4, j, k]
+                vals = col.tolist() + [0.0] * (4 - col.numel())
+                mn, mx = min(vals), max(vals)
+                s = ((torch.tensor(mx, dtype=bf) - torch.tensor(mn, dtype=bf)) / 3)
+                s = s if s.item() > 0 else torch.tensor(1.0, dtype=bf)
+                z = (-torch.tensor(mn, dtype=bf)) / s + 0
+                assert sf[b, j, k] == s and zp[b, j, k] == z
+                for i in range(col.numel()):
+                    q = torch.clamp(torch.round(col[i] / s + z), 0, 3)
+                    assert y[4 * b + i, j, k] == (q - z) * s

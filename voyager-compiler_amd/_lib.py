@@ -75,6 +75,7 @@ _SIGNATURES = {
                          _F, _P, _P, _P, _P, _P, _P, _P, _I32, _P], ctypes.c_int),
     "vqx_mx_decode": ([_P, _I32, _P, _I32, _P, _I32, _I64, _I64, _P, _I32, _P], ctypes.c_int),
     "vqx_decode_table": ([ctypes.POINTER(VqxFormat), _P, _I32, _P], ctypes.c_int),
+    "vqx_gwa_fake_quant": ([_P, _I32, _I64, _I64, _I64, _I64, _F, _F, _P, _P, _P, _P, _P], ctypes.c_int),
     "vqx_codebook_encode": ([_P, _I32, _I64, _I64, _P, _I32, _P, _P], ctypes.c_int),
     "vqx_codebook_decode": ([_P, _I64, _I64, _P, _I32, _P, _I32, _P], ctypes.c_int),
     "vqx_nf4_linear": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], ctypes.c_int),

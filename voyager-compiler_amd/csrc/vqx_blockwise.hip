@@ -291,6 +291,94 @@ __global__ __launch_bounds__(256) void mx_block_kernel(const T* __restrict__ x, 
 }
 
 // ---------------------------------------------------------------------------
+// Group-wise affine fake-quant (GroupWiseAffineFakeQuantFunction.forward,
+// quantization/fake_quantize.py:162-211): per block of bs along L, min and
+// max (a short last block is zero-padded, which pulls both towards 0),
+//   sf = (max - min) / (qmax - qmin), 1 where not > 0;  zp = -min / sf + qmin;
+// optionally both through scale_qmap (vmap); then per element
+//   (clamp(round(x / sf + zp), qmin, qmax) - zp) * sf.
+// Every step rounds to the input dtype as torch's ops on that dtype do (the
+// fp32 result of each operation, then RNE to bf16 for bf16 inputs), the
+// divisions are IEEE-correct, and NaN propagates as in torch (amin / amax
+// and clamp keep it).  One thread per block, x viewed as [outer, L, inner].
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float round_to(float f) {
+  return BT<T>::val(BT<T>::round_bits(f));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void gwa_fq_kernel(const T* __restrict__ x, int64_t outer, int64_t L,
+                                                     int64_t inner, int64_t bs, float qmin, float qmax,
+                                                     const uint16_t* __restrict__ scale_qmap, T* scale_out,
+                                                     T* zp_out, T* __restrict__ y) {
+  const int64_t nblk_l = (L + bs - 1) / bs;
+  const int64_t total = outer * nblk_l * inner;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const float qrange = qmax - qmin;
+  auto vmap = [&](float v) { return round_to<T>(bf2f(scale_qmap[f2bf(v)])); };
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const int64_t in = t % inner;
+    const int64_t rest = t / inner;
+    const int64_t bl = rest % nblk_l;
+    const int64_t o = rest / nblk_l;
+    const int64_t l0 = bl * bs;
+    const int64_t l1 = l0 + bs < L ? l0 + bs : L;
+    const T* base = x + (o * L) * inner + in;
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    bool nan = false;
+    for (int64_t l = l0; l < l1; ++l) {
+      const float v = BT<T>::val(BT<T>::bits(base + l * inner));
+      nan |= v != v;
+      mn = v < mn ? v : mn;
+      mx = v > mx ? v : mx;
+    }
+    if (l1 - l0 < bs) {  // the zero padding of a short last block
+      mn = mn < 0.0f ? mn : 0.0f;
+      mx = mx > 0.0f ? mx : 0.0f;
+    }
+    if (nan) mn = mx = __builtin_nanf("");
+    float sf = round_to<T>(round_to<T>(mx - mn) / qrange);
+    sf = sf > 0.0f ? sf : 1.0f;
+    float zp = round_to<T>(round_to<T>(-mn / sf) + qmin);
+    if (scale_qmap) {
+      sf = vmap(sf);
+      zp = vmap(zp);
+    }
+    if (scale_out) BT<T>::put(scale_out + t, BT<T>::round_bits(sf));
+    if (zp_out) BT<T>::put(zp_out + t, BT<T>::round_bits(zp));
+    for (int64_t l = l0; l < l1; ++l) {
+      const int64_t i = (o * L + l) * inner + in;
+      const float v = BT<T>::val(BT<T>::bits(x + i));
+      float q = __builtin_rintf(round_to<T>(round_to<T>(v / sf) + zp));
+      q = q < qmin ? qmin : (q > qmax ? qmax : q);  // NaN stays NaN
+      BT<T>::put(y + i, BT<T>::round_bits(round_to<T>(q - zp) * sf));
+    }
+  }
+}
+
+int gwa_fake_quant(const void* x, int dtype, int64_t outer, int64_t L, int64_t inner, int64_t bs, float qmin,
+                   float qmax, const uint16_t* scale_qmap, void* scale_out, void* zp_out, void* y,
+                   hipStream_t st) {
+  if (outer < 0 || L < 0 || inner < 0) return set_error(kErrInvalid, "gwa_fake_quant: negative shape");
+  if (bs < 1) return set_error(kErrInvalid, "gwa_fake_quant: block_size must be >= 1");
+  if (!(qmax > qmin)) return set_error(kErrInvalid, "gwa_fake_quant: quant_max must exceed quant_min");
+  const int64_t total = outer * ((L + bs - 1) / bs) * inner;
+  if (total == 0) return kOk;
+  if (!x || !y) return set_error(kErrInvalid, "gwa_fake_quant: null tensor");
+  const unsigned grid = grid_for(total, 256);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(gwa_fq_kernel<uint16_t>, dim3(grid), dim3(256), 0, st, (const uint16_t*)x, outer, L, inner,
+                       bs, qmin, qmax, scale_qmap, (uint16_t*)scale_out, (uint16_t*)zp_out, (uint16_t*)y);
+  else if (dtype == kF32)
+    hipLaunchKernelGGL(gwa_fq_kernel<float>, dim3(grid), dim3(256), 0, st, (const float*)x, outer, L, inner, bs,
+                       qmin, qmax, scale_qmap, (float*)scale_out, (float*)zp_out, (float*)y);
+  else
+    return set_error(kErrInvalid, "gwa_fake_quant: input dtype %d not supported (bf16 or fp32)", dtype);
+  return check_launch("gwa_fake_quant");
+}
+
+// ---------------------------------------------------------------------------
 // LUT fast path: bf16 input, blocks of 16*LPB along the last dim.
 // ---------------------------------------------------------------------------
 // RN_bf16(x / s) for bf16-valued x and s (s normal with a normal reciprocal):

@@ -207,6 +207,14 @@ int vqx_mx_decode(const uint8_t* codes, int32_t code_bits, const uint16_t* decod
                    (hipStream_t)stream);
 }
 
+int vqx_gwa_fake_quant(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                       int64_t block_size, float quant_min, float quant_max, const uint16_t* scale_qmap,
+                       void* scale_out, void* zero_point_out, void* y, vqx_stream_t stream) {
+  g_err[0] = 0;
+  return gwa_fake_quant(x, x_dtype, outer, L, inner, block_size, quant_min, quant_max, scale_qmap, scale_out,
+                        zero_point_out, y, (hipStream_t)stream);
+}
+
 int vqx_decode_table(const vqx_format* fmt, uint16_t* dtab, int32_t ntab, vqx_stream_t stream) {
   g_err[0] = 0;
   FormatDesc d;

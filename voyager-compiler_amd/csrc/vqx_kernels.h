@@ -52,6 +52,9 @@ int mx_decode(const uint8_t* codes, int code_bits, const uint16_t* decode_table,
               const void* scale, int scale_kind, int64_t n, int64_t bs, void* out, int out_dtype,
               hipStream_t st);
 int decode_table(const FormatDesc& fmt, uint16_t* dtab, int ntab, hipStream_t st);
+int gwa_fake_quant(const void* x, int dtype, int64_t outer, int64_t L, int64_t inner, int64_t bs, float qmin,
+                   float qmax, const uint16_t* scale_qmap, void* scale_out, void* zp_out, void* y,
+                   hipStream_t st);
 
 // vqx_codebook.hip
 int codebook_encode(const void* x, int dtype, int64_t rows, int64_t cols, const float* cb, int K,

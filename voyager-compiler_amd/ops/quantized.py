@@ -354,6 +354,30 @@ def mx_fake_quantize(input, fmt: Format, axis, block_size, quant_max, force_pow2
     return scale, fq
 
 
+def gwa_fake_quantize(input, axis, block_size, quant_min, quant_max, scale_qmap=None):
+    """GroupWiseAffineFakeQuantFunction.forward's numerics (fake_quantize.py:
+    162-211): (scale, zero_point, fake-quantized input) in one pass, scale and
+    zero_point shaped like the blocks (the axis becomes ceil(L / block_size))
+    and in the input's dtype."""
+    if input.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"vqx: group-wise affine fake-quant takes bfloat16/float32 inputs, not {input.dtype}")
+    if block_size is None or block_size <= 0:
+        raise AssertionError("block_size must be positive")
+    _lib.require_device(input, "group_wise_affine fake-quant")
+    x = input.contiguous()
+    axis, outer, L, inner = _axis_geometry(list(x.shape), axis)
+    sshape = list(x.shape)
+    sshape[axis] = -(-L // block_size)
+    scale = torch.empty(sshape, dtype=x.dtype, device=x.device)
+    zero_point = torch.empty_like(scale)
+    y = torch.empty_like(x)
+    sq = _table_bf16(scale_qmap.to(x.device)) if scale_qmap is not None else None
+    _lib.call("vqx_gwa_fake_quant", _lib.ptr(x), _lib.dtype_tag(x.dtype), outer, L, inner, block_size,
+              float(quant_min), float(quant_max), _lib.ptr(sq), _lib.ptr(scale), _lib.ptr(zero_point),
+              _lib.ptr(y), _lib.stream_of(x))
+    return scale, zero_point, y
+
+
 # ---------------------------------------------------------------------------
 # linear_mx / matmul_mx  (quantized.py:286-432): decode on the GPU, then the
 # dense product (hipBLASLt).  The fused NF4 product is linear_nf4.

@@ -9,9 +9,11 @@ kernels:
   (``quantized_ops.fake_quant``), or the table path when ``qmap`` has been
   replaced or edited in place (as codebook fitting does);
 * microscaling: one fused pass that computes the block scales, quantizes and
-  multiplies back (``mx_fake_quantize``).
+  multiplies back (``mx_fake_quantize``);
+* group-wise affine: one fused pass over each block's min / max, scale, zero
+  point and the affine fake-quant (``gwa_fake_quantize``).
 
-Both autograd functions pass gradients straight through to the input.
+All three autograd functions pass gradients straight through to the input.
 """
 
 import logging
@@ -29,6 +31,7 @@ from .qspec import QScheme
 __all__ = [
     "FakeQuantizeFunction",
     "MXFakeQuantizeFunction",
+    "GroupWiseAffineFakeQuantFunction",
     "FusedAmaxObsFakeQuantize",
     "get_quantization_map",
 ]
@@ -93,6 +96,29 @@ class MXFakeQuantizeFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output):
         return (grad_output,) + (None,) * 9
+
+
+class GroupWiseAffineFakeQuantFunction(torch.autograd.Function):
+    """Group-wise affine fake-quant (fake_quantize.py:162-216): per block of
+    block_size along the axis, scale and zero point from the block min / max,
+    then (clamp(round(x / sf + zp)) - zp) * sf; scale and zero_point are
+    written into the given buffers; straight-through gradient."""
+
+    @staticmethod
+    def forward(ctx, input, fake_quant_enabled, scale, zero_point, axes, block_size, quant_min, quant_max,
+                scale_qmap=None):
+        if not fake_quant_enabled:
+            return input
+        assert block_size > 0
+        axis = qops._single_axis(axes)
+        sf, zp, y = qops.gwa_fake_quantize(input, axis, block_size, quant_min, quant_max, scale_qmap)
+        scale.resize_(sf.shape).copy_(sf)
+        zero_point.resize_(zp.shape).copy_(zp)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        return (grad_output,) + (None,) * 8
 
 
 class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
@@ -268,8 +294,9 @@ class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
                                              self.block_size, self.quant_max,
                                              self.force_scale_power_of_two, self.scale_qmap, fmt)
         elif self.qscheme == QScheme.GROUP_WISE_AFFINE:
-            raise NotImplementedError(
-                "vqx: group-wise affine fake-quant has no MI355X kernel yet")
+            x = GroupWiseAffineFakeQuantFunction.apply(x, self._fq_on, self.scale, self.zero_point, self.ch_axis,
+                                                       self.block_size, self.quant_min, self.quant_max,
+                                                       self.scale_qmap)
         else:
             if self._observe:
                 self._update_amax_scale(x)
@@ -281,9 +308,9 @@ class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):
-        # scale / amax_history start empty or size 1 and take their observed
-        # shape on the first forward; resize before the default copy.
-        for name in ("scale", "amax_history"):
+        # scale / zero_point / amax_history start empty or size 1 and take
+        # their observed shape on the first forward; resize before the copy.
+        for name in ("scale", "zero_point", "amax_history"):
             key = prefix + name
             if key in state_dict:
                 getattr(self, name).resize_(state_dict[key].shape)
