@@ -243,6 +243,70 @@ int vqx_nf4_linear(const uint16_t* A, const uint8_t* codes, const float* scale, 
                    const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K,
                    vqx_stream_t stream);
 
+/*
+ * quantized_ops::filter_outlier (src/vc/ops/quantized.py:532-630, with
+ * _pad_csr at :537-569), and the outlier half of quantize_mx_outlier
+ * (:633-712, indptr_offset added to the row pointers).
+ * x: [batches, rows, cols] F32, BF16 or F16.  An outlier is an element with
+ * |x| > threshold and x != 0, threshold given already rounded to x's dtype
+ * (torch casts the Python scalar to the tensor's dtype before comparing).
+ * Outputs per batch b, each matrix's outliers in row-major order:
+ *   inlier [batches, rows, cols]  x with outliers replaced by +0
+ *   indptr [batches, rows + 1]    int32, min(prefix count, max_nnz) + indptr_offset
+ *                                 (int32 wrap-around)
+ *   data, indices [batches, max_nnz]  values (x's dtype) and int32 columns of
+ *                                 the first max_nnz outliers; unused slots 0 / -1.
+ */
+int vqx_filter_outlier(const void* x, int32_t x_dtype, int64_t batches, int64_t rows, int64_t cols,
+                       float threshold, int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices,
+                       int32_t* indptr, void* inlier, vqx_stream_t stream);
+
+/*
+ * quantized_ops::slice_csr_tensor (src/vc/ops/quantized.py:715-777) of one CSR
+ * matrix: data [nnz] (F32, BF16 or F16), indices [nnz] int32, indptr [rows + 1]
+ * int32 starting at 0; entries past indptr[rows] are padding (index -1).
+ * dim 0: rows [start, end), 0 <= start <= end <= rows; indptr_out [end - start + 1].
+ * dim 1: columns [start, end), start >= 0, indices rebased by -start;
+ *        indptr_out [rows + 1].
+ * data_out / indices_out [max_nnz]: the kept entries in order, padded with
+ * 0 / -1; past max_nnz they are dropped and indptr_out clamped to max_nnz.
+ */
+int vqx_slice_csr(const void* data, int32_t dtype, const int32_t* indices, const int32_t* indptr, int64_t nnz,
+                  int64_t rows, int32_t dim, int64_t start, int64_t end, int64_t max_nnz, void* data_out,
+                  int32_t* indices_out, int32_t* indptr_out, vqx_stream_t stream);
+
+/*
+ * The weight decode of quantized_ops::spmm_csr (src/vc/ops/quantized.py:816-836):
+ * B [batches, rows, cols] (F32, BF16, F16 or U8) ->
+ *   v = code ? code[trunc(B)] : B        (negative index from the end; out of range -> NaN)
+ *   v = scale ? round_out(v * scale[b * scale_batch_stride + (r / row_block) * scale_cols
+ *                                   + c / col_block]) : v
+ * stored as out_dtype (F32, BF16 or F16: the dtype torch's decode produces),
+ * transposed to [batches, cols, rows] when transpose != 0 (the "kc" layout).
+ * scale_rows / scale_cols must cover B through row_block / col_block.
+ */
+int vqx_csr_decode_weight(const void* B, int32_t B_dtype, int64_t batches, int64_t rows, int64_t cols,
+                          int32_t transpose, const void* code, int32_t code_dtype, int64_t code_len,
+                          const void* scale, int32_t scale_dtype, int64_t scale_batch_stride, int64_t scale_rows,
+                          int64_t scale_cols, int64_t row_block, int64_t col_block, void* out, int32_t out_dtype,
+                          vqx_stream_t stream);
+
+/*
+ * quantized_ops::spmm_csr product (src/vc/ops/quantized.py:838-878):
+ *   out[b, r, n] = round_B(sum over the row's entries p, in order, of
+ *                  fp32(data[b, p]) * B[b, indices[b, p], n])
+ * accumulated in fp32; with an addend, out = round_B(addend + round_B(sum))
+ * (the dense + sparse sum of linear_mx / matmul_mx, :335-348, :408-420).
+ * data / indices [batches, nnz_stride]; indptr [batches, rows + 1], a batch's
+ * entries at positions indptr[b][r] - indptr[b][0] (row pointers lifted out
+ * of a longer array).  B: [K, N] row-major (F32, BF16 or F16; also the
+ * output dtype) at B + b * B_batch_stride (0 = shared).  Entries whose index
+ * is outside [0, K) add nothing; positions are clamped to [0, nnz_stride).
+ */
+int vqx_spmm_csr(const void* data, int32_t data_dtype, const int32_t* indices, const int32_t* indptr,
+                 int64_t batches, int64_t rows, int64_t nnz_stride, const void* B, int32_t B_dtype,
+                 int64_t B_batch_stride, int64_t K, int64_t N, const void* addend, void* out, vqx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

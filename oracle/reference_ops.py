@@ -30,6 +30,11 @@ __all__ = [
     "codebook_encode_rows",
     "codebook_decode_rows",
     "linear_mx",
+    "filter_outlier",
+    "quantize_mx_outlier",
+    "slice_csr_tensor",
+    "spmm_csr",
+    "csr_to_dense",
 ]
 
 
@@ -195,3 +200,131 @@ def linear_mx(x, weight, bias=None, weight_scale=None, block_size=None, weight_c
     if weight_scale is not None:
         w = w * expand(weight_scale, weight.shape, block_size)
     return torch.nn.functional.linear(x, w, bias)
+
+
+# ---------------------------------------------------------------------------
+# outliers as CSR (src/vc/ops/quantized.py:532-895)
+# ---------------------------------------------------------------------------
+def _pad_csr(values, cols, crow, max_nnz):
+    """src/vc/ops/quantized.py:537-569: pad to max_nnz with 0 / -1, or keep
+    the first max_nnz entries and clamp the row pointers (in place)."""
+    nse = int(crow[-1])
+    if nse <= max_nnz:
+        pad = max_nnz - nse
+        return (torch.cat([values, values.new_zeros(pad)]),
+                torch.cat([cols, cols.new_full((pad,), -1)]))
+    crow.clamp_(max=max_nnz)
+    return values[:max_nnz], cols[:max_nnz]
+
+
+def filter_outlier(x, threshold, max_pct=0.01, indptr_offset=0):
+    """src/vc/ops/quantized.py:572-630: outliers |x| > threshold (the Python
+    scalar compared in x's dtype); per matrix of the last two dims, the CSR of
+    the nonzero outliers in row-major order (numpy nonzero), int32 indices,
+    padded by _pad_csr; inliers are x with outliers set to 0.  indptr_offset
+    is quantize_mx_outlier's shift of the row pointers (:686-687)."""
+    is_out = torch.abs(x) > threshold
+    inlier = torch.where(is_out, 0, x)
+    R, C = x.shape[-2:]
+    batch = x.shape[:-2]
+    max_nnz = int(math.prod((R, C)) * max_pct)
+    xs = x.reshape(-1, R, C)
+    keep = (is_out & (x != 0)).reshape(-1, R, C).numpy()
+    datas, idxs, ptrs = [], [], []
+    for b in range(xs.shape[0]):
+        r, c = np.nonzero(keep[b])
+        crow = np.zeros(R + 1, dtype=np.int64)
+        crow[1:] = np.cumsum(np.bincount(r, minlength=R))
+        vals = xs[b][torch.from_numpy(r), torch.from_numpy(c)]
+        crow_t = torch.from_numpy(crow.astype(np.int32))
+        d, i = _pad_csr(vals, torch.from_numpy(c.astype(np.int32)), crow_t, max_nnz)
+        datas.append(d)
+        idxs.append(i)
+        ptrs.append(crow_t)
+    data = torch.stack(datas).reshape(*batch, max_nnz)
+    indices = torch.stack(idxs).reshape(*batch, max_nnz)
+    indptr = torch.stack(ptrs).reshape(*batch, R + 1)
+    if indptr_offset:
+        indptr = indptr + indptr_offset
+    return data, indices, indptr, inlier
+
+
+def quantize_mx_outlier(x, qmap, axes, block_size, quant_max, force_scale_power_of_two=False,
+                        scale_qmap=None, threshold=None, max_pct=0.01, indptr_offset=0):
+    """src/vc/ops/quantized.py:642-691: filter_outlier, then quantize_mx of
+    the inliers.  Returns (data, indices, indptr, scale, inliers)."""
+    data, indices, indptr, inl = filter_outlier(x, threshold, max_pct, indptr_offset)
+    scale, q = quantize_mx(inl, qmap, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap)
+    return data, indices, indptr, scale, q
+
+
+def slice_csr_tensor(data, indices, indptr, dim=0, start=None, end=None, size_factor=1.0):
+    """src/vc/ops/quantized.py:722-763 (numpy): rows [start, end) with the
+    pointers rebased, or columns [start, end) with per-row counts of the kept
+    entries and the indices rebased; then _pad_csr to int(len(data) * size_factor)."""
+    dim = dim + 2 if dim < 0 else dim
+    if dim not in (0, 1):
+        raise ValueError(f"Cannot slice sparse CSR matrix along dim {dim}")
+    p = indptr.numpy().astype(np.int64)
+    d = data
+    ix = indices.numpy()
+    if dim == 0:
+        s0, e0 = int(p[start]), int(p[end])
+        new_ptr = (p[start:end + 1] - s0).astype(np.int32)
+        vals = d[s0:e0]
+        cols = torch.from_numpy(ix[s0:e0].copy())
+    else:
+        mask = (ix >= start) & (ix < end)
+        nse = int(p[-1])
+        counts = np.array([mask[p[r]:p[r + 1]].sum() for r in range(len(p) - 1)], dtype=np.int64)
+        assert counts.sum() == mask[:nse].sum()
+        new_ptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+        vals = d[torch.from_numpy(mask)]
+        cols = torch.from_numpy((ix[mask] - start).astype(ix.dtype))
+    new_ptr = torch.from_numpy(new_ptr)
+    max_nnz = int(data.shape[0] * size_factor)
+    nd, ni = _pad_csr(vals, cols, new_ptr, max_nnz)
+    return nd, ni, new_ptr
+
+
+def csr_to_dense(data, indices, indptr, cols, dtype=None):
+    """Dense [rows, cols] matrix of one CSR matrix (rows from indptr, entries
+    at positions indptr[r] - indptr[0]); later duplicates overwrite."""
+    p = indptr.numpy().astype(np.int64)
+    p = p - p[0]
+    R = len(p) - 1
+    out = torch.zeros((R, cols), dtype=dtype or data.dtype)
+    ix = indices.numpy()
+    for r in range(R):
+        for q in range(p[r], p[r + 1]):
+            out[r, int(ix[q])] = data[q]
+    return out
+
+
+def spmm_csr(data, indices, indptr, B, B_scale=None, B_code=None, block_size=None, weight_layout="kc"):
+    """src/vc/ops/quantized.py:816-878: decode B (B_code[B.long()], then times
+    the expanded scale, in torch's dtypes), transpose a "kc" B to [K, N], then
+    per batch the rebased CSR rows times B in fp32 (torch.sparse.mm), cast to
+    the decoded B's dtype."""
+    if B_code is not None:
+        B = B_code[B.to(torch.long)]
+    if B_scale is not None:
+        B = B * expand(B_scale, B.shape, block_size)
+    if weight_layout == "kc":
+        B = B.mT
+    batch = indptr.shape[:-1]
+    nb = int(math.prod(batch))
+    ip = indptr.reshape(-1, indptr.shape[-1])
+    ix = indices.reshape(-1, indices.shape[-1])
+    dt = data.reshape(-1, data.shape[-1])
+    if B.ndim > 2:
+        B = B.reshape(nb, B.shape[-2], B.shape[-1])
+    outs = []
+    for i in range(nb):
+        Bi = B[i] if B.ndim == 3 else B
+        base = int(ip[i][0])
+        n = int(ip[i][-1]) - base
+        csr = torch.sparse_csr_tensor(ip[i] - base, ix[i, :n], dt[i, :n], dtype=torch.float32,
+                                      size=(ip[i].numel() - 1, Bi.shape[0]))
+        outs.append(torch.sparse.mm(csr, Bi.to(torch.float32)).to(B.dtype))
+    return torch.stack(outs).reshape(*batch, -1, B.shape[-1])

@@ -245,4 +245,40 @@ int vqx_nf4_linear(const uint16_t* A, const uint8_t* codes, const float* scale, 
   return nf4_gemm(A, codes, scale, levels, bias, out, M, N, K, (hipStream_t)stream);
 }
 
+int vqx_filter_outlier(const void* x, int32_t x_dtype, int64_t batches, int64_t rows, int64_t cols,
+                       float threshold, int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices,
+                       int32_t* indptr, void* inlier, vqx_stream_t stream) {
+  g_err[0] = 0;
+  return filter_outlier(x, x_dtype, batches, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr,
+                        inlier, (hipStream_t)stream);
+}
+
+int vqx_slice_csr(const void* data, int32_t dtype, const int32_t* indices, const int32_t* indptr, int64_t nnz,
+                  int64_t rows, int32_t dim, int64_t start, int64_t end, int64_t max_nnz, void* data_out,
+                  int32_t* indices_out, int32_t* indptr_out, vqx_stream_t stream) {
+  g_err[0] = 0;
+  return csr_slice(data, dtype, indices, indptr, nnz, rows, dim, start, end, max_nnz, data_out, indices_out,
+                   indptr_out, (hipStream_t)stream);
+}
+
+int vqx_csr_decode_weight(const void* B, int32_t B_dtype, int64_t batches, int64_t rows, int64_t cols,
+                          int32_t transpose, const void* code, int32_t code_dtype, int64_t code_len,
+                          const void* scale, int32_t scale_dtype, int64_t scale_batch_stride, int64_t scale_rows,
+                          int64_t scale_cols, int64_t row_block, int64_t col_block, void* out, int32_t out_dtype,
+                          vqx_stream_t stream) {
+  g_err[0] = 0;
+  CsrDecode d{B, B_dtype, batches, rows, cols, transpose, code, code_dtype, code_len, scale, scale_dtype,
+              scale_batch_stride, scale_rows, scale_cols, row_block, col_block, out, out_dtype};
+  return csr_decode(d, (hipStream_t)stream);
+}
+
+int vqx_spmm_csr(const void* data, int32_t data_dtype, const int32_t* indices, const int32_t* indptr,
+                 int64_t batches, int64_t rows, int64_t nnz_stride, const void* B, int32_t B_dtype,
+                 int64_t B_batch_stride, int64_t K, int64_t N, const void* addend, void* out, vqx_stream_t stream) {
+  g_err[0] = 0;
+  SpmmArgs a{data, data_dtype, indices, indptr, batches, rows, nnz_stride, B, B_dtype, B_batch_stride, K, N,
+             addend, out};
+  return spmm_csr(a, (hipStream_t)stream);
+}
+
 }  // extern "C"

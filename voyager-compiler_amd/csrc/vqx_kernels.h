@@ -66,4 +66,42 @@ int codebook_decode(const uint8_t* codes, int64_t rows, int64_t cols, const floa
 int nf4_gemm(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
              const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, hipStream_t st);
 
+// vqx_sparse.hip
+struct CsrDecode {
+  const void* B;        // [nb, br, bc], dtype b_dtype (float tags or kU8)
+  int b_dtype;
+  int64_t nb, br, bc;
+  int transpose;        // out [nb, bc, br] ("kc") or [nb, br, bc] ("ck")
+  const void* code;     // optional [code_len] lookup of trunc(B)
+  int code_dtype;
+  int64_t code_len;
+  const void* scale;    // optional; element (b, r, c) -> b*sb_stride + (r/rdiv)*sc + c/cdiv
+  int scale_dtype;
+  int64_t sb_stride, sr, sc, rdiv, cdiv;
+  void* out;
+  int out_dtype;        // the decoded dtype; value * scale is rounded to it
+};
+
+struct SpmmArgs {
+  const void* data;     // [nb, nnz_stride]
+  int data_dtype;
+  const int32_t* indices;  // [nb, nnz_stride]
+  const int32_t* indptr;   // [nb, rows + 1]; a batch's entries start at indptr[b][0]
+  int64_t nb, rows, nnz_stride;
+  const void* B;        // [.., K, N] row-major, batch stride b_stride (0: shared)
+  int b_dtype;          // also the output dtype
+  int64_t b_stride, K, N;
+  const void* addend;   // optional [nb, rows, N]
+  void* out;            // [nb, rows, N]
+};
+
+int filter_outlier(const void* x, int dtype, int64_t nb, int64_t rows, int64_t cols, float threshold,
+                   int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices, int32_t* indptr,
+                   void* inlier, hipStream_t st);
+int csr_slice(const void* data, int dtype, const int32_t* indices, const int32_t* indptr, int64_t nnz_in,
+              int64_t rows, int dim, int64_t start, int64_t end, int64_t max_nnz, void* data_out,
+              int32_t* indices_out, int32_t* indptr_out, hipStream_t st);
+int csr_decode(const CsrDecode& d, hipStream_t st);
+int spmm_csr(const SpmmArgs& a, hipStream_t st);
+
 }  // namespace vqx

@@ -1,0 +1,642 @@
+// Outlier split and CSR kernels behind filter_outlier, quantize_mx_outlier,
+// slice_csr_tensor and spmm_csr (src/voyager_compiler/ops/quantized.py:532-895).
+//
+// filter_outlier over a [batches, rows, cols] input is three launches:
+//   1. outlier_count_kernel  one wave per row counts the outliers (|x| > t and
+//                            x != 0) and stores the count where the row's end
+//                            pointer goes (indptr[b][r + 1]);
+//   2. csr_scan_kernel       one workgroup per batch turns those counts into
+//                            row pointers in place, clamped to the capacity,
+//                            and pads data / indices past the last entry with
+//                            0 / -1;
+//   3. outlier_split_kernel  one wave per row writes the inliers and scatters
+//                            the outliers, in column order, to their CSR slots.
+// An outlier's slot is its row's pointer plus its rank within the row; ranks
+// come from wave ballots (lane-major, so column order is kept).  Entries past
+// the capacity are dropped, which keeps the first max_nnz in row-major order.
+//
+// The column slice of a CSR matrix reuses the same count -> scan -> scatter
+// shape over the stored entries; the row slice is one gather launch.
+//
+// spmm_csr: one wave per (row, 64*V-column chunk) of the output runs down the
+// row's entries in order and accumulates a * B[k, n] in fp32 (B row-major
+// [K, N]).  A "kc"-stored or coded/scaled B is first decoded and transposed
+// into that layout by csr_decode_kernel, in the dtype the reference's decode
+// produces.
+#include "vqx_common.h"
+#include "vqx_kernels.h"
+
+namespace vqx {
+namespace {
+
+// ---------------------------------------------------------------------------
+// element traits: storage type, exact widening, round-to-nearest-even narrowing
+// ---------------------------------------------------------------------------
+template <int DT>
+struct FT;
+template <>
+struct FT<kF32> {
+  using S = uint32_t;
+  static constexpr int kVec = 4;  // elements per 16 bytes
+  __device__ static float val(uint32_t b) { return u2f(b); }
+  __device__ static uint32_t bits(float f) { return f2u(f); }
+};
+template <>
+struct FT<kBF16> {
+  using S = uint16_t;
+  static constexpr int kVec = 8;
+  __device__ static float val(uint32_t b) { return bf2f(b); }
+  __device__ static uint32_t bits(float f) { return f2bf(f); }
+};
+template <>
+struct FT<kF16> {
+  using S = uint16_t;
+  static constexpr int kVec = 8;
+  __device__ static float val(uint32_t b) { return h2f_exact(b); }
+  __device__ static uint32_t bits(float f) { return f2h_exact(f); }
+};
+
+// V consecutive elements starting at p: one 16-byte load when V fills it,
+// else V element loads.  Element j of the group is get(w, j).
+template <typename S, int V>
+struct Group {
+  static constexpr bool kWide = V * sizeof(S) == 16;
+  uint32_t w[V * sizeof(S) / 4 > 0 ? V * sizeof(S) / 4 : 1];
+  S e[kWide ? 1 : V];
+  __device__ void load(const S* p) {
+    if constexpr (kWide) {
+      u32x4 v = *(const u32x4*)p;
+      w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) e[j] = p[j];
+    }
+  }
+  __device__ uint32_t get(int j) const {
+    if constexpr (kWide) {
+      if constexpr (sizeof(S) == 4) return w[j];
+      else return (w[j >> 1] >> ((j & 1) * 16)) & 0xFFFFu;
+    } else {
+      return (uint32_t)e[j];
+    }
+  }
+};
+
+template <typename S, int V>
+__device__ __forceinline__ void store_group(S* p, const uint32_t (&b)[V]) {
+  if constexpr (V * sizeof(S) == 16) {
+    u32x4 v;
+    if constexpr (sizeof(S) == 4) {
+      v = u32x4{b[0], b[1], b[2], b[3]};
+    } else {
+      v = u32x4{b[0] | b[1] << 16, b[2] | b[3] << 16, b[4] | b[5] << 16, b[6] | b[7] << 16};
+    }
+    *(u32x4*)p = v;
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) p[j] = (S)b[j];
+  }
+}
+
+__device__ __forceinline__ int64_t min64(int64_t a, int64_t b) { return a < b ? a : b; }
+
+__device__ __forceinline__ bool is_outlier(float v, float t) { return fabsf(v) > t && v != 0.f; }
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ int64_t wave_incl_scan(int64_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int64_t u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// filter_outlier
+// ---------------------------------------------------------------------------
+// Row group loads are clamped into the row (cols >= V), so every lane loads
+// unconditionally and lanes past the end only drop their flags.
+template <int DT, int V>
+__global__ __launch_bounds__(256) void outlier_count_kernel(const typename FT<DT>::S* __restrict__ x,
+                                                            int64_t nrows, int64_t rows, int64_t cols,
+                                                            float t, int32_t* __restrict__ indptr) {
+  using S = typename FT<DT>::S;
+  constexpr int U = 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); g < nrows; g += nw) {
+    const S* row = x + g * cols;
+    uint32_t cnt = 0;
+    for (int64_t c0 = 0; c0 < cols; c0 += U * 64 * V) {
+      Group<S, V> grp[U];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = c0 + (int64_t)(u * 64 + lane) * V;
+        ok[u] = c < cols;
+        grp[u].load(row + (ok[u] ? c : cols - V));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < V; ++j) cnt += (ok[u] && is_outlier(FT<DT>::val(grp[u].get(j)), t)) ? 1u : 0u;
+    }
+    cnt = wave_sum(cnt);
+    if (lane == 0) {
+      const int64_t b = g / rows, r = g - b * rows;
+      indptr[b * (rows + 1) + r + 1] = (int32_t)cnt;
+    }
+  }
+}
+
+// In place: indptr[b][r + 1] holds row r's count on entry and
+// min(prefix, max_nnz) + offset on exit (int32 wrap-around, as the
+// reference's int32 add); indptr[b][0] = offset.  Slots from min(total,
+// max_nnz) to max_nnz of data / indices get 0 / -1.
+template <typename S>
+__global__ __launch_bounds__(1024) void csr_scan_kernel(int32_t* __restrict__ indptr, int64_t rows, int64_t max_nnz,
+                                                        int32_t offset, S* __restrict__ data,
+                                                        int32_t* __restrict__ indices) {
+  __shared__ int64_t wsum[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t b = blockIdx.x;
+  int32_t* ptr = indptr + b * (rows + 1);
+  const int64_t per = (rows + 1023) / 1024;
+  const int64_t r0 = min64(tid * per, rows), r1 = min64(r0 + per, rows);
+  int64_t s = 0;
+  for (int64_t r = r0; r < r1; ++r) s += ptr[r + 1];
+  const int64_t incl = wave_incl_scan(s, lane);
+  if (lane == 63) wsum[wv] = incl;
+  __syncthreads();
+  int64_t before = 0, total = 0;
+  for (int w = 0; w < 16; ++w) {
+    const int64_t v = wsum[w];
+    before += w < wv ? v : 0;
+    total += v;
+  }
+  int64_t run = before + incl - s;
+  for (int64_t r = r0; r < r1; ++r) {
+    run += ptr[r + 1];
+    const int64_t c = run < max_nnz ? run : max_nnz;
+    ptr[r + 1] = (int32_t)((uint32_t)c + (uint32_t)offset);
+  }
+  if (tid == 0) ptr[0] = offset;
+  const int64_t used = total < max_nnz ? total : max_nnz;
+  for (int64_t j = used + tid; j < max_nnz; j += 1024) {
+    data[b * max_nnz + j] = (S)0;
+    indices[b * max_nnz + j] = -1;
+  }
+}
+
+template <int DT, int V>
+__global__ __launch_bounds__(256) void outlier_split_kernel(const typename FT<DT>::S* __restrict__ x,
+                                                            int64_t nrows, int64_t rows, int64_t cols,
+                                                            float t, const int32_t* __restrict__ indptr,
+                                                            int64_t max_nnz, typename FT<DT>::S* __restrict__ inlier,
+                                                            typename FT<DT>::S* __restrict__ data,
+                                                            int32_t* __restrict__ indices) {
+  using S = typename FT<DT>::S;
+  const int lane = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); g < nrows; g += nw) {
+    const int64_t b = g / rows, r = g - b * rows;
+    const int32_t* ptr = indptr + b * (rows + 1);
+    int64_t pos = (int64_t)(uint32_t)((uint32_t)ptr[r] - (uint32_t)ptr[0]);
+    const S* row = x + g * cols;
+    S* irow = inlier + g * cols;
+    S* drow = data + b * max_nnz;
+    int32_t* crow = indices + b * max_nnz;
+    for (int64_t c0 = 0; c0 < cols; c0 += 64 * V) {
+      const int64_t c = c0 + (int64_t)lane * V;
+      const bool ok = c < cols;
+      Group<S, V> grp;
+      grp.load(row + (ok ? c : cols - V));
+      uint32_t keep[V];
+      bool f[V];
+      uint32_t below = 0, n = 0;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const uint32_t e = grp.get(j);
+        const float v = FT<DT>::val(e);
+        // every |x| > t inlier is +0 (a negative t takes zeros too); only
+        // nonzero ones are stored
+        keep[j] = fabsf(v) > t ? 0u : e;
+        f[j] = ok && is_outlier(v, t);
+        const uint64_t m = __ballot(f[j]);
+        below += lanes_below(m);
+        n += (uint32_t)__popcll(m);
+      }
+      if (ok) store_group<S, V>(irow + c, keep);
+      if (n != 0 && pos < max_nnz) {
+        int64_t p = pos + below;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          if (f[j]) {
+            if (p < max_nnz) {
+              drow[p] = (S)grp.get(j);
+              crow[p] = (int32_t)(c + j);
+            }
+            ++p;
+          }
+        }
+      }
+      pos += n;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// slice_csr_tensor
+// ---------------------------------------------------------------------------
+// Rows [start, start + nrows_out): rebased pointers and the entries they cover.
+template <typename S>
+__global__ __launch_bounds__(256) void csr_slice_rows_kernel(const S* __restrict__ data,
+                                                             const int32_t* __restrict__ indices,
+                                                             const int32_t* __restrict__ indptr, int64_t nnz_in,
+                                                             int64_t start, int64_t nrows_out, int64_t max_nnz,
+                                                             S* __restrict__ data_out, int32_t* __restrict__ indices_out,
+                                                             int32_t* __restrict__ indptr_out) {
+  const int64_t s0 = indptr[start];
+  const int64_t nse = (int64_t)indptr[start + nrows_out] - s0;
+  const bool over = nse > max_nnz;
+  const int64_t n = max_nnz > nrows_out + 1 ? max_nnz : nrows_out + 1;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    if (i <= nrows_out) {
+      int64_t v = (int64_t)indptr[start + i] - s0;
+      if (over && v > max_nnz) v = max_nnz;
+      indptr_out[i] = (int32_t)v;
+    }
+    if (i < max_nnz) {
+      const int64_t p = s0 + i;
+      const bool real = i < nse && p >= 0 && p < nnz_in;
+      data_out[i] = real ? data[p] : (S)0;
+      indices_out[i] = real ? indices[p] : -1;
+    }
+  }
+}
+
+// Column slice [start, end): per-row count of the stored entries in range,
+// written where the row's end pointer goes (csr_scan_kernel follows).
+__global__ __launch_bounds__(256) void csr_cols_count_kernel(const int32_t* __restrict__ indices,
+                                                             const int32_t* __restrict__ indptr, int64_t rows,
+                                                             int64_t nnz_in, int64_t start, int64_t end,
+                                                             int32_t* __restrict__ indptr_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += nw) {
+    int64_t p0 = indptr[r], p1 = indptr[r + 1];
+    p0 = p0 < 0 ? 0 : (p0 > nnz_in ? nnz_in : p0);
+    p1 = p1 < p0 ? p0 : (p1 > nnz_in ? nnz_in : p1);
+    uint32_t cnt = 0;
+    for (int64_t p = p0 + lane; p < p1; p += 64) {
+      const int64_t k = indices[p];
+      cnt += (k >= start && k < end) ? 1u : 0u;
+    }
+    cnt = wave_sum(cnt);
+    if (lane == 0) indptr_out[r + 1] = (int32_t)cnt;
+  }
+}
+
+template <typename S>
+__global__ __launch_bounds__(256) void csr_cols_scatter_kernel(const S* __restrict__ data,
+                                                               const int32_t* __restrict__ indices,
+                                                               const int32_t* __restrict__ indptr, int64_t rows,
+                                                               int64_t nnz_in, int64_t start, int64_t end,
+                                                               int64_t max_nnz, const int32_t* __restrict__ indptr_out,
+                                                               S* __restrict__ data_out,
+                                                               int32_t* __restrict__ indices_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += nw) {
+    int64_t p0 = indptr[r], p1 = indptr[r + 1];
+    p0 = p0 < 0 ? 0 : (p0 > nnz_in ? nnz_in : p0);
+    p1 = p1 < p0 ? p0 : (p1 > nnz_in ? nnz_in : p1);
+    int64_t pos = indptr_out[r];
+    for (int64_t q0 = p0; q0 < p1 && pos < max_nnz; q0 += 64) {
+      const int64_t p = q0 + lane;
+      const bool live = p < p1;
+      const int64_t k = live ? indices[p] : -1;
+      const bool f = live && k >= start && k < end;
+      const uint64_t m = __ballot(f);
+      const int64_t o = pos + lanes_below(m);
+      if (f && o < max_nnz) {
+        data_out[o] = data[p];
+        indices_out[o] = (int32_t)(k - start);
+      }
+      pos += __popcll(m);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// spmm_csr
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float load_f(const void* p, int dt, int64_t i) {
+  switch (dt) {
+    case kF32: return ((const float*)p)[i];
+    case kBF16: return bf2f(((const uint16_t*)p)[i]);
+    case kF16: return h2f_exact(((const uint16_t*)p)[i]);
+    default: return (float)((const uint8_t*)p)[i];
+  }
+}
+
+__device__ __forceinline__ float round_as(float v, int dt) {
+  switch (dt) {
+    case kBF16: return bf2f(f2bf(v));
+    case kF16: return h2f_exact(f2h_exact(v));
+    default: return v;
+  }
+}
+
+__device__ __forceinline__ void store_f(void* p, int dt, int64_t i, float v) {
+  switch (dt) {
+    case kF32: ((float*)p)[i] = v; break;
+    case kBF16: ((uint16_t*)p)[i] = (uint16_t)f2bf(v); break;
+    default: ((uint16_t*)p)[i] = (uint16_t)f2h_exact(v); break;
+  }
+}
+
+// Bt[b][k][n] = decode(B[b][n][k]) ("kc", transpose) or decode(B[b][k][n])
+// ("ck"), 64x64 tiles through LDS.  decode(v) = code[trunc(v)] (negative
+// indices count from the end; out of range -> NaN) and, with a scale,
+// round_to(out_dtype, value * scale) with the scale expanded by block.
+__global__ __launch_bounds__(256) void csr_decode_kernel(CsrDecode d) {
+  __shared__ float tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t tr = (d.br + 63) / 64, tc = (d.bc + 63) / 64;
+  const int64_t ntiles = d.nb * tr * tc;
+  for (int64_t tIdx = blockIdx.x; tIdx < ntiles; tIdx += gridDim.x) {
+    const int64_t b = tIdx / (tr * tc), rem = tIdx - b * tr * tc;
+    const int64_t r0 = rem / tc * 64, c0 = rem % tc * 64;
+    const int64_t c = c0 + tx;
+    for (int i = ty; i < 64; i += 4) {
+      const int64_t r = r0 + i;
+      float v = 0.f;
+      if (r < d.br && c < d.bc) {
+        v = load_f(d.B, d.b_dtype, (b * d.br + r) * d.bc + c);
+        if (d.code) {
+          if (!(v == v) || fabsf(v) >= (float)d.code_len + 1.f) {
+            v = __builtin_nanf("");
+          } else {
+            int64_t k = (int64_t)v;
+            if (k < 0) k += d.code_len;
+            v = (k >= 0 && k < d.code_len) ? load_f(d.code, d.code_dtype, k) : __builtin_nanf("");
+          }
+        }
+        if (d.scale) {
+          const int64_t si = b * d.sb_stride + (r / d.rdiv) * d.sc + c / d.cdiv;
+          v = round_as(v * load_f(d.scale, d.scale_dtype, si), d.out_dtype);
+        }
+      }
+      tile[i][tx] = v;
+    }
+    __syncthreads();
+    if (d.transpose) {
+      // out[b][c0 + i][r0 + tx] = tile[tx][i]: out is [nb, bc, br]
+      for (int i = ty; i < 64; i += 4) {
+        const int64_t oc = c0 + i, orow = r0 + tx;
+        if (oc < d.bc && orow < d.br) store_f(d.out, d.out_dtype, (b * d.bc + oc) * d.br + orow, tile[tx][i]);
+      }
+    } else {
+      for (int i = ty; i < 64; i += 4) {
+        const int64_t r = r0 + i;
+        if (r < d.br && c < d.bc) store_f(d.out, d.out_dtype, (b * d.br + r) * d.bc + c, tile[i][tx]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// out[g][n] = round(sum over the row's entries p, in order, of a_p * B[k_p][n])
+// (+ addend[g][n], rounded again, when given).  One wave per (row, chunk of
+// 64*V columns); entries are read four at a time.
+template <int DT, int V>
+__global__ __launch_bounds__(256) void spmm_csr_kernel(SpmmArgs a) {
+  using S = typename FT<DT>::S;
+  const int lane = threadIdx.x & 63;
+  const int64_t nch = (a.N + 64 * V - 1) / (64 * V);
+  const int64_t items = a.nb * a.rows * nch;
+  const S* B = (const S*)a.B;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); w < items; w += nw) {
+    const int64_t g = w / nch, ch = w - g * nch;
+    const int64_t b = g / a.rows, r = g - b * a.rows;
+    const int32_t* ptr = a.indptr + b * (a.rows + 1);
+    const int64_t base = ptr[0];
+    int64_t p0 = (int64_t)ptr[r] - base, p1 = (int64_t)ptr[r + 1] - base;
+    p0 = p0 < 0 ? 0 : (p0 > a.nnz_stride ? a.nnz_stride : p0);
+    p1 = p1 < p0 ? p0 : (p1 > a.nnz_stride ? a.nnz_stride : p1);
+    if (a.K == 0) p1 = p0;  // no row of B to read
+    const int64_t n = ch * 64 * V + (int64_t)lane * V;
+    const bool nok = n < a.N;
+    const int64_t nn = nok ? n : a.N - V;
+    const S* Bb = B + b * a.b_stride + nn;
+    const int32_t* idx = a.indices + b * a.nnz_stride;
+    const int64_t dbase = b * a.nnz_stride;
+    float acc[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) acc[j] = 0.f;
+    int64_t p = p0;
+    for (; p + 4 <= p1; p += 4) {
+      Group<S, V> grp[4];
+      float av[4];
+      bool ok[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t k = idx[p + u];
+        ok[u] = (uint64_t)k < (uint64_t)a.K;
+        av[u] = load_f(a.data, a.data_dtype, dbase + p + u);
+        grp[u].load(Bb + (ok[u] ? k : 0) * a.N);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+          if (ok[u]) acc[j] = fmaf(av[u], FT<DT>::val(grp[u].get(j)), acc[j]);
+    }
+    for (; p < p1; ++p) {
+      const int64_t k = idx[p];
+      const bool ok = (uint64_t)k < (uint64_t)a.K;
+      const float av = load_f(a.data, a.data_dtype, dbase + p);
+      Group<S, V> grp;
+      grp.load(Bb + (ok ? k : 0) * a.N);
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        if (ok) acc[j] = fmaf(av, FT<DT>::val(grp.get(j)), acc[j]);
+    }
+    if (nok) {
+      uint32_t o[V];
+      if (a.addend) {
+        Group<S, V> ad;
+        ad.load((const S*)a.addend + g * a.N + n);
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+          o[j] = FT<DT>::bits(FT<DT>::val(ad.get(j)) + FT<DT>::val(FT<DT>::bits(acc[j])));
+      } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) o[j] = FT<DT>::bits(acc[j]);
+      }
+      store_group<S, V>((S*)a.out + g * a.N + n, o);
+    }
+  }
+}
+
+template <int DT>
+int launch_filter(const void* x, int64_t nb, int64_t rows, int64_t cols, float t, int64_t max_nnz, int32_t offset,
+                  void* data, int32_t* indices, int32_t* indptr, void* inlier, hipStream_t st) {
+  using S = typename FT<DT>::S;
+  constexpr int V = FT<DT>::kVec;
+  const int64_t nrows = nb * rows;
+  const bool wide = cols % V == 0 && aligned(x, 16) && aligned(inlier, 16);
+  // cols == 0 runs the count kernel too: its row loop is empty and it
+  // stores zero counts.
+  if (nrows > 0) {
+    if (wide) {
+      hipLaunchKernelGGL((outlier_count_kernel<DT, V>), dim3(grid_for(nrows, 4, 16)), dim3(256), 0, st,
+                         (const S*)x, nrows, rows, cols, t, indptr);
+    } else {
+      hipLaunchKernelGGL((outlier_count_kernel<DT, 1>), dim3(grid_for(nrows, 4, 16)), dim3(256), 0, st,
+                         (const S*)x, nrows, rows, cols, t, indptr);
+    }
+  }
+  if (nb > 0)
+    hipLaunchKernelGGL(csr_scan_kernel<S>, dim3((unsigned)nb), dim3(1024), 0, st, indptr, rows, max_nnz, offset,
+                       (S*)data, indices);
+  if (nrows > 0 && cols > 0) {
+    if (wide) {
+      hipLaunchKernelGGL((outlier_split_kernel<DT, V>), dim3(grid_for(nrows, 4, 16)), dim3(256), 0, st,
+                         (const S*)x, nrows, rows, cols, t, indptr, max_nnz, (S*)inlier, (S*)data, indices);
+    } else {
+      hipLaunchKernelGGL((outlier_split_kernel<DT, 1>), dim3(grid_for(nrows, 4, 16)), dim3(256), 0, st,
+                         (const S*)x, nrows, rows, cols, t, indptr, max_nnz, (S*)inlier, (S*)data, indices);
+    }
+  }
+  return check_launch("filter_outlier");
+}
+
+template <int DT>
+int launch_spmm(const SpmmArgs& a, hipStream_t st) {
+  constexpr int V = FT<DT>::kVec;
+  const bool wide = a.N % V == 0 && aligned(a.B, 16) && aligned(a.out, 16) && (a.b_stride % V == 0) &&
+                    (!a.addend || aligned(a.addend, 16));
+  if (wide) {
+    const int64_t items = a.nb * a.rows * ((a.N + 64 * V - 1) / (64 * V));
+    hipLaunchKernelGGL((spmm_csr_kernel<DT, V>), dim3(grid_for(items, 4, 16)), dim3(256), 0, st, a);
+  } else {
+    const int64_t items = a.nb * a.rows * ((a.N + 63) / 64);
+    hipLaunchKernelGGL((spmm_csr_kernel<DT, 1>), dim3(grid_for(items, 4, 16)), dim3(256), 0, st, a);
+  }
+  return check_launch("spmm_csr");
+}
+
+}  // namespace
+
+int filter_outlier(const void* x, int dtype, int64_t nb, int64_t rows, int64_t cols, float threshold,
+                   int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices, int32_t* indptr,
+                   void* inlier, hipStream_t st) {
+  if (nb < 0 || rows < 0 || cols < 0 || max_nnz < 0) return set_error(kErrInvalid, "filter_outlier: negative size");
+  if (nb == 0) return kOk;
+  if (!indptr || (max_nnz > 0 && (!data || !indices)) || (rows * cols > 0 && (!x || !inlier)))
+    return set_error(kErrInvalid, "filter_outlier: null buffer");
+  if (max_nnz > INT32_MAX || rows >= INT32_MAX || cols > INT32_MAX)
+    return set_error(kErrInvalid, "filter_outlier: sizes beyond int32 indices");
+  switch (dtype) {
+    case kF32: return launch_filter<kF32>(x, nb, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr, inlier, st);
+    case kBF16: return launch_filter<kBF16>(x, nb, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr, inlier, st);
+    case kF16: return launch_filter<kF16>(x, nb, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr, inlier, st);
+    default: return set_error(kErrInvalid, "filter_outlier: dtype %d not supported (fp32, bf16, fp16)", dtype);
+  }
+}
+
+int csr_slice(const void* data, int dtype, const int32_t* indices, const int32_t* indptr, int64_t nnz_in,
+              int64_t rows, int dim, int64_t start, int64_t end, int64_t max_nnz, void* data_out,
+              int32_t* indices_out, int32_t* indptr_out, hipStream_t st) {
+  if (rows < 0 || nnz_in < 0 || max_nnz < 0) return set_error(kErrInvalid, "slice_csr_tensor: negative size");
+  if (max_nnz > INT32_MAX) return set_error(kErrInvalid, "slice_csr_tensor: capacity beyond int32 indices");
+  if (!indptr || !indptr_out || (max_nnz > 0 && (!data_out || !indices_out)) || (nnz_in > 0 && (!data || !indices)))
+    return set_error(kErrInvalid, "slice_csr_tensor: null buffer");
+  const bool wide16 = dtype == kBF16 || dtype == kF16;
+  if (!wide16 && dtype != kF32)
+    return set_error(kErrInvalid, "slice_csr_tensor: dtype %d not supported (fp32, bf16, fp16)", dtype);
+  if (dim == 0) {
+    if (start < 0 || end < start || end > rows)
+      return set_error(kErrInvalid, "slice_csr_tensor: rows [%lld, %lld] outside [0, %lld]", (long long)start,
+                       (long long)end, (long long)rows);
+    const int64_t nrows_out = end - start;
+    const int64_t n = max_nnz > nrows_out + 1 ? max_nnz : nrows_out + 1;
+    if (wide16)
+      hipLaunchKernelGGL(csr_slice_rows_kernel<uint16_t>, dim3(grid_for(n, 256)), dim3(256), 0, st,
+                         (const uint16_t*)data, indices, indptr, nnz_in, start, nrows_out, max_nnz,
+                         (uint16_t*)data_out, indices_out, indptr_out);
+    else
+      hipLaunchKernelGGL(csr_slice_rows_kernel<uint32_t>, dim3(grid_for(n, 256)), dim3(256), 0, st,
+                         (const uint32_t*)data, indices, indptr, nnz_in, start, nrows_out, max_nnz,
+                         (uint32_t*)data_out, indices_out, indptr_out);
+    return check_launch("slice_csr_tensor");
+  }
+  if (dim != 1) return set_error(kErrInvalid, "slice_csr_tensor: cannot slice along dim %d", dim);
+  if (start < 0) return set_error(kErrInvalid, "slice_csr_tensor: column start must be >= 0");
+  if (rows > 0)
+    hipLaunchKernelGGL(csr_cols_count_kernel, dim3(grid_for(rows, 4, 16)), dim3(256), 0, st, indices, indptr, rows,
+                       nnz_in, start, end, indptr_out);
+  if (wide16) {
+    hipLaunchKernelGGL(csr_scan_kernel<uint16_t>, dim3(1), dim3(1024), 0, st, indptr_out, rows, max_nnz, 0,
+                       (uint16_t*)data_out, indices_out);
+    if (rows > 0)
+      hipLaunchKernelGGL(csr_cols_scatter_kernel<uint16_t>, dim3(grid_for(rows, 4, 16)), dim3(256), 0, st,
+                         (const uint16_t*)data, indices, indptr, rows, nnz_in, start, end, max_nnz, indptr_out,
+                         (uint16_t*)data_out, indices_out);
+  } else {
+    hipLaunchKernelGGL(csr_scan_kernel<uint32_t>, dim3(1), dim3(1024), 0, st, indptr_out, rows, max_nnz, 0,
+                       (uint32_t*)data_out, indices_out);
+    if (rows > 0)
+      hipLaunchKernelGGL(csr_cols_scatter_kernel<uint32_t>, dim3(grid_for(rows, 4, 16)), dim3(256), 0, st,
+                         (const uint32_t*)data, indices, indptr, rows, nnz_in, start, end, max_nnz, indptr_out,
+                         (uint32_t*)data_out, indices_out);
+  }
+  return check_launch("slice_csr_tensor");
+}
+
+int csr_decode(const CsrDecode& d, hipStream_t st) {
+  if (d.nb < 0 || d.br < 0 || d.bc < 0) return set_error(kErrInvalid, "csr_decode: negative size");
+  const int64_t n = d.nb * d.br * d.bc;
+  if (n == 0) return kOk;
+  if (!d.B || !d.out) return set_error(kErrInvalid, "csr_decode: null buffer");
+  if (d.b_dtype < kF32 || d.b_dtype > kU8) return set_error(kErrInvalid, "csr_decode: B dtype %d", d.b_dtype);
+  if (d.out_dtype < kF32 || d.out_dtype > kF16) return set_error(kErrInvalid, "csr_decode: out dtype %d", d.out_dtype);
+  if (d.code && (d.code_len < 1 || d.code_dtype < kF32 || d.code_dtype > kF16))
+    return set_error(kErrInvalid, "csr_decode: bad code table");
+  if (d.scale && (d.scale_dtype < kF32 || d.scale_dtype > kF16 || d.rdiv < 1 || d.cdiv < 1 || d.sr < 1 || d.sc < 1 ||
+                  (d.br - 1) / d.rdiv >= d.sr || (d.bc - 1) / d.cdiv >= d.sc))
+    return set_error(kErrInvalid, "csr_decode: scale does not cover B");
+  const int64_t tiles = d.nb * ((d.br + 63) / 64) * ((d.bc + 63) / 64);
+  hipLaunchKernelGGL(csr_decode_kernel, dim3(grid_for(tiles, 1, 8)), dim3(256), 0, st, d);
+  return check_launch("csr_decode");
+}
+
+int spmm_csr(const SpmmArgs& a, hipStream_t st) {
+  if (a.nb < 0 || a.rows < 0 || a.K < 0 || a.N < 0 || a.nnz_stride < 0 || a.b_stride < 0)
+    return set_error(kErrInvalid, "spmm_csr: negative size");
+  if (a.nb * a.rows * a.N == 0) return kOk;
+  if (!a.indptr || !a.B || !a.out || (a.nnz_stride > 0 && (!a.data || !a.indices)))
+    return set_error(kErrInvalid, "spmm_csr: null buffer");
+  if (a.data_dtype < kF32 || a.data_dtype > kF16) return set_error(kErrInvalid, "spmm_csr: data dtype %d", a.data_dtype);
+  switch (a.b_dtype) {
+    case kF32: return launch_spmm<kF32>(a, st);
+    case kBF16: return launch_spmm<kBF16>(a, st);
+    case kF16: return launch_spmm<kF16>(a, st);
+    default: return set_error(kErrInvalid, "spmm_csr: B dtype %d not supported (fp32, bf16, fp16)", a.b_dtype);
+  }
+}
+
+}  // namespace vqx

@@ -2,7 +2,7 @@
 
 Same qualified names and schema strings as the reference library
 (src/voyager_compiler/ops/quantized.py:12, :98, :124-128, :175-179, :286-292,
-:363-368, :435-439, :502-506), so converted graphs and FakeQuantize modules
+:363-368, :435-439, :502-506, :532-535, :633-639, :715-719, :809-813), so converted graphs and FakeQuantize modules
 call into these kernels unchanged.  Every op has a kernel for the CUDA
 dispatch key only (HIP tensors on ROCm dispatch there) plus a fake
 implementation for tracing; CPU tensors raise, there is no CPU path.
@@ -53,6 +53,23 @@ _SCHEMAS = {
         "quantize_mx(Tensor self, Tensor qmap, SymInt[] axes, int block_size, "
         "float quant_max, bool force_scale_power_of_two=False, "
         "Tensor scale_qmap=None, Tensor output_code=None) -> (Tensor, Tensor)"),
+    "filter_outlier": (
+        "filter_outlier(Tensor input, float threshold, float max_pct=0.01) "
+        "-> (Tensor, Tensor, Tensor, Tensor)"),
+    "quantize_mx_outlier": (
+        "quantize_mx_outlier(Tensor self, Tensor qmap, SymInt[] axes, "
+        "int block_size, float quant_max, bool force_scale_power_of_two=False, "
+        "Tensor scale_qmap=None, Tensor output_code=None, float? threshold=None, "
+        "float max_pct=0.01, SymInt indptr_offset=0) "
+        "-> (Tensor, Tensor, Tensor, Tensor, Tensor)"),
+    "slice_csr_tensor": (
+        "slice_csr_tensor(Tensor data, Tensor indices, Tensor indptr, int dim=0, "
+        "SymInt? start=None, SymInt? end=None, float size_factor=1.0) "
+        "-> (Tensor, Tensor, Tensor)"),
+    "spmm_csr": (
+        "spmm_csr(Tensor data, Tensor indices, Tensor indptr, Tensor B, "
+        "Tensor? B_scale=None, Tensor? B_code=None, int? block_size=None, "
+        'str weight_layout="kc") -> Tensor'),
     # this build's own
     "fake_quant": (
         "fake_quant(Tensor self, str dtype, Tensor? scale=None, bool mul_back=True, "
@@ -415,25 +432,23 @@ def _decode_operand(t, code, scale, block_size):
     return dequantize(t, scale, None, None, block_size, lut, None)
 
 
-def _no_outliers(A_data):
-    if A_data is not None:
-        raise NotImplementedError("vqx: the CSR outlier path (A_data/A_indices/A_indptr) is not implemented")
-
-
 @_impl("linear_mx")
 def linear_mx(input, weight, bias=None, *, input_scale=None, weight_scale=None, block_size=None,
               input_code=None, weight_code=None, A_data=None, A_indices=None, A_indptr=None,
               weight_layout="kc"):
     assert weight_layout in ("kc", "ck"), weight_layout
     _lib.require_device(input, "linear_mx")
-    _no_outliers(A_data)
     if weight_layout != "kc":
         raise NotImplementedError("vqx: the 'ck' hardware weight layout is not implemented")
     x = _decode_operand(input, input_code, input_scale, block_size)
     w = _decode_operand(weight, weight_code, weight_scale, block_size)
     if weight_code is not None:
         w = w.to(weight.dtype)
-    return torch.nn.functional.linear(x, w, bias)
+    dense = torch.nn.functional.linear(x, w, bias)
+    if A_data is None:
+        return dense
+    return _spmm(A_data, A_indices, A_indptr, weight, weight_scale, weight_code, block_size, weight_layout,
+                 addend=dense)
 
 
 @_impl("matmul_mx")
@@ -441,12 +456,221 @@ def matmul_mx(self, other, *, input_scale=None, weight_scale=None, block_size=No
               weight_code=None, A_data=None, A_indices=None, A_indptr=None, weight_layout="ck"):
     assert weight_layout in ("kc", "ck"), weight_layout
     _lib.require_device(self, "matmul_mx")
-    _no_outliers(A_data)
     if weight_layout != "ck":
         raise NotImplementedError("vqx: the 'kc' hardware layout for matmul is not implemented")
     a = _decode_operand(self, input_code, input_scale, block_size)
     b = _decode_operand(other, weight_code, weight_scale, block_size)
-    return torch.matmul(a, b.contiguous())
+    dense = torch.matmul(a, b.contiguous())
+    if A_data is None:
+        return dense
+    return _spmm(A_data, A_indices, A_indptr, other, weight_scale, weight_code, block_size, weight_layout,
+                 addend=dense)
+
+
+# ---------------------------------------------------------------------------
+# outliers as CSR: filter_outlier, quantize_mx_outlier, slice_csr_tensor,
+# spmm_csr (quantized.py:532-895)
+# ---------------------------------------------------------------------------
+_FLOAT_TAGS = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _float_tag(t, what):
+    if t.dtype not in _FLOAT_TAGS:
+        raise ValueError(f"vqx: {what} takes float32/bfloat16/float16 values, not {t.dtype}")
+    return _lib.dtype_tag(t.dtype)
+
+
+def _int32_index(t, what):
+    if t.dtype != torch.int32:
+        raise ValueError(f"vqx: {what} must be int32, not {t.dtype}")
+    return t.contiguous()
+
+
+def _outlier_csr(input, threshold, max_pct, indptr_offset):
+    """filter_outlier (quantized.py:572-630) with the row pointers shifted by
+    indptr_offset, on the GPU: (data, indices, indptr, inlier)."""
+    _lib.require_device(input, "filter_outlier")
+    if threshold is None:
+        raise TypeError("filter_outlier: threshold must be a float, not None")
+    if input.ndim < 2:
+        raise ValueError(f"filter_outlier: input must have at least 2 dims, got {input.ndim}")
+    x = input.contiguous()
+    tag = _float_tag(x, "filter_outlier")
+    batch_shape = x.shape[:-2]
+    R, C = x.shape[-2:]
+    max_nnz = int(math.prod(x.shape[-2:]) * max_pct)
+    if max_nnz < 0:
+        raise ValueError(f"filter_outlier: max_pct {max_pct} gives a negative capacity")
+    if not -(1 << 31) <= indptr_offset < (1 << 31):
+        raise ValueError(f"indptr_offset {indptr_offset} does not fit the int32 row pointers")
+    # torch compares against the Python scalar cast to the tensor's dtype
+    t = torch.tensor(float(threshold), dtype=x.dtype).item()
+    nb = math.prod(batch_shape)
+    dev = x.device
+    data = torch.empty((*batch_shape, max_nnz), dtype=x.dtype, device=dev)
+    indices = torch.empty((*batch_shape, max_nnz), dtype=torch.int32, device=dev)
+    indptr = torch.empty((*batch_shape, R + 1), dtype=torch.int32, device=dev)
+    inlier = torch.empty_like(x)
+    _lib.call("vqx_filter_outlier", _lib.ptr(x), tag, nb, R, C, t, max_nnz, int(indptr_offset), _lib.ptr(data),
+              _lib.ptr(indices), _lib.ptr(indptr), _lib.ptr(inlier), _lib.stream_of(x))
+    return data, indices, indptr, inlier
+
+
+@_impl("filter_outlier")
+def filter_outlier(input, threshold, max_pct=0.01):
+    """Outliers (|x| > threshold) as a per-matrix CSR over the last two dims,
+    int32 indices, data/indices sized int(rows*cols*max_pct) and padded with
+    0/-1 (the first entries in row-major order kept on overflow, row pointers
+    clamped), plus the input with outliers zeroed (quantized.py:537-630)."""
+    return _outlier_csr(input, threshold, max_pct, 0)
+
+
+@_impl("quantize_mx_outlier")
+def quantize_mx_outlier(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False,
+                        scale_qmap=None, output_code=None, threshold=None, max_pct=0.01, indptr_offset=0):
+    """filter_outlier, row pointers + indptr_offset, then quantize_mx of the
+    inliers (quantized.py:642-691): (data, indices, indptr, scale, inliers)."""
+    data, indices, indptr, inliers = _outlier_csr(input, threshold, max_pct, indptr_offset)
+    scale, q = quantize_mx(inliers, qmap, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap)
+    return data, indices, indptr, scale, q
+
+
+@_impl("slice_csr_tensor")
+def slice_csr_tensor(data, indices, indptr, dim=0, start=None, end=None, size_factor=1.0):
+    """Rows (dim 0) or columns (dim 1) [start, end) of one CSR matrix, data and
+    indices sized int(len(data) * size_factor) and padded like filter_outlier's
+    (quantized.py:722-777)."""
+    dim = dim + 2 if dim < 0 else dim
+    if dim not in (0, 1):
+        raise ValueError(f"Cannot slice sparse CSR matrix along dim {dim}")
+    _lib.require_device(data, "slice_csr_tensor")
+    if data.ndim != 1 or indices.ndim != 1 or indptr.ndim != 1:
+        raise ValueError("slice_csr_tensor takes one CSR matrix: 1-D data, indices and indptr")
+    if start is None or end is None:
+        raise TypeError("slice_csr_tensor: start and end are required")
+    tag = _float_tag(data, "slice_csr_tensor")
+    data = data.contiguous()
+    indices = _int32_index(indices, "slice_csr_tensor indices")
+    indptr = _int32_index(indptr, "slice_csr_tensor indptr")
+    rows = indptr.numel() - 1
+    if rows < 0:
+        raise ValueError("slice_csr_tensor: indptr is empty")
+    max_nnz = int(data.shape[0] * size_factor)
+    if max_nnz < 0:
+        raise ValueError(f"slice_csr_tensor: size_factor {size_factor} gives a negative capacity")
+    dev = data.device
+    if dim == 0:
+        L = rows + 1
+        s = start + L if start < 0 else start
+        e = end + L if end < 0 else end
+        n_out = len(range(L)[start:end + 1])
+        if not (0 <= s <= e <= rows) or n_out != e - s + 1:
+            raise IndexError(f"slice_csr_tensor: rows [{start}, {end}) of a {rows}-row matrix")
+        indptr_out = torch.empty(n_out, dtype=torch.int32, device=dev)
+    else:
+        if start < 0:
+            raise ValueError("slice_csr_tensor: column slices start at a column >= 0")
+        s, e = start, end
+        indptr_out = torch.empty_like(indptr)
+    data_out = torch.empty(max_nnz, dtype=data.dtype, device=dev)
+    indices_out = torch.empty(max_nnz, dtype=torch.int32, device=dev)
+    _lib.call("vqx_slice_csr", _lib.ptr(data), tag, _lib.ptr(indices), _lib.ptr(indptr), data.numel(), rows, dim,
+              s, e, max_nnz, _lib.ptr(data_out), _lib.ptr(indices_out), _lib.ptr(indptr_out), _lib.stream_of(data))
+    return data_out, indices_out, indptr_out
+
+
+def _scale_index(scale, shape, block_size):
+    """The element -> scale map of expand(scale, shape, block_size)
+    (quantized.py:82-95) for a [.., rows, cols] operand:
+    (batch stride, scale rows, scale cols, row block, col block)."""
+    s = list(scale.shape)
+    if len(s) > len(shape):
+        raise ValueError(f"scale shape {tuple(scale.shape)} has more dims than {tuple(shape)}")
+    s = [1] * (len(shape) - len(s)) + s
+    div = []
+    for a, b in zip(s, shape):
+        if a == b:
+            div.append(1)
+        elif block_size is not None and a * block_size >= b:
+            div.append(block_size)
+        elif a == 1 and block_size == 1:
+            div.append(max(b, 1))  # stays size 1 and broadcasts
+        else:
+            raise ValueError(f"scale shape {tuple(scale.shape)} does not expand to {tuple(shape)} "
+                             f"with block_size {block_size}")
+    sr, sc = s[-2], s[-1]
+    lead = list(zip(s[:-2], shape[:-2], div[:-2]))
+    if all(d == 1 for _, _, d in lead):
+        sb = sr * sc
+    elif all(b <= d for _, b, d in lead):
+        sb = 0  # every batch maps to scale batch 0
+    else:
+        raise NotImplementedError("vqx: scales blocked across batch dims are not supported")
+    return sb, sr, sc, div[-2], div[-1]
+
+
+def _spmm(data, indices, indptr, B, B_scale=None, B_code=None, block_size=None, weight_layout="kc",
+          addend=None):
+    """spmm_csr (quantized.py:816-878) on the GPU; with an addend of the
+    output's shape and dtype, addend + spmm in the same pass."""
+    assert weight_layout in ("kc", "ck"), weight_layout
+    _lib.require_device(B, "spmm_csr")
+    if B.ndim < 2:
+        raise ValueError("spmm_csr: B must have at least 2 dims")
+    dev = B.device
+    out_dtype = B.dtype if B_code is None else B_code.dtype
+    if B_scale is not None:
+        out_dtype = torch.promote_types(out_dtype, B_scale.dtype)
+    if out_dtype not in _FLOAT_TAGS:
+        raise ValueError(f"vqx: spmm_csr computes in float32/bfloat16/float16, not {out_dtype}")
+    batch_shape = indptr.shape[:-1]
+    nb = math.prod(batch_shape)
+    R = indptr.shape[-1] - 1
+    indptr2 = _int32_index(indptr, "spmm_csr indptr").reshape(nb, R + 1)
+    indices2 = _int32_index(indices, "spmm_csr indices").reshape(nb, -1)
+    data2 = data.contiguous().reshape(nb, -1)
+    dtag = _float_tag(data2, "spmm_csr data")
+    if indices2.shape[1] != data2.shape[1]:
+        raise ValueError("spmm_csr: data and indices must have the same length")
+    br, bc = B.shape[-2:]
+    nbB = math.prod(B.shape[:-2]) if B.ndim > 2 else 1
+    if B.ndim > 2 and nbB != nb:
+        raise ValueError(f"spmm_csr: B holds {nbB} matrices for {nb} CSR batches")
+    K, N = (bc, br) if weight_layout == "kc" else (br, bc)
+    Bc = B.contiguous()
+    if B_code is None and B_scale is None and weight_layout == "ck":
+        Bt = Bc
+    else:
+        Bt = torch.empty((nbB, K, N), dtype=out_dtype, device=dev)
+        code = None if B_code is None else B_code.reshape(-1).contiguous()
+        scale = None if B_scale is None else B_scale.contiguous()
+        sb, sr, sc, rdiv, cdiv = (0, 1, 1, 1, 1) if scale is None else _scale_index(scale, B.shape, block_size)
+        if code is not None and code.dtype not in _FLOAT_TAGS:
+            raise ValueError(f"vqx: B_code must be float32/bfloat16/float16, not {code.dtype}")
+        if scale is not None and scale.dtype not in _FLOAT_TAGS:
+            raise ValueError(f"vqx: B_scale must be float32/bfloat16/float16, not {scale.dtype}")
+        _lib.call("vqx_csr_decode_weight", _lib.ptr(Bc), _lib.dtype_tag(Bc.dtype), nbB, br, bc,
+                  1 if weight_layout == "kc" else 0, _lib.ptr(code),
+                  _lib.dtype_tag(code.dtype) if code is not None else 0, 0 if code is None else code.numel(),
+                  _lib.ptr(scale), _lib.dtype_tag(scale.dtype) if scale is not None else 0, sb, sr, sc, rdiv, cdiv,
+                  _lib.ptr(Bt), _lib.dtype_tag(out_dtype), _lib.stream_of(Bc))
+    out_shape = (*batch_shape, R, N)
+    fuse = (addend is not None and addend.dtype == out_dtype and tuple(addend.shape) == out_shape
+            and addend.is_contiguous() and addend.device == dev)
+    out = torch.empty(out_shape, dtype=out_dtype, device=dev)
+    _lib.call("vqx_spmm_csr", _lib.ptr(data2), dtag, _lib.ptr(indices2), _lib.ptr(indptr2), nb, R, data2.shape[1],
+              _lib.ptr(Bt), _lib.dtype_tag(out_dtype), K * N if B.ndim > 2 else 0, K, N,
+              _lib.ptr(addend) if fuse else None, _lib.ptr(out), _lib.stream_of(Bc))
+    if addend is not None and not fuse:
+        return addend + out
+    return out
+
+
+@_impl("spmm_csr")
+def spmm_csr(data, indices, indptr, B, B_scale=None, B_code=None, block_size=None, weight_layout="kc"):
+    """Per-batch CSR [rows, K] x decoded B [K, N] in fp32, cast to the decoded
+    B's dtype (quantized.py:816-878)."""
+    return _spmm(data, indices, indptr, B, B_scale, B_code, block_size, weight_layout)
 
 
 # ---------------------------------------------------------------------------
@@ -635,6 +859,47 @@ def _(input, weight, bias=None, **kwargs):
 @torch.library.register_fake("quantized_ops::matmul_mx")
 def _(self, other, **kwargs):
     return torch.matmul(self, other)
+
+
+def _csr_fake(input, max_pct):
+    batch_shape = input.shape[:-2]
+    max_nnz = int(math.prod(input.shape[-2:]) * max_pct)
+    return (input.new_empty((*batch_shape, max_nnz)),
+            input.new_empty((*batch_shape, max_nnz), dtype=torch.int32),
+            input.new_empty((*batch_shape, input.shape[-2] + 1), dtype=torch.int32))
+
+
+@torch.library.register_fake("quantized_ops::filter_outlier")
+def _(input, threshold, max_pct=0.01):
+    data, indices, indptr = _csr_fake(input, max_pct)
+    return data, indices, indptr, torch.empty_like(input)
+
+
+@torch.library.register_fake("quantized_ops::quantize_mx_outlier")
+def _(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False, scale_qmap=None,
+      output_code=None, threshold=None, max_pct=0.01, indptr_offset=0):
+    data, indices, indptr = _csr_fake(input, max_pct)
+    shape = list(input.shape)
+    for a in ([axes] if isinstance(axes, int) else axes):
+        shape[a] = -(-shape[a] // block_size)
+    return (data, indices, indptr, input.new_empty(shape),
+            torch.empty_like(input, memory_format=torch.contiguous_format))
+
+
+@torch.library.register_fake("quantized_ops::slice_csr_tensor")
+def _(data, indices, indptr, dim=0, start=None, end=None, size_factor=1.0):
+    max_nnz = int(data.shape[0] * size_factor)
+    rows = indptr.shape[0] if dim not in (0, -2) else len(range(indptr.shape[0])[start:end + 1])
+    return (data.new_empty((max_nnz,)), indices.new_empty((max_nnz,)), indptr.new_empty((rows,)))
+
+
+@torch.library.register_fake("quantized_ops::spmm_csr")
+def _(data, indices, indptr, B, B_scale=None, B_code=None, block_size=None, weight_layout="kc"):
+    dt = B.dtype if B_code is None else B_code.dtype
+    if B_scale is not None:
+        dt = torch.promote_types(dt, B_scale.dtype)
+    N = B.shape[-2] if weight_layout == "kc" else B.shape[-1]
+    return data.new_empty((*indptr.shape[:-1], indptr.shape[-1] - 1, N), dtype=dt)
 
 
 @torch.library.register_fake("quantized_ops::fake_quant")
