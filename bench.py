@@ -199,6 +199,89 @@ def setup_c5(vqx, torch, L):
         bound="mfma", dtype="bf16")
 
 
+def outlier_input(torch, rows=4096, cols=11008, seed=5):
+    """Activation-like bf16 [tokens, features]: N(0,1) with 0.5% of the
+    entries scaled by 32, the outliers the CSR path splits off (|x| > 6)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, cols, generator=g)
+    m = torch.rand(rows, cols, generator=g) < 0.005
+    return torch.where(m, x * 32, x).to(torch.bfloat16)
+
+
+OUTLIER_THRESHOLD, OUTLIER_PCT = 6.0, 0.01
+
+
+def _outlier_csr(torch, L, x):
+    R, C = x.shape
+    max_nnz = int(R * C * OUTLIER_PCT)
+    bufs = dict(data=torch.empty(max_nnz, dtype=torch.bfloat16, device="cuda"),
+                idx=torch.empty(max_nnz, dtype=torch.int32, device="cuda"),
+                ptr=torch.empty(R + 1, dtype=torch.int32, device="cuda"),
+                inl=torch.empty_like(x))
+    args = (L.ptr(x), L.BF16, 1, R, C, L.ctypes.c_float(OUTLIER_THRESHOLD), max_nnz, 0, L.ptr(bufs["data"]),
+            L.ptr(bufs["idx"]), L.ptr(bufs["ptr"]), L.ptr(bufs["inl"]), L.stream_of(x))
+    return bufs, args, max_nnz
+
+
+def setup_o1(vqx, torch, L, mx=False):
+    xc = outlier_input(torch)
+    x = xc.cuda()
+    R, C = x.shape
+    n = x.numel()
+    bufs, fargs, max_nnz = _outlier_csr(torch, L, x)
+    filt = L.load().vqx_filter_outlier
+    filt(*fargs)
+    torch.cuda.synchronize()
+    nnz = int(bufs["ptr"][-1])
+    csr_bytes = 6 * max_nnz + 4 * (R + 1)
+    common = dict(elements=n, bound="hbm", dtype="bf16", nnz=nnz,
+                  cpu_input=(xc, OUTLIER_THRESHOLD, OUTLIER_PCT))
+    if not mx:
+        return (lambda: filt(*fargs)), dict(
+            name=f"O1 filter_outlier, bf16 4096x11008 N(0,1) with 0.5% x32 seed 5, |x| > {OUTLIER_THRESHOLD}, "
+                 f"capacity 1% -> CSR ({nnz} outliers) + inliers",
+            bytes=4 * n + csr_bytes, **common)
+    fmt = vqx.parse_format("fp8_e4m3")
+    desc = fmt.desc(x.device)
+    sc = torch.empty(R, C // 32, dtype=torch.bfloat16, device="cuda")
+    qv = torch.empty_like(x)
+    mxq = L.load().vqx_mx_quantize
+    margs = (L.ptr(bufs["inl"]), L.BF16, R, C, 1, 32, L.ctypes.byref(desc), 0, 8, L.ctypes.c_float(448.0), None,
+             L.ptr(sc), None, None, L.ptr(qv), None, None, 1, L.stream_of(x))
+
+    def launch():
+        rc = filt(*fargs)
+        return rc if rc else mxq(*margs)
+    return launch, dict(
+        name=f"O2 quantize_mx_outlier: O1's split, then MX block-32 fp8_e4m3 power-of-two scales of the inliers "
+             f"-> CSR + bf16 scales + bf16 quantized inliers",
+        bytes=4 * n + n // 32 * 2 + csr_bytes, keep=(desc, fmt), **common)
+
+
+def setup_o3(vqx, torch, L):
+    x = outlier_input(torch).cuda()
+    R, K = x.shape
+    N = 4096
+    bufs, fargs, max_nnz = _outlier_csr(torch, L, x)
+    L.load().vqx_filter_outlier(*fargs)
+    torch.cuda.synchronize()
+    nnz = int(bufs["ptr"][-1])
+    del x
+    g = torch.Generator().manual_seed(6)
+    Bc = (0.02 * torch.randn(K, N, generator=g)).to(torch.bfloat16)
+    B = Bc.cuda()
+    out = torch.empty(R, N, dtype=torch.bfloat16, device="cuda")
+    fn = L.load().vqx_spmm_csr
+    args = (L.ptr(bufs["data"]), L.BF16, L.ptr(bufs["idx"]), L.ptr(bufs["ptr"]), 1, R, max_nnz, L.ptr(B), L.BF16,
+            0, K, N, None, L.ptr(out), L.stream_of(B))
+    cpu = (bufs["data"].cpu(), bufs["idx"].cpu(), bufs["ptr"].cpu(), Bc)
+    return (lambda: fn(*args)), dict(
+        name=f"O3 spmm_csr: O1's CSR [4096 x 11008] ({nnz} entries) x bf16 [11008, 4096] ('ck') -> bf16, "
+             f"fp32 accumulate",
+        elements=R * N, bytes=nnz * 6 + 4 * (R + 1) + K * N * 2 + R * N * 2, gathered_bytes=nnz * N * 2,
+        flops=2 * nnz * N, bound="hbm", dtype="bf16", nnz=nnz, cpu_input=cpu, keep=bufs)
+
+
 CONFIGS = {
     "c2": lambda v, t, L: setup_c2(v, t, L),
     "c1": lambda v, t, L: setup_c1(v, t, L),
@@ -211,6 +294,9 @@ CONFIGS = {
     "c4_k256": lambda v, t, L: setup_c4(v, t, L, 256),
     "c4_k16_decode": lambda v, t, L: setup_c4(v, t, L, 16, decode=True),
     "c5": lambda v, t, L: setup_c5(v, t, L),
+    "o1_filter": lambda v, t, L: setup_o1(v, t, L),
+    "o2_quantize_mx_outlier": lambda v, t, L: setup_o1(v, t, L, mx=True),
+    "o3_spmm": lambda v, t, L: setup_o3(v, t, L),
 }
 HEADLINE = "c2"
 
@@ -290,6 +376,35 @@ def cpu_baseline_c2(torch, x):
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
 
 
+def cpu_oracle_time(torch, k, info, kernel_ms):
+    """One run of the CPU oracle (the reference's torch-CPU op sequence) on a
+    outlier config's full input, timed beside the GPU figure."""
+    from oracle import formats as F
+    from oracle import reference_ops as R
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    if k == "o3_spmm":
+        d, i, p, B = info["cpu_input"]
+
+        def fn():
+            return R.spmm_csr(d, i, p, B, weight_layout="ck")
+    else:
+        x, t, pct = info["cpu_input"]
+        if k == "o1_filter":
+            def fn():
+                return R.filter_outlier(x, t, pct)
+        else:
+            qmap = R.table_tensor(F.quantization_table("fp8_e4m3"))
+
+            def fn():
+                return R.quantize_mx_outlier(x, qmap, [-1], 32, 448.0, True, threshold=t, max_pct=pct)
+    t0 = time.perf_counter()
+    fn()
+    dt = time.perf_counter() - t0
+    return {"seconds": dt, "cores": torch.get_num_threads(), "kind": "port", "gpu_speedup": dt / (kernel_ms * 1e-3),
+            "sample": "one run on the config's full input"}
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -313,6 +428,9 @@ DOMINANT = {
     "c4_k256": "cb_encode_kernel<float, 8>",
     "c4_k16_decode": "cb_decode_kernel<float>",
     "c5": "nf4_gemm_kernel",
+    "o1_filter": "outlier_split_kernel<1, 8>",
+    "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8>",
+    "o3_spmm": "spmm_csr_kernel<1, 8>",
 }
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
 
@@ -433,6 +551,14 @@ def main():
         else:
             print(f"[bench] {k}: {ms * 1e3:.1f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)",
                   file=sys.stderr, flush=True)
+        if "nnz" in info:
+            results[k]["nnz"] = info["nnz"]
+        if "gathered_bytes" in info:
+            results[k]["gathered_bytes"] = info["gathered_bytes"]
+            results[k]["gathered_GBps"] = info["gathered_bytes"] / (ms * 1e-3) / 1e9
+            results[k]["achieved_TFLOPs"] = info["flops"] / (ms * 1e-3) / 1e12
+        if k.startswith("o") and not a.no_cpu:
+            results[k]["cpu_oracle"] = cpu_oracle_time(torch, k, info, ms)
         if k == HEADLINE:
             info_head = info
         del launch

@@ -152,15 +152,6 @@ __device__ __forceinline__ void load_chunk(const T* xr, int64_t base, int lane, 
   }
 }
 
-// Wave-level LDS hand-off: the wave's own LDS writes are complete and visible
-// to all its lanes before any lane reads past this point.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-}
-
 // Per-channel encode.  Each wave works through its own rows (row gw, gw + nw,
 // ... for global wave gw of nw) with no workgroup barriers; the items it
 // streams are the 1024-element chunks of those rows in order, in two register

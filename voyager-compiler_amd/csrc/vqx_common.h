@@ -74,6 +74,15 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint3
                                0x05040100u);
 }
 
+// Wave-level LDS hand-off: the wave's own LDS writes are complete and visible
+// to all its lanes before any lane reads past this point.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
 // Exact fp16 <-> fp32 conversions in integer arithmetic (subnormals and signed
 // zeros kept, round to nearest even), independent of the device's fp16
 // denormal mode; torch's CPU conversions are the reference.

@@ -6,11 +6,13 @@
 //                            x != 0) and stores the count where the row's end
 //                            pointer goes (indptr[b][r + 1]);
 //   2. csr_scan_kernel       one workgroup per batch turns those counts into
-//                            row pointers in place, clamped to the capacity,
-//                            and pads data / indices past the last entry with
-//                            0 / -1;
-//   3. outlier_split_kernel  one wave per row writes the inliers and scatters
-//                            the outliers, in column order, to their CSR slots.
+//                            row pointers in place, clamped to the capacity;
+//   3. outlier_split_kernel  one wave per row reads the row again, writes the
+//                            inliers, gathers the outliers in column order in
+//                            LDS and writes them to their CSR slots as one
+//                            contiguous run;
+//                            the whole grid then pads data / indices past the
+//                            last entry with 0 / -1.
 // An outlier's slot is its row's pointer plus its rank within the row; ranks
 // come from wave ballots (lane-major, so column order is kept).  Entries past
 // the capacity are dropped, which keeps the first max_nnz in row-major order.
@@ -18,8 +20,8 @@
 // The column slice of a CSR matrix reuses the same count -> scan -> scatter
 // shape over the stored entries; the row slice is one gather launch.
 //
-// spmm_csr: one wave per (row, 64*V-column chunk) of the output runs down the
-// row's entries in order and accumulates a * B[k, n] in fp32 (B row-major
+// spmm_csr: one wave per (row, 1 KiB column chunk) of the output runs down
+// the row's entries in order and accumulates a * B[k, n] in fp32 (B row-major
 // [K, N]).  A "kc"-stored or coded/scaled B is first decoded and transposed
 // into that layout by csr_decode_kernel, in the dtype the reference's decode
 // produces.
@@ -56,24 +58,28 @@ struct FT<kF16> {
   __device__ static uint32_t bits(float f) { return f2h_exact(f); }
 };
 
-// V consecutive elements starting at p: one 16-byte load when V fills it,
-// else V element loads.  Element j of the group is get(w, j).
+// V consecutive elements starting at p: one 16-byte or 4-byte load when V
+// fills it, else V element loads.  Element j of the group is get(j).
 template <typename S, int V>
 struct Group {
-  static constexpr bool kWide = V * sizeof(S) == 16;
-  uint32_t w[V * sizeof(S) / 4 > 0 ? V * sizeof(S) / 4 : 1];
-  S e[kWide ? 1 : V];
+  static constexpr int kBytes = V * (int)sizeof(S);
+  static constexpr bool kWide = kBytes == 16;
+  static constexpr bool kWord = kBytes == 4 && V > 1;
+  uint32_t w[kBytes / 4 > 0 ? kBytes / 4 : 1];
+  S e[(kWide || kWord) ? 1 : V];
   __device__ void load(const S* p) {
     if constexpr (kWide) {
       u32x4 v = *(const u32x4*)p;
       w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
+    } else if constexpr (kWord) {
+      w[0] = *(const uint32_t*)p;
     } else {
 #pragma unroll
       for (int j = 0; j < V; ++j) e[j] = p[j];
     }
   }
   __device__ uint32_t get(int j) const {
-    if constexpr (kWide) {
+    if constexpr (kWide || kWord) {
       if constexpr (sizeof(S) == 4) return w[j];
       else return (w[j >> 1] >> ((j & 1) * 16)) & 0xFFFFu;
     } else {
@@ -82,7 +88,9 @@ struct Group {
   }
 };
 
-template <typename S, int V>
+// NT: non-temporal (streaming) store, so that a write-once output does not
+// push re-read data out of the caches.
+template <typename S, int V, bool NT = false>
 __device__ __forceinline__ void store_group(S* p, const uint32_t (&b)[V]) {
   if constexpr (V * sizeof(S) == 16) {
     u32x4 v;
@@ -91,7 +99,10 @@ __device__ __forceinline__ void store_group(S* p, const uint32_t (&b)[V]) {
     } else {
       v = u32x4{b[0] | b[1] << 16, b[2] | b[3] << 16, b[4] | b[5] << 16, b[6] | b[7] << 16};
     }
-    *(u32x4*)p = v;
+    if constexpr (NT) st_nt((u32x4*)p, v);
+    else *(u32x4*)p = v;
+  } else if constexpr (V * sizeof(S) == 4 && V == 2) {
+    *(uint32_t*)p = b[0] | b[1] << 16;
   } else {
 #pragma unroll
     for (int j = 0; j < V; ++j) p[j] = (S)b[j];
@@ -124,8 +135,9 @@ __device__ __forceinline__ int64_t wave_incl_scan(int64_t v, int lane) {
 // ---------------------------------------------------------------------------
 // filter_outlier
 // ---------------------------------------------------------------------------
-// Row group loads are clamped into the row (cols >= V), so every lane loads
-// unconditionally and lanes past the end only drop their flags.
+// Pass 1 counts each row's outliers.  Row group loads are clamped into the
+// row (cols >= V), so every lane loads unconditionally and lanes past the end
+// only drop their flags.
 template <int DT, int V>
 __global__ __launch_bounds__(256) void outlier_count_kernel(const typename FT<DT>::S* __restrict__ x,
                                                             int64_t nrows, int64_t rows, int64_t cols,
@@ -161,12 +173,9 @@ __global__ __launch_bounds__(256) void outlier_count_kernel(const typename FT<DT
 
 // In place: indptr[b][r + 1] holds row r's count on entry and
 // min(prefix, max_nnz) + offset on exit (int32 wrap-around, as the
-// reference's int32 add); indptr[b][0] = offset.  Slots from min(total,
-// max_nnz) to max_nnz of data / indices get 0 / -1.
-template <typename S>
+// reference's int32 add); indptr[b][0] = offset.
 __global__ __launch_bounds__(1024) void csr_scan_kernel(int32_t* __restrict__ indptr, int64_t rows, int64_t max_nnz,
-                                                        int32_t offset, S* __restrict__ data,
-                                                        int32_t* __restrict__ indices) {
+                                                        int32_t offset) {
   __shared__ int64_t wsum[16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int64_t b = blockIdx.x;
@@ -178,12 +187,8 @@ __global__ __launch_bounds__(1024) void csr_scan_kernel(int32_t* __restrict__ in
   const int64_t incl = wave_incl_scan(s, lane);
   if (lane == 63) wsum[wv] = incl;
   __syncthreads();
-  int64_t before = 0, total = 0;
-  for (int w = 0; w < 16; ++w) {
-    const int64_t v = wsum[w];
-    before += w < wv ? v : 0;
-    total += v;
-  }
+  int64_t before = 0;
+  for (int w = 0; w < wv; ++w) before += wsum[w];
   int64_t run = before + incl - s;
   for (int64_t r = r0; r < r1; ++r) {
     run += ptr[r + 1];
@@ -191,24 +196,50 @@ __global__ __launch_bounds__(1024) void csr_scan_kernel(int32_t* __restrict__ in
     ptr[r + 1] = (int32_t)((uint32_t)c + (uint32_t)offset);
   }
   if (tid == 0) ptr[0] = offset;
-  const int64_t used = total < max_nnz ? total : max_nnz;
-  for (int64_t j = used + tid; j < max_nnz; j += 1024) {
-    data[b * max_nnz + j] = (S)0;
-    indices[b * max_nnz + j] = -1;
+}
+
+// Slots [indptr[b][rows] - indptr[b][0], max_nnz) of every batch's data /
+// indices get 0 / -1, spread over the whole grid (the pointers are clamped,
+// so the kept entries never reach past max_nnz).
+template <typename S>
+__device__ void pad_tail(const int32_t* __restrict__ indptr, int64_t rows, int64_t nb, int64_t max_nnz,
+                         S* __restrict__ data, int32_t* __restrict__ indices) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nt = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t b = 0; b < nb; ++b) {
+    const int32_t* ptr = indptr + b * (rows + 1);
+    const int64_t used = (int64_t)(uint32_t)((uint32_t)ptr[rows] - (uint32_t)ptr[0]);
+    for (int64_t j = used + tid; j < max_nnz; j += nt) {
+      data[b * max_nnz + j] = (S)0;
+      indices[b * max_nnz + j] = -1;
+    }
   }
 }
 
+// Pass 2 reads each row again, writes the inliers (every |x| > t becomes +0,
+// zeros too when t is negative) and moves the outliers (the nonzero ones), in
+// column order, to their CSR slots.  Each wave gathers its row's outliers in
+// an LDS buffer
+// (slot = running count + rank from the ballots) and writes them out as one
+// contiguous run when the row ends or the buffer nears full, instead of
+// scattering 2- and 4-byte stores.
 template <int DT, int V>
 __global__ __launch_bounds__(256) void outlier_split_kernel(const typename FT<DT>::S* __restrict__ x,
-                                                            int64_t nrows, int64_t rows, int64_t cols,
+                                                            int64_t nb, int64_t rows, int64_t cols,
                                                             float t, const int32_t* __restrict__ indptr,
                                                             int64_t max_nnz, typename FT<DT>::S* __restrict__ inlier,
                                                             typename FT<DT>::S* __restrict__ data,
                                                             int32_t* __restrict__ indices) {
   using S = typename FT<DT>::S;
-  const int lane = threadIdx.x & 63;
+  constexpr int U = 4;
+  constexpr uint32_t CAP = 1024, FLUSH = CAP - 64 * V;  // a group adds at most 64 * V
+  __shared__ uint32_t s_val[4][CAP];
+  __shared__ uint32_t s_col[4][CAP];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  uint32_t* bval = s_val[wv];
+  uint32_t* bcol = s_col[wv];
   const int64_t nw = (int64_t)gridDim.x * 4;
-  for (int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); g < nrows; g += nw) {
+  const int64_t nrows = nb * rows;
+  for (int64_t g = (int64_t)blockIdx.x * 4 + wv; g < nrows; g += nw) {
     const int64_t b = g / rows, r = g - b * rows;
     const int32_t* ptr = indptr + b * (rows + 1);
     int64_t pos = (int64_t)(uint32_t)((uint32_t)ptr[r] - (uint32_t)ptr[0]);
@@ -216,43 +247,64 @@ __global__ __launch_bounds__(256) void outlier_split_kernel(const typename FT<DT
     S* irow = inlier + g * cols;
     S* drow = data + b * max_nnz;
     int32_t* crow = indices + b * max_nnz;
-    for (int64_t c0 = 0; c0 < cols; c0 += 64 * V) {
-      const int64_t c = c0 + (int64_t)lane * V;
-      const bool ok = c < cols;
-      Group<S, V> grp;
-      grp.load(row + (ok ? c : cols - V));
-      uint32_t keep[V];
-      bool f[V];
-      uint32_t below = 0, n = 0;
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        const uint32_t e = grp.get(j);
-        const float v = FT<DT>::val(e);
-        // every |x| > t inlier is +0 (a negative t takes zeros too); only
-        // nonzero ones are stored
-        keep[j] = fabsf(v) > t ? 0u : e;
-        f[j] = ok && is_outlier(v, t);
-        const uint64_t m = __ballot(f[j]);
-        below += lanes_below(m);
-        n += (uint32_t)__popcll(m);
-      }
-      if (ok) store_group<S, V>(irow + c, keep);
-      if (n != 0 && pos < max_nnz) {
-        int64_t p = pos + below;
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-          if (f[j]) {
-            if (p < max_nnz) {
-              drow[p] = (S)grp.get(j);
-              crow[p] = (int32_t)(c + j);
-            }
-            ++p;
-          }
+    uint32_t nbuf = 0;
+    auto flush = [&]() {
+      wave_lds_sync();
+      for (uint32_t i = lane; i < nbuf; i += 64) {
+        const int64_t p = pos + i;
+        if (p < max_nnz) {
+          drow[p] = (S)bval[i];
+          crow[p] = (int32_t)bcol[i];
         }
       }
-      pos += n;
+      wave_lds_sync();
+      pos += nbuf;
+      nbuf = 0;
+    };
+    for (int64_t c0 = 0; c0 < cols; c0 += U * 64 * V) {
+      Group<S, V> grp[U];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = c0 + (int64_t)(u * 64 + lane) * V;
+        ok[u] = c < cols;
+        grp[u].load(row + (ok[u] ? c : cols - V));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t c = (uint32_t)(c0 + (u * 64 + lane) * V);
+        bool f[V];
+        uint32_t keep[V];
+        uint32_t below = 0, n = 0;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const uint32_t e = grp[u].get(j);
+          const float v = FT<DT>::val(e);
+          keep[j] = fabsf(v) > t ? 0u : e;
+          f[j] = ok[u] && is_outlier(v, t);
+          const uint64_t m = __ballot(f[j]);
+          below += lanes_below(m);
+          n += (uint32_t)__popcll(m);
+        }
+        if (ok[u]) store_group<S, V, true>(irow + c, keep);
+        if (n != 0) {
+          uint32_t q = nbuf + below;
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            if (f[j]) {
+              bval[q] = grp[u].get(j);
+              bcol[q] = c + j;
+              ++q;
+            }
+          }
+          nbuf += n;
+          if (nbuf >= FLUSH) flush();
+        }
+      }
     }
+    if (nbuf != 0) flush();
   }
+  pad_tail(indptr, rows, nb, max_nnz, data, indices);
 }
 
 // ---------------------------------------------------------------------------
@@ -286,7 +338,8 @@ __global__ __launch_bounds__(256) void csr_slice_rows_kernel(const S* __restrict
 }
 
 // Column slice [start, end): per-row count of the stored entries in range,
-// written where the row's end pointer goes (csr_scan_kernel follows).
+// written where the row's end pointer goes (csr_scan_kernel follows, then
+// csr_cols_scatter_kernel).
 __global__ __launch_bounds__(256) void csr_cols_count_kernel(const int32_t* __restrict__ indices,
                                                              const int32_t* __restrict__ indptr, int64_t rows,
                                                              int64_t nnz_in, int64_t start, int64_t end,
@@ -336,6 +389,7 @@ __global__ __launch_bounds__(256) void csr_cols_scatter_kernel(const S* __restri
       pos += __popcll(m);
     }
   }
+  pad_tail(indptr_out, rows, 1, max_nnz, data_out, indices_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -419,10 +473,13 @@ __global__ __launch_bounds__(256) void csr_decode_kernel(CsrDecode d) {
 
 // out[g][n] = round(sum over the row's entries p, in order, of a_p * B[k_p][n])
 // (+ addend[g][n], rounded again, when given).  One wave per (row, chunk of
-// 64*V columns); entries are read four at a time.
+// 64*V columns: 1 KiB of a B row), consecutive waves on consecutive chunks of
+// a row; entries are read four at a time.  Each entry reads its piece of a B
+// row from L2 / MALL: nnz * N * sizeof(B) bytes gathered in all.
 template <int DT, int V>
 __global__ __launch_bounds__(256) void spmm_csr_kernel(SpmmArgs a) {
   using S = typename FT<DT>::S;
+  constexpr int U = 4;
   const int lane = threadIdx.x & 63;
   const int64_t nch = (a.N + 64 * V - 1) / (64 * V);
   const int64_t items = a.nb * a.rows * nch;
@@ -430,63 +487,65 @@ __global__ __launch_bounds__(256) void spmm_csr_kernel(SpmmArgs a) {
   const int64_t nw = (int64_t)gridDim.x * 4;
   for (int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); w < items; w += nw) {
     const int64_t g = w / nch, ch = w - g * nch;
-    const int64_t b = g / a.rows, r = g - b * a.rows;
-    const int32_t* ptr = a.indptr + b * (a.rows + 1);
-    const int64_t base = ptr[0];
-    int64_t p0 = (int64_t)ptr[r] - base, p1 = (int64_t)ptr[r + 1] - base;
-    p0 = p0 < 0 ? 0 : (p0 > a.nnz_stride ? a.nnz_stride : p0);
-    p1 = p1 < p0 ? p0 : (p1 > a.nnz_stride ? a.nnz_stride : p1);
-    if (a.K == 0) p1 = p0;  // no row of B to read
     const int64_t n = ch * 64 * V + (int64_t)lane * V;
     const bool nok = n < a.N;
     const int64_t nn = nok ? n : a.N - V;
-    const S* Bb = B + b * a.b_stride + nn;
-    const int32_t* idx = a.indices + b * a.nnz_stride;
-    const int64_t dbase = b * a.nnz_stride;
-    float acc[V];
+    {
+      const int64_t b = g / a.rows, r = g - b * a.rows;
+      const int32_t* ptr = a.indptr + b * (a.rows + 1);
+      const int64_t base = ptr[0];
+      int64_t p0 = (int64_t)ptr[r] - base, p1 = (int64_t)ptr[r + 1] - base;
+      p0 = p0 < 0 ? 0 : (p0 > a.nnz_stride ? a.nnz_stride : p0);
+      p1 = p1 < p0 ? p0 : (p1 > a.nnz_stride ? a.nnz_stride : p1);
+      if (a.K == 0) p1 = p0;  // no row of B to read
+      const S* Bb = B + b * a.b_stride + nn;
+      const int32_t* idx = a.indices + b * a.nnz_stride;
+      const int64_t dbase = b * a.nnz_stride;
+      float acc[V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) acc[j] = 0.f;
-    int64_t p = p0;
-    for (; p + 4 <= p1; p += 4) {
-      Group<S, V> grp[4];
-      float av[4];
-      bool ok[4];
+      for (int j = 0; j < V; ++j) acc[j] = 0.f;
+      int64_t p = p0;
+      for (; p + U <= p1; p += U) {
+        Group<S, V> grp[U];
+        float av[U];
+        bool ok[U];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t k = idx[p + u];
-        ok[u] = (uint64_t)k < (uint64_t)a.K;
-        av[u] = load_f(a.data, a.data_dtype, dbase + p + u);
-        grp[u].load(Bb + (ok[u] ? k : 0) * a.N);
+        for (int q = 0; q < U; ++q) {
+          const int64_t k = idx[p + q];
+          ok[q] = (uint64_t)k < (uint64_t)a.K;
+          av[q] = load_f(a.data, a.data_dtype, dbase + p + q);
+          grp[q].load(Bb + (ok[q] ? k : 0) * a.N);
+        }
+#pragma unroll
+        for (int q = 0; q < U; ++q)
+#pragma unroll
+          for (int j = 0; j < V; ++j)
+            if (ok[q]) acc[j] = fmaf(av[q], FT<DT>::val(grp[q].get(j)), acc[j]);
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (; p < p1; ++p) {
+        const int64_t k = idx[p];
+        const bool ok = (uint64_t)k < (uint64_t)a.K;
+        const float av = load_f(a.data, a.data_dtype, dbase + p);
+        Group<S, V> grp;
+        grp.load(Bb + (ok ? k : 0) * a.N);
 #pragma unroll
         for (int j = 0; j < V; ++j)
-          if (ok[u]) acc[j] = fmaf(av[u], FT<DT>::val(grp[u].get(j)), acc[j]);
-    }
-    for (; p < p1; ++p) {
-      const int64_t k = idx[p];
-      const bool ok = (uint64_t)k < (uint64_t)a.K;
-      const float av = load_f(a.data, a.data_dtype, dbase + p);
-      Group<S, V> grp;
-      grp.load(Bb + (ok ? k : 0) * a.N);
-#pragma unroll
-      for (int j = 0; j < V; ++j)
-        if (ok) acc[j] = fmaf(av, FT<DT>::val(grp.get(j)), acc[j]);
-    }
-    if (nok) {
-      uint32_t o[V];
-      if (a.addend) {
-        Group<S, V> ad;
-        ad.load((const S*)a.addend + g * a.N + n);
-#pragma unroll
-        for (int j = 0; j < V; ++j)
-          o[j] = FT<DT>::bits(FT<DT>::val(ad.get(j)) + FT<DT>::val(FT<DT>::bits(acc[j])));
-      } else {
-#pragma unroll
-        for (int j = 0; j < V; ++j) o[j] = FT<DT>::bits(acc[j]);
+          if (ok) acc[j] = fmaf(av, FT<DT>::val(grp.get(j)), acc[j]);
       }
-      store_group<S, V>((S*)a.out + g * a.N + n, o);
+      if (nok) {
+        uint32_t o[V];
+        if (a.addend) {
+          Group<S, V> ad;
+          ad.load((const S*)a.addend + g * a.N + n);
+#pragma unroll
+          for (int j = 0; j < V; ++j)
+            o[j] = FT<DT>::bits(FT<DT>::val(ad.get(j)) + FT<DT>::val(FT<DT>::bits(acc[j])));
+        } else {
+#pragma unroll
+          for (int j = 0; j < V; ++j) o[j] = FT<DT>::bits(acc[j]);
+        }
+        store_group<S, V>((S*)a.out + g * a.N + n, o);
+      }
     }
   }
 }
@@ -509,17 +568,15 @@ int launch_filter(const void* x, int64_t nb, int64_t rows, int64_t cols, float t
                          (const S*)x, nrows, rows, cols, t, indptr);
     }
   }
-  if (nb > 0)
-    hipLaunchKernelGGL(csr_scan_kernel<S>, dim3((unsigned)nb), dim3(1024), 0, st, indptr, rows, max_nnz, offset,
-                       (S*)data, indices);
-  if (nrows > 0 && cols > 0) {
-    if (wide) {
-      hipLaunchKernelGGL((outlier_split_kernel<DT, V>), dim3(grid_for(nrows, 4, 16)), dim3(256), 0, st,
-                         (const S*)x, nrows, rows, cols, t, indptr, max_nnz, (S*)inlier, (S*)data, indices);
-    } else {
-      hipLaunchKernelGGL((outlier_split_kernel<DT, 1>), dim3(grid_for(nrows, 4, 16)), dim3(256), 0, st,
-                         (const S*)x, nrows, rows, cols, t, indptr, max_nnz, (S*)inlier, (S*)data, indices);
-    }
+  hipLaunchKernelGGL(csr_scan_kernel, dim3((unsigned)nb), dim3(1024), 0, st, indptr, rows, max_nnz, offset);
+  // the split kernel also pads every batch's tail, so it runs when rows == 0
+  const unsigned grid = grid_for(nrows > 0 ? nrows : 1, 4, 16);
+  if (wide) {
+    hipLaunchKernelGGL((outlier_split_kernel<DT, V>), dim3(grid), dim3(256), 0, st, (const S*)x, nb, rows, cols, t,
+                       indptr, max_nnz, (S*)inlier, (S*)data, indices);
+  } else {
+    hipLaunchKernelGGL((outlier_split_kernel<DT, 1>), dim3(grid), dim3(256), 0, st, (const S*)x, nb, rows, cols, t,
+                       indptr, max_nnz, (S*)inlier, (S*)data, indices);
   }
   return check_launch("filter_outlier");
 }
@@ -529,13 +586,12 @@ int launch_spmm(const SpmmArgs& a, hipStream_t st) {
   constexpr int V = FT<DT>::kVec;
   const bool wide = a.N % V == 0 && aligned(a.B, 16) && aligned(a.out, 16) && (a.b_stride % V == 0) &&
                     (!a.addend || aligned(a.addend, 16));
-  if (wide) {
-    const int64_t items = a.nb * a.rows * ((a.N + 64 * V - 1) / (64 * V));
+  const int v = wide ? V : 1;
+  const int64_t items = a.nb * a.rows * ((a.N + 64 * v - 1) / (64 * v));
+  if (wide)
     hipLaunchKernelGGL((spmm_csr_kernel<DT, V>), dim3(grid_for(items, 4, 16)), dim3(256), 0, st, a);
-  } else {
-    const int64_t items = a.nb * a.rows * ((a.N + 63) / 64);
+  else
     hipLaunchKernelGGL((spmm_csr_kernel<DT, 1>), dim3(grid_for(items, 4, 16)), dim3(256), 0, st, a);
-  }
   return check_launch("spmm_csr");
 }
 
@@ -589,21 +645,17 @@ int csr_slice(const void* data, int dtype, const int32_t* indices, const int32_t
   if (rows > 0)
     hipLaunchKernelGGL(csr_cols_count_kernel, dim3(grid_for(rows, 4, 16)), dim3(256), 0, st, indices, indptr, rows,
                        nnz_in, start, end, indptr_out);
-  if (wide16) {
-    hipLaunchKernelGGL(csr_scan_kernel<uint16_t>, dim3(1), dim3(1024), 0, st, indptr_out, rows, max_nnz, 0,
-                       (uint16_t*)data_out, indices_out);
-    if (rows > 0)
-      hipLaunchKernelGGL(csr_cols_scatter_kernel<uint16_t>, dim3(grid_for(rows, 4, 16)), dim3(256), 0, st,
-                         (const uint16_t*)data, indices, indptr, rows, nnz_in, start, end, max_nnz, indptr_out,
-                         (uint16_t*)data_out, indices_out);
-  } else {
-    hipLaunchKernelGGL(csr_scan_kernel<uint32_t>, dim3(1), dim3(1024), 0, st, indptr_out, rows, max_nnz, 0,
-                       (uint32_t*)data_out, indices_out);
-    if (rows > 0)
-      hipLaunchKernelGGL(csr_cols_scatter_kernel<uint32_t>, dim3(grid_for(rows, 4, 16)), dim3(256), 0, st,
-                         (const uint32_t*)data, indices, indptr, rows, nnz_in, start, end, max_nnz, indptr_out,
-                         (uint32_t*)data_out, indices_out);
-  }
+  hipLaunchKernelGGL(csr_scan_kernel, dim3(1), dim3(1024), 0, st, indptr_out, rows, max_nnz, 0);
+  // the scatter kernel also pads the tail, so it runs when rows == 0
+  const unsigned grid = grid_for(rows > 0 ? rows : 1, 4, 16);
+  if (wide16)
+    hipLaunchKernelGGL(csr_cols_scatter_kernel<uint16_t>, dim3(grid), dim3(256), 0, st, (const uint16_t*)data,
+                       indices, indptr, rows, nnz_in, start, end, max_nnz, indptr_out, (uint16_t*)data_out,
+                       indices_out);
+  else
+    hipLaunchKernelGGL(csr_cols_scatter_kernel<uint32_t>, dim3(grid), dim3(256), 0, st, (const uint32_t*)data,
+                       indices, indptr, rows, nnz_in, start, end, max_nnz, indptr_out, (uint32_t*)data_out,
+                       indices_out);
   return check_launch("slice_csr_tensor");
 }
 
