@@ -556,7 +556,7 @@ def main():
         if "gathered_bytes" in info:
             results[k]["gathered_bytes"] = info["gathered_bytes"]
             results[k]["gathered_GBps"] = info["gathered_bytes"] / (ms * 1e-3) / 1e9
-            results[k]["achieved_TFLOPs"] = info["flops"] / (ms * 1e-3) / 1e12
+            results[k]["spmm_TFLOPs"] = info["flops"] / (ms * 1e-3) / 1e12
         if k.startswith("o") and not a.no_cpu:
             results[k]["cpu_oracle"] = cpu_oracle_time(torch, k, info, ms)
         if k == HEADLINE:
