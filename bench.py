@@ -199,6 +199,26 @@ def setup_c5(vqx, torch, L):
         bound="mfma", dtype="bf16")
 
 
+def setup_c5_skinny(vqx, torch, L, M):
+    """C5's weight with a decode-time batch of M rows (the skinny kernel,
+    bound by the 4-bit weight's bytes)."""
+    g = torch.Generator().manual_seed(4)
+    N, K = 11008, 4096
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).cuda()
+    Q = torch.ops.quantized_ops
+    sc, codes = Q.quantize_mx_packed(W, "nf4", -1, 64, False, 1.0, "float32")
+    del W
+    lv = vqx.parse_format("nf4").tables(A.device)["levels_bf16"]
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    fn = L.load().vqx_nf4_linear
+    args = (L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), M, N, K, L.stream_of(A))
+    return (lambda: fn(*args)), dict(
+        name=f"C5 skinny NF4-dequant linear: A bf16 [{M},4096] x W NF4 block-64 [11008,4096]^T -> bf16",
+        elements=M * N, bytes=N * K // 2 + N * K // 64 * 4 + M * K * 2 + M * N * 2, flops=2 * M * N * K,
+        bound="hbm", dtype="bf16", keep=(A, codes, sc, lv, out))
+
+
 def outlier_input(torch, rows=4096, cols=11008, seed=5):
     """Activation-like bf16 [tokens, features]: N(0,1) with 0.5% of the
     entries scaled by 32, the outliers the CSR path splits off (|x| > 6)."""
@@ -294,6 +314,8 @@ CONFIGS = {
     "c4_k256": lambda v, t, L: setup_c4(v, t, L, 256),
     "c4_k16_decode": lambda v, t, L: setup_c4(v, t, L, 16, decode=True),
     "c5": lambda v, t, L: setup_c5(v, t, L),
+    "c5_m1": lambda v, t, L: setup_c5_skinny(v, t, L, 1),
+    "c5_m16": lambda v, t, L: setup_c5_skinny(v, t, L, 16),
     "o1_filter": lambda v, t, L: setup_o1(v, t, L),
     "o2_quantize_mx_outlier": lambda v, t, L: setup_o1(v, t, L, mx=True),
     "o3_spmm": lambda v, t, L: setup_o3(v, t, L),
@@ -428,6 +450,8 @@ DOMINANT = {
     "c4_k256": "cb_encode_kernel<float, 8>",
     "c4_k16_decode": "cb_decode_kernel<float>",
     "c5": "nf4_gemm_kernel",
+    "c5_m1": "nf4_skinny_kernel",
+    "c5_m16": "nf4_skinny_kernel",
     "o1_filter": "outlier_split_kernel<1, 8>",
     "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8>",
     "o3_spmm": "spmm_csr_kernel<1, 8>",

@@ -236,8 +236,10 @@ int vqx_codebook_decode(const uint8_t* codes, int64_t rows, int64_t cols, const 
  *   out[M, N] = A[M, K] . W[N, K]^T + bias,  W[n, k] = bf16(levels[c] * scale[n, k/64])
  * A: bf16 row-major [M, K]; codes: packed 4-bit [N, K/2] (low nibble = even k);
  * scale: fp32 [N, K/64]; levels: 16 bf16 patterns; bias: bf16 [N] or NULL;
- * out: bf16 [M, N].  bf16 MFMA with fp32 accumulation.  Needs M % 256 == 0,
- * N % 128 == 0, K % 64 == 0 (VQX_ERR_UNSUPPORTED otherwise).
+ * out: bf16 [M, N], fp32 accumulation.  Any M >= 1: M <= 16 runs a skinny
+ * kernel bound by the weight's bytes (any N); larger M the bf16 MFMA tile
+ * kernel (256 x 128 tiles, a partial last row tile; needs N % 128 == 0).
+ * K % 64 == 0 always (VQX_ERR_UNSUPPORTED otherwise).
  */
 int vqx_nf4_linear(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
                    const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K,

@@ -62,10 +62,55 @@ def test_nf4_linear_bias_and_batch(vqx):
     assert rel < 1e-2
 
 
+def check_against_reference(A, W, bias=None):
+    M, K = A.shape
+    N = W.shape[0]
+    sc, codes = Q.quantize_mx_packed(W.cuda(), "nf4", -1, 64, False, 1.0, "float32")
+    out = Q.linear_nf4(A.cuda(), codes, sc, None if bias is None else bias.cuda(), 64, "nf4")
+    assert out.shape == (M, N) and out.dtype == torch.bfloat16
+    Wd = decode_reference(codes, sc, N, K).cuda()
+    ref = A.cuda().float() @ Wd.float().t()
+    if bias is not None:
+        ref = ref + bias.cuda().float()
+    ref = ref.to(torch.bfloat16).float()
+    err = (out.float() - ref).abs()
+    tol = 1e-2 * ref.abs() + 1e-2 * ref.abs().mean()
+    frac_bad = (err > tol).float().mean().item()
+    rel = (err.norm() / ref.norm()).item()
+    assert rel < 1e-2 and frac_bad < 1e-3, (rel, frac_bad)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(1, 11008, 4096), (1, 64, 64), (2, 4096, 11008), (3, 200, 512), (4, 130, 256),
+                                   (8, 1000, 1024), (16, 4096, 4096), (16, 64, 192)])
+def test_nf4_linear_skinny_matches_reference(vqx, M, N, K):
+    # M <= 16: the skinny kernel (any N; K % 64)
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    check_against_reference(torch.randn(M, K, generator=g).to(torch.bfloat16), make_weight(N, K, seed=M))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(17, 128, 64), (100, 256, 512), (300, 384, 256), (2047, 512, 1024)])
+def test_nf4_linear_partial_row_tile(vqx, M, N, K):
+    # M > 16 and not a multiple of 256: the MFMA kernel with a partial last row tile
+    g = torch.Generator().manual_seed(M + N + K)
+    check_against_reference(torch.randn(M, K, generator=g).to(torch.bfloat16), make_weight(N, K, seed=M))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 5, 33])
+def test_nf4_linear_skinny_and_tail_bias(vqx, M):
+    g = torch.Generator().manual_seed(M)
+    A = torch.randn(M, 256, generator=g).to(torch.bfloat16)
+    bias = torch.randn(256, generator=g).to(torch.bfloat16)
+    check_against_reference(A, make_weight(256, 256, seed=9), bias)
+
+
 @pytest.mark.gpu
 def test_nf4_linear_rejects_unsupported_shape(vqx):
+    # K must be a multiple of the 64-element scale block; N % 128 for M > 16
     A = torch.randn(100, 64).to(torch.bfloat16).cuda()
-    W = make_weight(128, 64)
+    W = make_weight(200, 64)
     sc, codes = Q.quantize_mx_packed(W.cuda(), "nf4", -1, 64, False, 1.0, "float32")
     with pytest.raises(RuntimeError, match="nf4_gemm"):
         Q.linear_nf4(A, codes, sc, None, 64, "nf4")

@@ -23,7 +23,9 @@
 //  * The MFMA takes the W fragment as its first operand, so each lane ends
 //    with four consecutive output columns per group: 8-byte stores.
 // Workgroups are ordered so each XCD runs whole 256-row slabs of A, which stay
-// in its L2 while W streams past.
+// in its L2 while W streams past.  A partial last row tile runs as a launch
+// of its own that loads row M - 1 in place of the missing rows and stores
+// only rows < M.  M <= 16 takes the skinny kernel further down instead.
 #include <type_traits>
 
 #include "vqx_kernels.h"
@@ -103,12 +105,17 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// PARTIAL: the launch covers one row tile starting at row m_base with fewer
+// than 256 rows left; the full tiles run in a launch of their own without
+// the row clamping.
+template <bool PARTIAL>
 __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __restrict__ A,
                                                              const uint8_t* __restrict__ codes,
                                                              const float* __restrict__ scale,
                                                              const uint16_t* __restrict__ levels,
                                                              const uint16_t* __restrict__ bias,
-                                                             uint16_t* __restrict__ out, int M, int N, int K) {
+                                                             uint16_t* __restrict__ out, int M, int N, int K,
+                                                             int m_base) {
   __shared__ __attribute__((aligned(16))) uint8_t wl[3 * kWTile];
   __shared__ __attribute__((aligned(16))) uint8_t al[3 * kATile];
   const int tid = threadIdx.x;
@@ -122,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
   // XCD-aware tile order: consecutive workgroup ids go round-robin over the 8
   // XCDs; give each XCD a contiguous range of tiles, M-major, so an XCD works
   // through whole A slabs.
-  const int ntn = N / kBN, ntm = M / kBM;
+  const int ntn = N / kBN, ntm = PARTIAL ? 1 : (M - m_base) / kBM;
   const int ntiles = ntn * ntm;
   int bid = blockIdx.x;
   int per_xcd = (ntiles + 7) / 8;
@@ -130,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
   if (ntiles % 8 != 0) tile = bid;  // uneven split: plain order
   if (tile >= ntiles) return;
   const int tm = tile / ntn, tn = tile % ntn;
-  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int m0 = m_base + tm * kBM, n0 = tn * kBN;
 
   // level byte tables (uniform)
   LevelBytes lb;
@@ -150,13 +157,24 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
   const int kb = K / 64;  // scale blocks per row
 
   // A staging: load q (0..3) of a step covers rows 32 wave + 8 q .. +7, lane
-  // L chunk L % 8 of row 32 wave + 8 q + L / 8
+  // L chunk L % 8 of row 32 wave + 8 q + L / 8.  In a partial tile, rows
+  // past M load row M - 1 instead; their outputs are not stored.
   const uint16_t* asrc = A + (size_t)(m0 + wave * 32 + (lane >> 3)) * K + (lane & 7) * 8;
+  int aoff[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = m0 + wave * 32 + 8 * q + (lane >> 3);
+    aoff[q] = PARTIAL ? ((r < M ? r : M - 1) - (m0 + wave * 32 + (lane >> 3))) * K : 8 * q * K;
+  }
   u32x4 areg[4];
   auto load_a = [&](int ks) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      areg[q] = *reinterpret_cast<const u32x4*>(asrc + (size_t)(8 * q) * K + (size_t)ks * kBK);
+    for (int q = 0; q < 4; ++q) {
+      if constexpr (PARTIAL)
+        areg[q] = *reinterpret_cast<const u32x4*>(asrc + aoff[q] + (size_t)ks * kBK);
+      else
+        areg[q] = *reinterpret_cast<const u32x4*>(asrc + (size_t)(8 * q) * K + (size_t)ks * kBK);
+    }
   };
   auto store_a = [&](uint32_t stage) {
 #pragma unroll
@@ -334,8 +352,100 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
         const int m = m0 + wm * 64 + i * 32 + lr;
         u32x2 o = {pack_bf16x2(acc[i][j][4 * g] + b0, acc[i][j][4 * g + 1] + b1),
                    pack_bf16x2(acc[i][j][4 * g + 2] + b2, acc[i][j][4 * g + 3] + b3)};
-        *reinterpret_cast<u32x2*>(out + (size_t)m * N + n) = o;
+        if (!PARTIAL || m < M) *reinterpret_cast<u32x2*>(out + (size_t)m * N + n) = o;
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny form for M <= 16 (decode-time batches).  Each wave computes a
+// 16 x 16 output tile (all of A's rows, padded to 16; 16 output columns)
+// over a quarter of K with v_mfma_f32_16x16x32_bf16; the workgroup's 4 waves
+// take the 4 quarters of K for the same columns and add their tiles in LDS in
+// wave (k) order.  Per 128-k step lane l loads 32 codes (16 bytes) of its
+// column's W row and the 32 matching A values (64 bytes) of its A row, for
+// row / column l % 16 and k = 128 s + 32 (l / 16) .. +31; MFMA c (0..3) of
+// the step takes the lane's k 32 (l / 16) + 8 c .. + 7 from both operands (one
+// permutation of k for both, so every product pairs the same k).  W is
+// decoded exactly as in the tile kernel (bf16(level * scale)).  The MFMAs
+// are idle most of the time: the decode's VALU and the weight's bytes bound
+// the kernel.
+// ---------------------------------------------------------------------------
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+constexpr int kSkinnyWaves = 4;
+
+__global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uint16_t* __restrict__ A,
+                                                                        const uint8_t* __restrict__ codes,
+                                                                        const float* __restrict__ scale,
+                                                                        const uint16_t* __restrict__ levels,
+                                                                        const uint16_t* __restrict__ bias,
+                                                                        uint16_t* __restrict__ out, int M, int N,
+                                                                        int K) {
+  __shared__ float part[kSkinnyWaves][16][16];  // [wave][row m][column]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int nn = n0 + r < N ? n0 + r : N - 1;
+  const int mm = r < M ? r : M - 1;
+  const int kb = K / 64;
+  const int steps = (K + 127) / 128;
+  const int s0 = steps * wave / kSkinnyWaves, s1 = steps * (wave + 1) / kSkinnyWaves;
+  LevelBytes lb;
+  {
+    uint32_t hb[4] = {0, 0, 0, 0}, lbv[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      uint32_t v = levels[c];
+      hb[c >> 2] |= ((v >> 8) & 0xFFu) << (8 * (c & 3));
+      lbv[c >> 2] |= (v & 0xFFu) << (8 * (c & 3));
+    }
+    lb.h0 = hb[0]; lb.h1 = hb[1]; lb.h2 = hb[2]; lb.h3 = hb[3];
+    lb.l0 = lbv[0]; lb.l1 = lbv[1]; lb.l2 = lbv[2]; lb.l3 = lbv[3];
+  }
+  const uint8_t* wrow = codes + (size_t)nn * (K / 2);
+  const float* srow = scale + (size_t)nn * kb;
+  const uint16_t* arow = A + (size_t)mm * K;
+  f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int st = s0; st < s1; ++st) {
+    // K % 64 == 0, so a 32-k group is either wholly inside K or wholly past
+    // it (the last step of an odd number of 64-blocks); past it: A = 0 and
+    // the loads are clamped to the last group
+    const int k = st * 128 + g * 32;
+    const bool kok = k < K;
+    const int kk = kok ? k : K - 32;
+    const u32x4 w = *reinterpret_cast<const u32x4*>(wrow + kk / 2);
+    const float sc = srow[kk / 64];
+    u32x4 a[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      a[c] = *reinterpret_cast<const u32x4*>(arow + kk + 8 * c);
+      if (!kok) a[c] = u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint32_t o[4];
+      decode8(w[c], sc, lb, o);
+      const u32x4 b = {o[0], o[1], o[2], o[3]};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[c]), __builtin_bit_cast(bf16x8, b),
+                                                    acc, 0, 0, 0);
+    }
+  }
+  // lane holds rows 4 (l / 16) .. + 3 of column l % 16
+#pragma unroll
+  for (int j = 0; j < 4; ++j) part[wave][4 * g + j][r] = acc[j];
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    const int t = threadIdx.x, m = t >> 4, c = t & 15;
+    float v = part[0][m][c];
+#pragma unroll
+    for (int w = 1; w < kSkinnyWaves; ++w) v += part[w][m][c];
+    const int n = n0 + c;
+    if (m < M && n < N) {
+      const float b = bias ? u2f((uint32_t)bias[n] << 16) : 0.0f;
+      out[(size_t)m * N + n] = (uint16_t)f2bf(v + b);
     }
   }
 }
@@ -343,15 +453,24 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
 int nf4_gemm(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
              const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
   if (M <= 0 || N <= 0 || K <= 0) return set_error(kErrInvalid, "nf4_gemm: empty shape");
-  if (M % kBM || N % kBN || K % kBK)
-    return set_error(kErrUnsupported, "nf4_gemm: needs M %% 256 == 0, N %% 128 == 0, K %% 64 == 0 "
-                     "(got %lld x %lld x %lld)", (long long)M, (long long)N, (long long)K);
   if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) return set_error(kErrInvalid, "nf4_gemm: shape too large");
+  if (K % kBK) return set_error(kErrUnsupported, "nf4_gemm: needs K %% 64 == 0 (got K = %lld)", (long long)K);
   if (!aligned(A, 16) || !aligned(codes, 16) || !aligned(out, 8) || (bias && !aligned(bias, 8)))
     return set_error(kErrInvalid, "nf4_gemm: A and codes must be 16-byte aligned, out and bias 8-byte aligned");
-  int ntiles = (int)((M / kBM) * (N / kBN));
-  hipLaunchKernelGGL(nf4_gemm_kernel, dim3(ntiles), dim3(kThreads), 0, st, A, codes, scale, levels, bias, out,
-                     (int)M, (int)N, (int)K);
+  if (M <= 16) {
+    hipLaunchKernelGGL(nf4_skinny_kernel, dim3((unsigned)((N + 15) / 16)), dim3(64 * kSkinnyWaves), 0, st, A, codes, scale,
+                       levels, bias, out, (int)M, (int)N, (int)K);
+    return check_launch("nf4_skinny");
+  }
+  if (N % kBN)
+    return set_error(kErrUnsupported, "nf4_gemm: needs N %% 128 == 0 for M > 16 (got N = %lld)", (long long)N);
+  const int64_t mfull = M / kBM * kBM;
+  if (mfull > 0)
+    hipLaunchKernelGGL(nf4_gemm_kernel<false>, dim3((unsigned)(mfull / kBM * (N / kBN))), dim3(kThreads), 0, st, A,
+                       codes, scale, levels, bias, out, (int)M, (int)N, (int)K, 0);
+  if (mfull < M)
+    hipLaunchKernelGGL(nf4_gemm_kernel<true>, dim3((unsigned)(N / kBN)), dim3(kThreads), 0, st, A, codes, scale,
+                       levels, bias, out, (int)M, (int)N, (int)K, (int)mfull);
   return check_launch("nf4_gemm");
 }
 
