@@ -219,6 +219,25 @@ def setup_c5_skinny(vqx, torch, L, M):
         bound="hbm", dtype="bf16", keep=(A, codes, sc, lv, out))
 
 
+def setup_l1(vqx, torch, L):
+    """Learned-codebook calibration statistics of a 4096x4096 fp32 weight:
+    unit_scale in blocks of 64 (quant_max 7) fused with the 4001-bin fp64
+    histogram of Histogram.add, unit weights."""
+    g = torch.Generator().manual_seed(9)
+    xc = torch.randn(4096, 4096, generator=g)
+    x = xc.cuda()
+    h = vqx.quantization.Histogram(-7.0, 7.0, 4001)
+    edges = h._prepare(x.device)
+    fn = L.load().vqx_lcq_histogram
+    args = (L.ptr(x), L.F32, x.numel(), 64, L.ctypes.c_float(7.0), None, 1, L.ptr(edges), 4001, L.ptr(h.weight),
+            L.ptr(h.total), L.ptr(h.square), L.stream_of(x))
+    return (lambda: fn(*args)), dict(
+        name="L1 LCQ calibration histogram: unit_scale (blocks of 64, quant_max 7) + 4001-bin fp64 moments of a "
+             "fp32 4096x4096 N(0,1) seed 9",
+        elements=x.numel(), bytes=x.numel() * 4 + 3 * 4001 * 8, bound="hbm", dtype="f32->f64",
+        cpu_input=xc, keep=(h, edges))
+
+
 def outlier_input(torch, rows=4096, cols=11008, seed=5):
     """Activation-like bf16 [tokens, features]: N(0,1) with 0.5% of the
     entries scaled by 32, the outliers the CSR path splits off (|x| > 6)."""
@@ -319,6 +338,7 @@ CONFIGS = {
     "o1_filter": lambda v, t, L: setup_o1(v, t, L),
     "o2_quantize_mx_outlier": lambda v, t, L: setup_o1(v, t, L, mx=True),
     "o3_spmm": lambda v, t, L: setup_o3(v, t, L),
+    "l1_histogram": lambda v, t, L: setup_l1(v, t, L),
 }
 HEADLINE = "c2"
 
@@ -399,13 +419,19 @@ def cpu_baseline_c2(torch, x):
 
 
 def cpu_oracle_time(torch, k, info, kernel_ms):
-    """One run of the CPU oracle (the reference's torch-CPU op sequence) on a
-    outlier config's full input, timed beside the GPU figure."""
+    """One run of the CPU oracle (the reference's torch-CPU op sequence) on an
+    outlier or calibration config's full input, timed beside the GPU figure."""
     from oracle import formats as F
     from oracle import reference_ops as R
 
     torch.set_num_threads(os.cpu_count() or 1)
-    if k == "o3_spmm":
+    if k == "l1_histogram":
+        x = info["cpu_input"]
+
+        def fn():
+            u = R.unit_scale(x, 64, 7.0).reshape(-1)
+            return R.lcq_histogram_add(u, torch.ones(()), -7.0, 7.0, 4001)
+    elif k == "o3_spmm":
         d, i, p, B = info["cpu_input"]
 
         def fn():
@@ -455,6 +481,7 @@ DOMINANT = {
     "o1_filter": "outlier_split_kernel<1, 8>",
     "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8>",
     "o3_spmm": "spmm_csr_kernel<1, 8>",
+    "l1_histogram": "lcq_hist_kernel<0, true, false>",
 }
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
 
@@ -581,7 +608,7 @@ def main():
             results[k]["gathered_bytes"] = info["gathered_bytes"]
             results[k]["gathered_GBps"] = info["gathered_bytes"] / (ms * 1e-3) / 1e9
             results[k]["spmm_TFLOPs"] = info["flops"] / (ms * 1e-3) / 1e12
-        if k.startswith("o") and not a.no_cpu:
+        if (k.startswith("o") or k.startswith("l")) and not a.no_cpu:
             results[k]["cpu_oracle"] = cpu_oracle_time(torch, k, info, ms)
         if k == HEADLINE:
             info_head = info

@@ -309,6 +309,23 @@ int vqx_spmm_csr(const void* data, int32_t data_dtype, const int32_t* indices, c
                  int64_t batches, int64_t rows, int64_t nnz_stride, const void* B, int32_t B_dtype,
                  int64_t B_batch_stride, int64_t K, int64_t N, const void* addend, void* out, vqx_stream_t stream);
 
+/*
+ * LCQ calibration statistics: Histogram.add (src/vc/quantization/lcq.py:44-119),
+ * optionally fused with unit_scale (:136-150) as _accumulate (:603-626) applies it.
+ * block_size = 0: v[i] = x[i];  block_size > 0 (n % block_size == 0):
+ * v[i] = x[i] / (max(amax |block|, 1e-12) / quant_max), fp32, IEEE division.
+ * bin = (number of edges <= v) - 1 clamped to [0, bins - 1] (torch.bucketize
+ * right=True; NaN counts every edge); with w = weights[i % weights_period]
+ * (weights NULL: w = 1):  weight[bin] += w, total[bin] += w v,
+ * square[bin] += (w v) v, in fp64, added to what the arrays hold (zero them
+ * before the first call).  x: n elements, F32, BF16 or F16; edges: bins + 1
+ * ascending fp32 values; bins <= 4096; weight / total / square: bins doubles.
+ * The fp64 sums are added in an unspecified order (as index_add_ on a GPU).
+ */
+int vqx_lcq_histogram(const void* x, int32_t x_dtype, int64_t n, int64_t block_size, float quant_max,
+                      const float* weights, int64_t weights_period, const float* edges, int32_t bins,
+                      double* weight, double* total, double* square, vqx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,8 @@ __all__ = [
     "slice_csr_tensor",
     "spmm_csr",
     "csr_to_dense",
+    "unit_scale",
+    "lcq_histogram_add",
 ]
 
 
@@ -328,3 +330,30 @@ def spmm_csr(data, indices, indptr, B, B_scale=None, B_code=None, block_size=Non
                                       size=(ip[i].numel() - 1, Bi.shape[0]))
         outs.append(torch.sparse.mm(csr, Bi.to(torch.float32)).to(B.dtype))
     return torch.stack(outs).reshape(*batch, -1, B.shape[-1])
+
+
+# ---------------------------------------------------------------------------
+# learned-codebook calibration statistics (src/vc/quantization/lcq.py)
+# ---------------------------------------------------------------------------
+def unit_scale(x, block_size, quant_max):
+    """src/vc/quantization/lcq.py:136-150: x / (max(block amax, 1e-12) / quant_max), fp32."""
+    x = x.float()
+    flat = x.reshape(-1, block_size)
+    scale = flat.abs().amax(-1, keepdim=True).clamp_min(1e-12) / quant_max
+    return (flat / scale).reshape(x.shape)
+
+
+def lcq_histogram_add(values, weights, quant_min, quant_max, bins=4001, sums=None):
+    """src/vc/quantization/lcq.py:77-109 on the CPU: bin by bucketize(right=True)
+    over fp32 linspace edges, then fp64 sums of w, w v, (w v) v per bin.
+    Returns (weight, total, square), added to ``sums`` when given."""
+    if sums is None:
+        sums = tuple(torch.zeros(bins, dtype=torch.float64) for _ in range(3))
+    edges = torch.linspace(quant_min - 0.5, quant_max + 0.5, bins + 1, dtype=torch.float32)
+    index = (torch.bucketize(values, edges, right=True) - 1).clamp_(0, bins - 1)
+    v = values.double()
+    w = weights.double().expand_as(v)
+    sums[0].index_add_(0, index, w)
+    sums[1].index_add_(0, index, w * v)
+    sums[2].index_add_(0, index, w * v * v)
+    return sums

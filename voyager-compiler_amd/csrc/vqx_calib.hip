@@ -1,0 +1,318 @@
+// LCQ calibration statistics: the weighted per-bin moments that the learned
+// codebook solver reads (src/voyager_compiler/quantization/lcq.py:44-119
+// Histogram.add, with unit_scale :136-150 as _accumulate :603-626 applies it).
+//
+// Per element v -- x itself, or x / blockscale with blockscale =
+// max(amax |block|, 1e-12) / quant_max in fp32 and IEEE division -- the bin
+// is the number of edges <= v, minus one, clamped to [0, bins - 1]
+// (torch.bucketize(right=True); NaN counts every edge), and
+//   weight[bin] += w,  total[bin] += w v,  square[bin] += (w v) v
+// in fp64 (w v is exact in fp64; the second product rounds as torch's does).
+// Only the order of the fp64 additions differs from the reference's
+// index_add_.
+//
+// Each workgroup keeps the three histograms in LDS (fp64 LDS atomics) with
+// the fp32 edges beside them, works through a grid-stride share of the
+// elements (four per lane per load, a block's amax a butterfly over its
+// lanes; odd block sizes one thread per block), then adds its histograms to
+// the global sums with fp64 atomics.  The bin of v starts from
+// the arithmetic guess of a uniform grid and is corrected against the actual
+// edges, so it is exact whatever rounding the edges carry.
+#include <type_traits>
+
+#include "vqx_common.h"
+#include "vqx_kernels.h"
+
+namespace vqx {
+namespace {
+
+constexpr int kHistThreads = 1024;
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* x, int64_t i) {
+  if constexpr (DT == kF32) return ((const float*)x)[i];
+  else if constexpr (DT == kBF16) return bf2f(((const uint16_t*)x)[i]);
+  else return h2f_exact(((const uint16_t*)x)[i]);
+}
+
+struct HistLds {
+  double* w;
+  double* t;
+  double* s;
+  const float* e;  // bins + 1 edges
+};
+
+// The bin guess on the uniform grid [e0, e0 + bins * step]: the number of
+// edges <= v if the edges were exactly uniform.  Monotone in v.
+__device__ __forceinline__ int grid_guess(float v, float e0, float inv_step, int bins) {
+  // fmaxf / fminf also send a NaN guess (degenerate edges) into [1, bins]
+  return (int)fminf(fmaxf(__builtin_floorf((v - e0) * inv_step) + 1.0f, 1.0f), (float)bins);
+}
+
+// Number of edges <= v (0 .. bins + 1).  With `tight` (every edge checked
+// at set-up: grid_guess(e[j]) >= j and grid_guess(just below e[j]) <= j + 1)
+// the guess is within one of the answer for every v between e[0] and
+// e[bins] (the guess is monotone), so one look at the two edges around it
+// settles the count; otherwise the guess is walked to the answer.
+__device__ __forceinline__ int edges_at_or_below(float v, const float* e, int bins, float e0, float elast,
+                                                 float inv_step, bool tight) {
+  if (!(v == v)) return bins + 1;  // NaN: bucketize places it past every edge
+  if (v >= elast) return bins + 1;
+  if (v < e0) return 0;
+  // e[0] <= v < e[bins]: the answer lies in [1, bins]
+  int g = grid_guess(v, e0, inv_step, bins);
+  if (tight) {
+    const float lo = e[g - 1], hi = e[g < bins ? g : bins];
+    return g - (lo > v ? 1 : 0) + (g < bins && hi <= v ? 1 : 0);
+  }
+  while (g > 1 && !(e[g - 1] <= v)) --g;
+  while (g < bins && e[g] <= v) ++g;
+  return g;
+}
+
+__device__ __forceinline__ void hist_add(const HistLds& h, int bins, float e0, float elast, float inv_step, bool tight,
+                                         float v, float w) {
+  int c = edges_at_or_below(v, h.e, bins, e0, elast, inv_step, tight) - 1;
+  c = c < 0 ? 0 : (c > bins - 1 ? bins - 1 : c);
+  const double vd = (double)v, wd = (double)w;
+  const double wv = wd * vd;
+  atomicAdd(&h.w[c], wd);
+  atomicAdd(&h.t[c], wv);
+  atomicAdd(&h.s[c], wv * vd);
+}
+
+// The bin of v when the guess is tight, without branches: the count from the
+// two edges around the guess, then NaN and v >= e[bins] to the last bin and
+// v < e[0] to the first (bucketize's count, minus one, clamped).
+__device__ __forceinline__ int bin_tight(float v, const float* e, int bins, float e0, float elast, float inv_step) {
+  const int g = grid_guess(v, e0, inv_step, bins);  // in [1, bins] for every v
+  const float lo = e[g - 1], hi = e[g];
+  const int c = g - (lo > v ? 1 : 0) + (g < bins && hi <= v ? 1 : 0);
+  return (!(v == v) || v >= elast) ? bins - 1 : (v < e0 ? 0 : c - 1);
+}
+
+// Adds of one element, the products in fp64 as the reference forms them
+// (w v is exact; w = 1 gives v and v v exactly).
+__device__ __forceinline__ void add_moments(const HistLds& h, int c, float v, float w) {
+  const double vd = (double)v, wd = (double)w;
+  const double wv = wd * vd;
+  atomicAdd(&h.w[c], wd);
+  atomicAdd(&h.t[c], wv);
+  atomicAdd(&h.s[c], wv * vd);
+}
+
+// max over a segment of lanes (xor butterfly over `span` lanes), NaN winning
+__device__ __forceinline__ float seg_max_nan(float a, int span) {
+  for (int o = 1; o < span; o <<= 1) {
+    const float b = __shfl_xor(a, o, 64);
+    a = (!(a == a) || !(b == b)) ? __builtin_nanf("") : (b > a ? b : a);
+  }
+  return a;
+}
+
+// Four consecutive elements as fp32 (one 16-byte or 8-byte load).
+template <int DT>
+__device__ __forceinline__ void load4(const void* x, int64_t i, float (&v)[4]) {
+  if constexpr (DT == kF32) {
+    const f32x4 q = *(const f32x4*)((const float*)x + i);
+    v[0] = q[0], v[1] = q[1], v[2] = q[2], v[3] = q[3];
+  } else {
+    const u32x2 q = *(const u32x2*)((const uint16_t*)x + i);
+    const uint32_t h[4] = {q[0] & 0xFFFFu, q[0] >> 16, q[1] & 0xFFFFu, q[1] >> 16};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = DT == kBF16 ? bf2f(h[j]) : h2f_exact(h[j]);
+  }
+}
+
+// VEC: n % 4 == 0 and block_size is 0 or a power of two in [4, 256].  Each
+// lane takes four consecutive elements (one load), so a wave covers 256
+// elements and a block is block_size / 4 consecutive lanes, whose amax is a
+// butterfly over those lanes.  Otherwise one thread per block (or element).
+template <int DT, bool VEC, bool W>
+__global__ __launch_bounds__(kHistThreads) void lcq_hist_kernel(const void* __restrict__ x, int64_t n, int64_t bs,
+                                                                float quant_max, const float* __restrict__ wts,
+                                                                int64_t wper, const float* __restrict__ edges,
+                                                                int bins, double* __restrict__ gw,
+                                                                double* __restrict__ gt, double* __restrict__ gs) {
+  __shared__ double s_w[kHistMaxBins], s_t[kHistMaxBins], s_s[kHistMaxBins];
+  __shared__ float s_e[kHistMaxBins + 1];
+  __shared__ int s_loose;
+  if (threadIdx.x == 0) s_loose = 0;
+  for (int j = threadIdx.x; j < bins; j += kHistThreads) s_w[j] = s_t[j] = s_s[j] = 0.0;
+  for (int j = threadIdx.x; j <= bins; j += kHistThreads) s_e[j] = edges[j];
+  __syncthreads();
+  const float e0 = s_e[0], elast = s_e[bins];
+  const float inv_step = (float)bins / (elast - e0);
+  {
+    // can the guess be trusted to within one?  (edges ascending, and the
+    // guess at and just below every edge within one of its count)
+    bool loose = false;
+    for (int j = threadIdx.x; j <= bins; j += kHistThreads) {
+      const float ej = s_e[j];
+      // the float just below ej (finite ej)
+      const uint32_t eb = f2u(ej);
+      const float below = (eb & 0x7FFFFFFFu) == 0 ? u2f(0x80000001u) : u2f((eb >> 31) ? eb + 1u : eb - 1u);
+      loose |= !(ej == ej) || (j > 0 && !(s_e[j - 1] < ej));
+      if (j >= 1 && j <= bins - 1) {
+        loose |= grid_guess(ej, e0, inv_step, bins) < j;
+        loose |= grid_guess(below, e0, inv_step, bins) > j + 1;
+      }
+    }
+    if (loose) s_loose = 1;
+  }
+  __syncthreads();
+  const bool tight = s_loose == 0;
+  const HistLds h{s_w, s_t, s_s, s_e};
+  const float eps = 1e-12f;
+  if constexpr (VEC) {
+    constexpr int U = 4;  // groups of 256 elements per wave in flight
+    const int lane = threadIdx.x & 63;
+    const int span = bs > 0 ? (int)(bs / 4) : 1;
+    const int64_t groups = (n + 255) / 256;
+    const int64_t wv = (int64_t)blockIdx.x * (kHistThreads / 64) + (threadIdx.x >> 6);
+    const int64_t nw = (int64_t)gridDim.x * (kHistThreads / 64);
+    const uint32_t per = (uint32_t)wper;
+    // the element loop, compiled once per kind of bin search (the choice is
+    // uniform, so it is made outside the loop)
+    auto run = [&](auto tight_c) {
+      constexpr bool T = decltype(tight_c)::value;
+      for (int64_t g0 = wv * U; g0 < groups; g0 += nw * U) {
+        float v[U][4];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t i = (g0 + u) * 256 + lane * 4;
+          ok[u] = g0 + u < groups && i < n;
+          load4<DT>(x, ok[u] ? i : 0, v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (bs > 0) {
+            float a = 0.0f;
+            bool nan = false;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float m = fabsf(v[u][j]);
+              nan |= !(m == m);
+              a = m > a ? m : a;
+            }
+            // blocks lie wholly inside or wholly outside n, so lanes past n
+            // only meet each other in the butterfly
+            a = seg_max_nan(nan ? __builtin_nanf("") : a, span);
+            // torch's amax propagates NaN; clamp_min keeps it
+            const float scale = ((a == a) ? (a > eps ? a : eps) : a) / quant_max;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[u][j] = v[u][j] / scale;
+          }
+          // lanes past n add v = 0 with weight 0, which changes no sum
+          float w[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+          if constexpr (W) {
+            // weight of element i: wts[i % period], from the group's start
+            // (wave-uniform) plus the lane's offset below 256
+            const uint32_t base = (uint32_t)(((g0 + u) * 256) % wper);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t k = base + (uint32_t)(lane * 4 + j);
+              w[j] = wts[per >= 256u ? (k >= per ? k - per : k) : k % per];
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float vj = ok[u] ? v[u][j] : 0.0f;
+            const int c = T ? bin_tight(vj, s_e, bins, e0, elast, inv_step)
+                            : min(max(edges_at_or_below(vj, s_e, bins, e0, elast, inv_step, false) - 1, 0), bins - 1);
+            add_moments(h, c, vj, ok[u] ? w[j] : 0.0f);
+          }
+        }
+      }
+    };
+    if (tight)
+      run(std::integral_constant<bool, true>());
+    else
+      run(std::integral_constant<bool, false>());
+  } else {
+    const int64_t tid = (int64_t)blockIdx.x * kHistThreads + threadIdx.x, nt = (int64_t)gridDim.x * kHistThreads;
+    if (bs == 0) {
+      for (int64_t i = tid; i < n; i += nt)
+        hist_add(h, bins, e0, elast, inv_step, tight, load_elem<DT>(x, i), wts ? wts[i % wper] : 1.0f);
+    } else {
+      for (int64_t b = tid; b < n / bs; b += nt) {
+        const int64_t i0 = b * bs;
+        float amax = 0.0f;
+        bool nan = false;
+        for (int64_t i = i0; i < i0 + bs; ++i) {
+          const float a = fabsf(load_elem<DT>(x, i));
+          nan |= !(a == a);
+          amax = a > amax ? a : amax;
+        }
+        const float scale = (nan ? __builtin_nanf("") : (amax > eps ? amax : eps)) / quant_max;
+        for (int64_t i = i0; i < i0 + bs; ++i)
+          hist_add(h, bins, e0, elast, inv_step, tight, load_elem<DT>(x, i) / scale, wts ? wts[i % wper] : 1.0f);
+      }
+    }
+  }
+  __syncthreads();
+  // every workgroup starts its flush at a different bin, so that workgroups
+  // finishing together do not queue on the same addresses
+  const int rot = (int)(((int64_t)blockIdx.x * 521) % bins);
+  for (int jj = threadIdx.x; jj < bins; jj += kHistThreads) {
+    const int j = jj + rot < bins ? jj + rot : jj + rot - bins;
+    const double a = s_w[j], t = s_t[j], q = s_s[j];
+    if (a != 0.0 || t != 0.0 || q != 0.0) {
+      atomicAdd(gw + j, a);
+      atomicAdd(gt + j, t);
+      atomicAdd(gs + j, q);
+    }
+  }
+}
+
+template <int DT, bool VEC>
+void launch_hist_w(unsigned grid, const void* x, int64_t n, int64_t bs, float quant_max, const float* w, int64_t wper,
+                   const float* edges, int bins, double* gw, double* gt, double* gs, hipStream_t st) {
+  if (w)
+    hipLaunchKernelGGL((lcq_hist_kernel<DT, VEC, true>), dim3(grid), dim3(kHistThreads), 0, st, x, n, bs, quant_max, w,
+                       wper, edges, bins, gw, gt, gs);
+  else
+    hipLaunchKernelGGL((lcq_hist_kernel<DT, VEC, false>), dim3(grid), dim3(kHistThreads), 0, st, x, n, bs, quant_max,
+                       w, wper, edges, bins, gw, gt, gs);
+}
+
+template <int DT>
+int launch_hist(const void* x, int64_t n, int64_t bs, float quant_max, const float* w, int64_t wper,
+                const float* edges, int bins, double* gw, double* gt, double* gs, hipStream_t st) {
+  const bool vec = n % 4 == 0 && (bs == 0 || (bs >= 4 && bs <= 256 && (bs & (bs - 1)) == 0)) &&
+                   aligned(x, DT == kF32 ? 16 : 8);
+  if (vec)
+    launch_hist_w<DT, true>(grid_for((n + 255) / 256 * 64, kHistThreads * 4, 1), x, n, bs, quant_max, w, wper, edges,
+                            bins, gw, gt, gs, st);
+  else
+    launch_hist_w<DT, false>(grid_for(bs > 0 ? n / bs : n, kHistThreads, 1), x, n, bs, quant_max, w, wper, edges,
+                             bins, gw, gt, gs, st);
+  return check_launch("lcq_histogram");
+}
+
+}  // namespace
+
+int lcq_histogram(const void* x, int dtype, int64_t n, int64_t block_size, float quant_max, const float* weights,
+                  int64_t weights_period, const float* edges, int bins, double* weight, double* total,
+                  double* square, hipStream_t st) {
+  if (n < 0 || block_size < 0) return set_error(kErrInvalid, "lcq_histogram: negative size");
+  if (bins < 1 || bins > kHistMaxBins)
+    return set_error(kErrInvalid, "lcq_histogram: bins must be in [1, %d] (got %d)", kHistMaxBins, bins);
+  if (block_size > 0 && n % block_size != 0)
+    return set_error(kErrInvalid, "lcq_histogram: %lld elements do not split into blocks of %lld", (long long)n,
+                     (long long)block_size);
+  if (weights && (weights_period < 1 || weights_period > INT32_MAX))
+    return set_error(kErrInvalid, "lcq_histogram: weights_period must be in [1, 2^31)");
+  if (!edges || !weight || !total || !square) return set_error(kErrInvalid, "lcq_histogram: null buffer");
+  if (n == 0) return kOk;
+  if (!x) return set_error(kErrInvalid, "lcq_histogram: null input");
+  switch (dtype) {
+    case kF32: return launch_hist<kF32>(x, n, block_size, quant_max, weights, weights_period, edges, bins, weight, total, square, st);
+    case kBF16: return launch_hist<kBF16>(x, n, block_size, quant_max, weights, weights_period, edges, bins, weight, total, square, st);
+    case kF16: return launch_hist<kF16>(x, n, block_size, quant_max, weights, weights_period, edges, bins, weight, total, square, st);
+    default: return set_error(kErrInvalid, "lcq_histogram: dtype %d not supported (fp32, bf16, fp16)", dtype);
+  }
+}
+
+}  // namespace vqx

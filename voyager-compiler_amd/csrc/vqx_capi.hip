@@ -281,4 +281,12 @@ int vqx_spmm_csr(const void* data, int32_t data_dtype, const int32_t* indices, c
   return spmm_csr(a, (hipStream_t)stream);
 }
 
+int vqx_lcq_histogram(const void* x, int32_t x_dtype, int64_t n, int64_t block_size, float quant_max,
+                      const float* weights, int64_t weights_period, const float* edges, int32_t bins,
+                      double* weight, double* total, double* square, vqx_stream_t stream) {
+  g_err[0] = 0;
+  return lcq_histogram(x, x_dtype, n, block_size, quant_max, weights, weights_period, edges, bins, weight, total,
+                       square, (hipStream_t)stream);
+}
+
 }  // extern "C"

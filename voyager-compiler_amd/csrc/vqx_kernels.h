@@ -104,4 +104,10 @@ int csr_slice(const void* data, int dtype, const int32_t* indices, const int32_t
 int csr_decode(const CsrDecode& d, hipStream_t st);
 int spmm_csr(const SpmmArgs& a, hipStream_t st);
 
+// vqx_calib.hip
+constexpr int kHistMaxBins = 4096;
+int lcq_histogram(const void* x, int dtype, int64_t n, int64_t block_size, float quant_max, const float* weights,
+                  int64_t weights_period, const float* edges, int bins, double* weight, double* total,
+                  double* square, hipStream_t st);
+
 }  // namespace vqx

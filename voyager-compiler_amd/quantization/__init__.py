@@ -1,4 +1,5 @@
-"""QuantizationSpec / FakeQuantize API of the hot path."""
+"""QuantizationSpec / FakeQuantize API of the hot path, and the learned-codebook
+calibration histogram."""
 
 from .fake_quantize import (  # noqa: F401
     FakeQuantizeFunction,
@@ -6,5 +7,6 @@ from .fake_quantize import (  # noqa: F401
     MXFakeQuantizeFunction,
     get_quantization_map,
 )
+from .lcq import HISTOGRAM_BINS, Histogram  # noqa: F401
 from .qspec import QScheme, parse_spec_fields  # noqa: F401
 from .quantizer import QuantizationSpec  # noqa: F401
