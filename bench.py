@@ -50,11 +50,88 @@ def parse():
 
 
 # ---------------------------------------------------------------------------
+# CPU oracle timings: each returns a callable that times the reference's
+# torch-CPU op sequence (the oracle) on a bounded sample of the config and
+# returns (seconds for the whole config, what the sample was)
+# ---------------------------------------------------------------------------
+def _timed(f):
+    t0 = time.perf_counter()
+    f()
+    return time.perf_counter() - t0
+
+
+def cpu_c1(torch, xc):
+    def run():
+        from oracle import formats as F
+        from oracle import reference_ops as R
+        q = R.table_tensor(F.posit_table(8, 1))
+        return _timed(lambda: R.fake_quantize_per_tensor(xc, q, torch.ones(()))), \
+            "full input: FakeQuantizeFunction.forward (vmap of x / 1 through the posit8_1 table)"
+    return run
+
+
+def cpu_c2_decode(torch, xc):
+    def run():
+        from oracle import formats as F
+        from oracle import reference_ops as R
+        xs = xc[:512]
+        s, q = R.quantize_mx(xs, R.table_tensor(F.quantization_table("nf4")), [-1], 64, 1.0, False)
+        return _timed(lambda: R.dequantize(q, s, None, [-1], 64)) * 8, \
+            "rows 0-511 (1/8), scaled: dequantize (values x expand(scale))"
+    return run
+
+
+def cpu_c3(torch, xc, dtype, qmax, fake):
+    def run():
+        from oracle import formats as F
+        from oracle import reference_ops as R
+        xs = xc[:1024]
+        q = R.table_tensor(F.quantization_table(dtype))
+        f = R.mx_fake_quantize if fake else R.quantize_mx
+        return _timed(lambda: f(xs, q, [-1], 32, qmax, True)) * 8, \
+            f"rows 0-1023 (1/8), scaled: {'MXFakeQuantizeFunction.forward' if fake else 'quantize_mx'}"
+    return run
+
+
+def cpu_c4(torch, xc, cbc, decode):
+    def run():
+        from oracle import reference_ops as R
+        xs, cs = xc[:128], cbc[:128]
+        if decode:
+            codes = R.codebook_encode_rows(xs, cs)
+            return _timed(lambda: R.codebook_decode_rows(codes, cs)) * 32, "rows 0-127 (1/32), scaled: decode"
+        return _timed(lambda: R.codebook_encode_rows(xs, cs)) * 32, \
+            "rows 0-127 (1/32), scaled: per-row argmin over the codebook"
+    return run
+
+
+def cpu_c5(torch, Ac, N):
+    def run():
+        from oracle import formats as F
+        from oracle import reference_ops as R
+        M, K = Ac.shape
+        g = torch.Generator().manual_seed(4)
+        codes = torch.randint(0, 16, (N, K), generator=g).to(torch.bfloat16)   # weight codes as floats
+        scale = (torch.rand(N, K // 64, generator=g) * 0.05).to(torch.bfloat16)
+        nf = R.table_tensor(F.nf_levels(4))
+        rows = min(M, 256)
+        R.linear_mx(Ac[:1], codes, None, scale, 64, nf)  # warm-up
+        full = _timed(lambda: R.linear_mx(Ac[:rows], codes, None, scale, 64, nf))
+        if rows == M:
+            return full, "full M: linear_mx (weight_code[w] * expand(scale), then F.linear in bf16)"
+        dec = _timed(lambda: nf[codes.to(torch.long)] * R.expand(scale, codes.shape, 64))
+        return dec + (full - dec) * (M / rows), \
+            f"rows 0-{rows - 1}: the weight decode timed once, the product scaled to M = {M}"
+    return run
+
+
+# ---------------------------------------------------------------------------
 # configs: setup() -> (launch callable, info)
 # ---------------------------------------------------------------------------
 def setup_c1(vqx, torch, L):
     torch.manual_seed(0)
-    x = torch.randn(4096, 4096, dtype=torch.float32).cuda()
+    xc = torch.randn(4096, 4096, dtype=torch.float32)
+    x = xc.cuda()
     y = torch.empty_like(x)
     codes = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
     desc = vqx.parse_format("posit8_1").desc(x.device)
@@ -64,7 +141,7 @@ def setup_c1(vqx, torch, L):
     n = x.numel()
     return (lambda: fn(*args)), dict(
         name="C1 posit8_1 fake-quant + uint8 codes, fp32 4096x4096 N(0,1) seed 0",
-        elements=n, bytes=9 * n, bound="hbm", dtype="f32->u8")
+        elements=n, bytes=9 * n, bound="hbm", dtype="f32->u8", cpu=cpu_c1(torch, xc))
 
 
 def c2_input(torch, rows=4096, cols=11008, seed=1):
@@ -102,7 +179,7 @@ def setup_c2(vqx, torch, L, decode=False):
     dargs = (L.ptr(codes), 4, L.ptr(dtab), dtab.numel(), L.ptr(scale), 0, n, 64, L.ptr(out), L.BF16, st)
     return (lambda: dec(*dargs)), dict(
         name="C2 NF4 block-64 decode: packed codes + fp32 scales -> bf16 4096x11008",
-        elements=n, bytes=algo, bound="hbm", dtype="u4->bf16")
+        elements=n, bytes=algo, bound="hbm", dtype="u4->bf16", cpu=cpu_c2_decode(torch, xc))
 
 
 def c3_input(torch, rows=8192, cols=8192, seed=2):
@@ -118,8 +195,10 @@ _C3_X = {}
 
 def setup_c3(vqx, torch, L, dtype, qmax, fake=False):
     if "x" not in _C3_X:
-        _C3_X["x"] = c3_input(torch).cuda()
+        _C3_X["xc"] = c3_input(torch)
+        _C3_X["x"] = _C3_X["xc"].cuda()
     x = _C3_X["x"]
+    cpu = cpu_c3(torch, _C3_X["xc"], dtype, qmax, fake)
     n = x.numel()
     fmt = vqx.parse_format(dtype)
     desc = fmt.desc(x.device)
@@ -133,7 +212,7 @@ def setup_c3(vqx, torch, L, dtype, qmax, fake=False):
                 None, L.ptr(sc), None, None, None, L.ptr(y), None, 1, st)
         return (lambda: fn(*args)), dict(
             name=f"C3 MX block-32 {dtype} fake-quant (bf16 values + bf16 scales), bf16 8192x8192 Laplace seed 2",
-            elements=n, bytes=n * 4 + sc.numel() * 2, bound="hbm", dtype="bf16")
+            elements=n, bytes=n * 4 + sc.numel() * 2, bound="hbm", dtype="bf16", cpu=cpu)
     cb = fmt.code_bits
     codes = torch.empty(n * cb // 8, dtype=torch.uint8, device="cuda")
     e8 = torch.empty(8192, 256, dtype=torch.uint8, device="cuda")
@@ -141,7 +220,7 @@ def setup_c3(vqx, torch, L, dtype, qmax, fake=False):
             None, None, None, L.ptr(e8), None, None, L.ptr(codes), 0, st)
     return (lambda: fn(*args)), dict(
         name=f"C3 MX block-32 {dtype} + E8M0 scales, bf16 8192x8192 Laplace x 10^U(-1,1) seed 2 -> packed codes",
-        elements=n, bytes=n * 2 + n * cb // 8 + e8.numel(), bound="hbm", dtype=f"bf16->{dtype}")
+        elements=n, bytes=n * 2 + n * cb // 8 + e8.numel(), bound="hbm", dtype=f"bf16->{dtype}", cpu=cpu)
 
 
 def c4_codebooks(torch, rows, K, seed=3):
@@ -170,20 +249,21 @@ def setup_c4(vqx, torch, L, K, decode=False):
     if not decode:
         return (lambda: enc(*eargs)), dict(
             name=f"C4 per-channel codebook encode K={K}, fp32 4096x4096 N(0,1) seed 3 -> uint8 indices",
-            elements=n, bytes=algo, bound="hbm", dtype="f32->u8", cpu_input=(xc, cbc))
+            elements=n, bytes=algo, bound="hbm", dtype="f32->u8", cpu=cpu_c4(torch, xc, cbc, False))
     enc(*eargs)
     out = torch.empty_like(x)
     dec = L.load().vqx_codebook_decode
     dargs = (L.ptr(codes), 4096, 4096, L.ptr(cb), K, L.ptr(out), L.F32, st)
     return (lambda: dec(*dargs)), dict(
         name=f"C4 per-channel codebook decode K={K}: uint8 indices -> fp32 4096x4096",
-        elements=n, bytes=algo, bound="hbm", dtype="u8->f32")
+        elements=n, bytes=algo, bound="hbm", dtype="u8->f32", cpu=cpu_c4(torch, xc, cbc, True))
 
 
 def setup_c5(vqx, torch, L):
     g = torch.Generator().manual_seed(4)
     M, N, K = 2048, 11008, 4096
-    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    Ac = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    A = Ac.cuda()
     W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).cuda()
     Q = torch.ops.quantized_ops
     sc, codes = Q.quantize_mx_packed(W, "nf4", -1, 64, False, 1.0, "float32")
@@ -196,7 +276,7 @@ def setup_c5(vqx, torch, L):
     return (lambda: fn(*args)), dict(
         name="C5 NF4-dequant linear: A bf16 [2048,4096] x W NF4 block-64 [11008,4096]^T -> bf16, fp32 accumulate",
         elements=M * N, flops=2 * M * N * K, bytes=M * K * 2 + N * K // 2 + N * K // 64 * 4 + M * N * 2,
-        bound="mfma", dtype="bf16")
+        bound="mfma", dtype="bf16", cpu=cpu_c5(torch, Ac, N))
 
 
 def setup_c5_skinny(vqx, torch, L, M):
@@ -204,7 +284,8 @@ def setup_c5_skinny(vqx, torch, L, M):
     bound by the 4-bit weight's bytes)."""
     g = torch.Generator().manual_seed(4)
     N, K = 11008, 4096
-    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    Ac = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    A = Ac.cuda()
     W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).cuda()
     Q = torch.ops.quantized_ops
     sc, codes = Q.quantize_mx_packed(W, "nf4", -1, 64, False, 1.0, "float32")
@@ -216,7 +297,7 @@ def setup_c5_skinny(vqx, torch, L, M):
     return (lambda: fn(*args)), dict(
         name=f"C5 skinny NF4-dequant linear: A bf16 [{M},4096] x W NF4 block-64 [11008,4096]^T -> bf16",
         elements=M * N, bytes=N * K // 2 + N * K // 64 * 4 + M * K * 2 + M * N * 2, flops=2 * M * N * K,
-        bound="hbm", dtype="bf16", keep=(A, codes, sc, lv, out))
+        bound="hbm", dtype="bf16", keep=(A, codes, sc, lv, out), cpu=cpu_c5(torch, Ac, N))
 
 
 def setup_l1(vqx, torch, L):
@@ -419,12 +500,17 @@ def cpu_baseline_c2(torch, x):
 
 
 def cpu_oracle_time(torch, k, info, kernel_ms):
-    """One run of the CPU oracle (the reference's torch-CPU op sequence) on an
-    outlier or calibration config's full input, timed beside the GPU figure."""
+    """One run of the CPU oracle (the reference's torch-CPU op sequence) on a
+    config's input, or a bounded sample of it scaled to the whole config,
+    timed beside the GPU figure."""
     from oracle import formats as F
     from oracle import reference_ops as R
 
     torch.set_num_threads(os.cpu_count() or 1)
+    if "cpu" in info:
+        dt, sample = info["cpu"]()
+        return {"seconds": dt, "cores": torch.get_num_threads(), "kind": "port",
+                "gpu_speedup": dt / (kernel_ms * 1e-3), "elements_per_s": info["elements"] / dt, "sample": sample}
     if k == "l1_histogram":
         x = info["cpu_input"]
 
@@ -450,7 +536,7 @@ def cpu_oracle_time(torch, k, info, kernel_ms):
     fn()
     dt = time.perf_counter() - t0
     return {"seconds": dt, "cores": torch.get_num_threads(), "kind": "port", "gpu_speedup": dt / (kernel_ms * 1e-3),
-            "sample": "one run on the config's full input"}
+            "elements_per_s": info["elements"] / dt, "sample": "one run on the config's full input"}
 
 
 def _cpu_model():
@@ -608,8 +694,10 @@ def main():
             results[k]["gathered_bytes"] = info["gathered_bytes"]
             results[k]["gathered_GBps"] = info["gathered_bytes"] / (ms * 1e-3) / 1e9
             results[k]["spmm_TFLOPs"] = info["flops"] / (ms * 1e-3) / 1e12
-        if (k.startswith("o") or k.startswith("l")) and not a.no_cpu:
+        if not a.no_cpu and ("cpu" in info or k.startswith("o") or k.startswith("l")):
             results[k]["cpu_oracle"] = cpu_oracle_time(torch, k, info, ms)
+            print(f"[bench] {k}: CPU oracle {results[k]['cpu_oracle']['seconds'] * 1e3:.1f} ms "
+                  f"({results[k]['cpu_oracle']['sample']})", file=sys.stderr, flush=True)
         if k == HEADLINE:
             info_head = info
         del launch
