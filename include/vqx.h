@@ -326,6 +326,24 @@ int vqx_lcq_histogram(const void* x, int32_t x_dtype, int64_t n, int64_t block_s
                       const float* weights, int64_t weights_period, const float* edges, int32_t bins,
                       double* weight, double* total, double* square, vqx_stream_t stream);
 
+/*
+ * The column loop of GPTQ's compensate_weight for one microscaling block
+ * (src/vc/quantization/gptq.py:241-262).  work, out: fp32 [rows, ld] row-major;
+ * the block is columns col0 .. col0 + ncols - 1 (ncols <= 64).  For each row r
+ * and block column j in order, c = col0 + j:
+ *   q = float(qmap[bf16(w[r, c] / scale[r])]) * scale[r];  out[r, c] = q
+ *   d = (w[r, c] - q) / max(hinv[c, c], 1e-12);            deltas[r, j] = d
+ *   w[r, c + k] -= d * hinv[c, c + k] for the block's later columns (on a
+ *   private copy: work is not written)
+ * each operation rounded to fp32 as torch performs it (no fused multiply-add).
+ * scale: fp32 [rows]; hinv: fp32 upper Cholesky factor of the inverse
+ * Hessian, row stride ldh; qmap: 65536 bf16 patterns, 16-byte aligned;
+ * deltas: fp32 [rows, ncols].
+ */
+int vqx_gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int32_t ncols, const float* scale,
+                   const float* hinv, int64_t ldh, const uint16_t* qmap, float* out, float* deltas,
+                   vqx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,8 @@ __all__ = [
     "csr_to_dense",
     "unit_scale",
     "lcq_histogram_add",
+    "gptq_block",
+    "gptq_compensate_weight",
 ]
 
 
@@ -357,3 +359,79 @@ def lcq_histogram_add(values, weights, quant_min, quant_max, bins=4001, sums=Non
     sums[1].index_add_(0, index, w * v)
     sums[2].index_add_(0, index, w * v * v)
     return sums
+
+
+# ---------------------------------------------------------------------------
+# GPTQ compensation (src/vc/quantization/gptq.py)
+# ---------------------------------------------------------------------------
+def gptq_block(work, scale, hinv, qmap, start, end):
+    """The column loop of src/vc/quantization/gptq.py:241-262 for one block on
+    a private copy of work: returns (out[:, start:end], deltas)."""
+    work = work.clone()
+    out = torch.zeros(work.shape[0], end - start)
+    deltas = torch.zeros(work.shape[0], end - start)
+    for offset, column in enumerate(range(start, end)):
+        values = work[:, column]
+        quantized = vmap((values / scale).bfloat16(), qmap).float() * scale
+        out[:, offset] = quantized
+        delta = (values - quantized) / hinv[column, column].clamp_min(1e-12)
+        deltas[:, offset] = delta
+        if column + 1 < end:
+            work[:, column + 1:end] -= delta.unsqueeze(1) * hinv[column, column + 1:end].unsqueeze(0)
+    return out, deltas
+
+
+def _hessian_inverse_chol(hessian, tokens, damping):
+    """src/vc/quantization/gptq.py:32-71."""
+    hessian = hessian / max(tokens, 1)
+    damp = damping * hessian.diagonal().mean().clamp_min(1e-12)
+    applied = 0
+    for escalation in (1, 10, 100, 1000, 10000):
+        hessian.diagonal().add_((escalation - applied) * damp)
+        applied = escalation
+        try:
+            chol = torch.linalg.cholesky(hessian)
+            return torch.linalg.cholesky(torch.cholesky_inverse(chol), upper=True)
+        except torch.linalg.LinAlgError:
+            continue
+    raise torch.linalg.LinAlgError("Hessian not positive-definite")
+
+
+def gptq_compensate_weight(weight, hessian, tokens, qmap, quant_max, block_size, damping, act_order=True,
+                           within_block=True, scale_qmap=None):
+    """src/vc/quantization/gptq.py:184-270 without the shrink search (scale =
+    calculate_mx_qparam of the block, clamped at 1e-12), torch CPU fp32."""
+    perm = None
+    if act_order and weight.shape[1] % block_size == 0:
+        blocks = weight.shape[1] // block_size
+        diagonal = hessian.diagonal().reshape(blocks, block_size)
+        block_order = torch.argsort(diagonal.mean(dim=1), descending=True)
+        rank = (torch.argsort(diagonal, dim=1, descending=True) if within_block
+                else torch.arange(block_size).expand(blocks, block_size))
+        perm = (torch.arange(blocks).unsqueeze(1) * block_size + rank)[block_order].reshape(-1)
+        hessian = hessian[perm][:, perm]
+        weight = weight[:, perm]
+    hinv = _hessian_inverse_chol(hessian, tokens, damping)
+    out = gptq_compensate_with_factor(weight, hinv, qmap, quant_max, block_size, scale_qmap)
+    if perm is None:
+        return out
+    restored = torch.empty_like(out)
+    restored[:, perm] = out
+    return restored
+
+
+def gptq_compensate_with_factor(weight, hinv, qmap, quant_max, block_size, scale_qmap=None):
+    """The block loop of src/vc/quantization/gptq.py:239-265 on columns in
+    processing order, given the factor."""
+    work = weight.float().clone()
+    out = torch.zeros_like(work)
+    for start in range(0, weight.shape[1], block_size):
+        end = min(start + block_size, weight.shape[1])
+        block = work[:, start:end]
+        scale = calculate_mx_qparam(block, [-1], block.shape[-1], quant_max, False, scale_qmap).reshape(-1)
+        scale = scale.clamp_min(1e-12)
+        o, deltas = gptq_block(work, scale, hinv, qmap, start, end)
+        out[:, start:end] = o
+        if end < weight.shape[1]:
+            work[:, end:] -= deltas @ hinv[start:end, end:]
+    return out

@@ -1,0 +1,105 @@
+"""GPU GPTQ compensation (src/vc/quantization/gptq.py:184-270): the per-block
+column loop bit for bit against the oracle; the whole block loop bit for bit
+where the factor makes the later-column updates exact; and, with a dense
+factor (a library GEMM on each side, summed in different orders), the
+Hessian-weighted error of compensate_weight against the oracle's."""
+
+import types
+
+import pytest
+import torch
+
+from oracle import formats as F
+from oracle import reference_ops as R
+
+
+def qmap_of(dtype):
+    return R.table_tensor(F.quantization_table(dtype))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["int4", "nf4", "fp4_e2m1"])
+@pytest.mark.parametrize("rows,cols,start,end", [(300, 64, 0, 64), (257, 128, 64, 81), (64, 32, 31, 32)])
+def test_gptq_block_matches_oracle(vqx, dtype, rows, cols, start, end):
+    g = torch.Generator().manual_seed(rows + cols + start)
+    work = torch.randn(rows, cols, generator=g)
+    scale = torch.rand(rows, generator=g) * 0.5 + 0.05
+    A = torch.randn(cols, cols, generator=g) * 0.1 + torch.eye(cols)
+    hinv = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(A @ A.T + 0.1 * torch.eye(cols))),
+                                 upper=True)
+    q = qmap_of(dtype)
+    want_out, want_d = R.gptq_block(work, scale, hinv, q, start, end)
+    out = torch.zeros(rows, cols, device="cuda")
+    d = torch.empty(rows, end - start, device="cuda")
+    L = vqx._lib
+    wk, sc, hv, qm = work.cuda(), scale.cuda(), hinv.contiguous().cuda(), q.cuda()
+    L.call("vqx_gptq_block", L.ptr(wk), rows, cols, start, end - start, L.ptr(sc), L.ptr(hv), cols, L.ptr(qm),
+           L.ptr(out), L.ptr(d), L.stream_of(wk))
+    assert torch.equal(out[:, start:end].cpu(), want_out)
+    assert torch.equal(d.cpu(), want_d)
+    assert torch.equal(wk.cpu(), work)       # the block's columns of work are left as they were
+
+
+def make_problem(seed, out_f, in_f):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(4 * in_f, in_f, generator=g) @ (torch.randn(in_f, in_f, generator=g) * 0.3 + torch.eye(in_f))
+    return (torch.randn(out_f, in_f, generator=g) * 0.05), X.T @ X, 4 * in_f
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,qmax", [("int4", 7.0), ("nf4", 1.0), ("fp4_e2m1", 6.0)])
+def test_compensation_with_block_diagonal_factor_is_exact(vqx, dtype, qmax):
+    # a factor with exact zeros between blocks makes every later-column update
+    # an exact zero on both sides, so the whole compensation is bit-exact
+    g = torch.Generator().manual_seed(7)
+    # any upper-triangular factor with a positive diagonal will do
+    blocks = [torch.triu(torch.randn(64, 64, generator=g) * 0.05, diagonal=1)
+              + torch.diag(0.2 + torch.rand(64, generator=g)) for _ in range(3)]
+    hinv = torch.block_diag(*blocks)
+    w = torch.randn(96, 192, generator=g) * 0.05
+    q = qmap_of(dtype)
+    fq = types.SimpleNamespace(qmap=q.cuda(), scale_qmap=None, quant_max=qmax, block_size=64, ch_axis=-1)
+    got = vqx.quantization.gptq.compensate_with_factor(w.cuda(), hinv.cuda(), hinv.diagonal().cuda(), fq).cpu()
+    want = R.gptq_compensate_with_factor(w, hinv, q, qmax, 64)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,qmax", [("int4", 7.0), ("nf4", 1.0)])
+@pytest.mark.parametrize("act_order", [True, False])
+def test_compensate_weight_quality_matches_oracle(vqx, dtype, qmax, act_order):
+    # with a dense factor the later-column updates are summed in different
+    # orders (GPU and CPU GEMMs), and GPTQ amplifies any difference once a
+    # rounding decision flips: compare what the compensation is for, the
+    # Hessian-weighted error, against the oracle's and against plain rounding
+    w, H, tokens = make_problem(3, 128, 256)
+    q = qmap_of(dtype)
+    fq = types.SimpleNamespace(qmap=q.cuda(), scale_qmap=None, quant_max=qmax, block_size=64, ch_axis=-1)
+    got = vqx.quantization.compensate_weight(w.cuda(), H.cuda(), tokens, fq, 0.01, act_order=act_order).cpu()
+    want = R.gptq_compensate_weight(w, H.clone(), tokens, q, qmax, 64, 0.01, act_order=act_order)
+    assert got.shape == want.shape and got.dtype == torch.float32
+
+    def err(o):
+        e = (w - o).double()
+        return torch.einsum("ij,jk,ik->", e, H.double() / tokens, e).item()
+
+    s = R.calculate_mx_qparam(w, [-1], 64, qmax).repeat_interleave(64, dim=1)
+    plain = R.vmap((w / s).bfloat16(), q).float() * s
+    assert abs(err(got) - err(want)) <= 0.05 * err(want)
+    assert err(got) < 0.9 * err(plain)
+
+
+@pytest.mark.gpu
+def test_compensate_weight_shrink_and_scale_codebook(vqx):
+    w, H, tokens = make_problem(5, 64, 128)
+    fq = types.SimpleNamespace(qmap=qmap_of("int4").cuda(), scale_qmap=qmap_of("fp8_e5m3").cuda(), quant_max=7.0,
+                               block_size=64, ch_axis=-1)
+    plain = vqx.quantization.compensate_weight(w.cuda(), H.cuda(), tokens, fq, 0.01, shrink=False)
+    shrunk = vqx.quantization.compensate_weight(w.cuda(), H.cuda(), tokens, fq, 0.01, shrink=True)
+    assert torch.isfinite(plain).all() and torch.isfinite(shrunk).all()
+
+    def err(o):
+        e = (w - o.cpu()).double()
+        return torch.einsum("ij,jk,ik->", e, H.double() / tokens, e).item()
+
+    assert err(shrunk) <= 1.05 * err(plain)

@@ -316,3 +316,161 @@ int lcq_histogram(const void* x, int dtype, int64_t n, int64_t block_size, float
 }
 
 }  // namespace vqx
+
+// ---------------------------------------------------------------------------
+// GPTQ column loop of one microscaling block
+// (src/voyager_compiler/quantization/gptq.py:241-262): for each row r and
+// block column j = 0 .. ncols - 1 in order, with c = col0 + j,
+//   q        = float(qmap[bf16(w[r, c] / scale[r])]) * scale[r]
+//   out[r,c] = q
+//   d        = (w[r, c] - q) / max(hinv[c, c], 1e-12)
+//   deltas[r, j] = d
+//   w[r, c + k] -= d * hinv[c, c + k]   for the block's later columns
+// every operation rounded to fp32 as torch performs it (the product and the
+// difference rounded separately, no fused multiply-add).  One thread per
+// row holds the row's block in registers; hinv is the same for every row
+// (scalar loads).  The block's columns of w are left as they were.
+// ---------------------------------------------------------------------------
+namespace vqx {
+namespace {
+
+constexpr int kGptqMaxCols = 64;
+constexpr int kGptqThreads = 256;
+constexpr int kGptqLanes = 4;                          // lanes per row: one DPP quad
+constexpr int kGptqSlots = kGptqMaxCols / kGptqLanes;  // columns per lane
+constexpr int kGptqRowsPerBlock = kGptqThreads / kGptqLanes;
+
+// Lane o's value in every lane of its quad (o is a constant after unrolling).
+__device__ __forceinline__ float quad_bcast(float v, int o) {
+  const int x = __float_as_int(v);
+  int y;
+  switch (o) {
+    case 0: y = __builtin_amdgcn_mov_dpp(x, 0x00, 0xF, 0xF, false); break;
+    case 1: y = __builtin_amdgcn_mov_dpp(x, 0x55, 0xF, 0xF, false); break;
+    case 2: y = __builtin_amdgcn_mov_dpp(x, 0xAA, 0xF, 0xF, false); break;
+    default: y = __builtin_amdgcn_mov_dpp(x, 0xFF, 0xF, 0xF, false); break;
+  }
+  return __int_as_float(y);
+}
+
+// Each row is split over a quad of lanes: lane q keeps columns 4i + q
+// (i < 16) in registers.  For column j the owning lane's value is broadcast
+// in the quad, all four lanes quantize it and form the delta (the same
+// arithmetic, so the same bits), and each lane subtracts delta times the
+// factor from its own later columns.  Every column still sees the
+// reference's sequence of updates, in the same order.  Slots whose column is
+// not after j may be updated too: they are no longer read.  The 65536-entry
+// bf16 table, the block's 64x64 corner of the factor (laid out so a lane's
+// 16 values are contiguous) and its diagonal are staged in LDS; the next
+// column's factor row is read while the current column is processed.
+// Multiply and subtract round separately, as the reference's two torch ops.
+__global__ __launch_bounds__(kGptqThreads) void gptq_block_kernel(
+    const float* __restrict__ work, int64_t rows, int64_t ld, int64_t col0, int ncols,
+    const float* __restrict__ scale, const float* __restrict__ hinv, int64_t ldh,
+    const uint16_t* __restrict__ qmap, float* __restrict__ out, float* __restrict__ deltas) {
+#pragma clang fp contract(off)
+  __shared__ __align__(16) uint16_t lut[65536];
+  __shared__ __align__(16) float hq[kGptqMaxCols * kGptqMaxCols];  // [j][lane][slot] = U[j][4 slot + lane]
+  __shared__ __align__(16) float hd[kGptqMaxCols];                 // U[j][j]
+  {
+    // all of a thread's loads are issued before the first LDS store, so the
+    // staging takes a few L2 round trips, not one per load
+    constexpr int kLutLoads = 65536 / 8 / kGptqThreads;                      // 32 x 16 bytes
+    constexpr int kHLoads = kGptqMaxCols * kGptqMaxCols / kGptqThreads;      // 16 floats
+    const uint4* src = reinterpret_cast<const uint4*>(qmap);
+    uint4* dst = reinterpret_cast<uint4*>(lut);
+    uint4 t[kLutLoads];
+#pragma unroll
+    for (int u = 0; u < kLutLoads; ++u) t[u] = src[threadIdx.x + u * kGptqThreads];
+    float h[kHLoads];
+#pragma unroll
+    for (int u = 0; u < kHLoads; ++u) {
+      const int i = threadIdx.x + u * kGptqThreads, j = i / kGptqMaxCols, k = i % kGptqMaxCols;
+      h[u] = (j < ncols && k < ncols) ? hinv[(col0 + j) * ldh + col0 + k] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kLutLoads; ++u) dst[threadIdx.x + u * kGptqThreads] = t[u];
+#pragma unroll
+    for (int u = 0; u < kHLoads; ++u) {
+      const int i = threadIdx.x + u * kGptqThreads, j = i / kGptqMaxCols, k = i % kGptqMaxCols;
+      hq[j * kGptqMaxCols + (k % kGptqLanes) * kGptqSlots + k / kGptqLanes] = h[u];
+      if (j == k) hd[j] = h[u];
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x % kGptqLanes;
+  const int64_t r = (int64_t)blockIdx.x * kGptqRowsPerBlock + threadIdx.x / kGptqLanes;
+  if (r >= rows) return;  // whole quads leave together
+  float w[kGptqSlots], oq[kGptqSlots], od[kGptqSlots];
+  const float* wr = work + r * ld + col0;
+#pragma unroll
+  for (int i = 0; i < kGptqSlots; ++i) {
+    const int k = i * kGptqLanes + lane;
+    w[i] = k < ncols ? wr[k] : 0.0f;
+    oq[i] = 0.0f;
+    od[i] = 0.0f;
+  }
+  const float s = scale[r];
+  const float* hl = hq + lane * kGptqSlots;
+  float hr[kGptqSlots];
+#pragma unroll
+  for (int i = 0; i < kGptqSlots; ++i) hr[i] = hl[i];
+#pragma unroll
+  for (int j = 0; j < kGptqMaxCols; ++j) {
+    if (j < ncols) {
+      const int owner = j % kGptqLanes, slot = j / kGptqLanes;
+      float hn[kGptqSlots];
+      if (j + 1 < kGptqMaxCols) {
+#pragma unroll
+        for (int i = (j + 2) / kGptqLanes; i < kGptqSlots; ++i) hn[i] = hl[(j + 1) * kGptqMaxCols + i];
+      }
+      const float hcc = hd[j];
+      const float v = quad_bcast(w[slot], owner);
+      const float q = bf2f(lut[f2bf(v / s)]) * s;
+      const float d = (v - q) / (hcc > 1e-12f ? hcc : 1e-12f);
+      oq[slot] = lane == owner ? q : oq[slot];
+      od[slot] = lane == owner ? d : od[slot];
+#pragma unroll
+      for (int i = (j + 1) / kGptqLanes; i < kGptqSlots; ++i) {
+        const float t = d * hr[i];
+        w[i] = w[i] - t;
+      }
+      if (j + 1 < kGptqMaxCols) {
+#pragma unroll
+        for (int i = (j + 2) / kGptqLanes; i < kGptqSlots; ++i) hr[i] = hn[i];
+      }
+    }
+  }
+  float* orow = out + r * ld + col0;
+  float* drow = deltas + r * ncols;
+#pragma unroll
+  for (int i = 0; i < kGptqSlots; ++i) {
+    const int k = i * kGptqLanes + lane;
+    if (k < ncols) {
+      orow[k] = oq[i];
+      drow[k] = od[i];
+    }
+  }
+}
+
+}  // namespace
+
+int gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int ncols, const float* scale,
+               const float* hinv, int64_t ldh, const uint16_t* qmap, float* out, float* deltas, hipStream_t st) {
+  if (rows < 0 || ld < 0 || col0 < 0 || ldh < 0) return set_error(kErrInvalid, "gptq_block: negative size");
+  if (ncols < 1 || ncols > kGptqMaxCols)
+    return set_error(kErrInvalid, "gptq_block: ncols must be in [1, %d] (got %d)", kGptqMaxCols, ncols);
+  if (col0 + ncols > ld || col0 + ncols > ldh)
+    return set_error(kErrInvalid, "gptq_block: columns %lld..%lld past the row length", (long long)col0,
+                     (long long)(col0 + ncols));
+  if (rows == 0) return kOk;
+  if (!work || !scale || !hinv || !qmap || !out || !deltas) return set_error(kErrInvalid, "gptq_block: null buffer");
+  if (reinterpret_cast<uintptr_t>(qmap) % 16)
+    return set_error(kErrInvalid, "gptq_block: the table must be 16-byte aligned");
+  hipLaunchKernelGGL(gptq_block_kernel, dim3((unsigned)((rows + kGptqRowsPerBlock - 1) / kGptqRowsPerBlock)),
+                     dim3(kGptqThreads), 0, st, work, rows, ld, col0,
+                     ncols, scale, hinv, ldh, qmap, out, deltas);
+  return check_launch("gptq_block");
+}
+
+}  // namespace vqx

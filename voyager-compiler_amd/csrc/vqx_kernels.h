@@ -109,5 +109,7 @@ constexpr int kHistMaxBins = 4096;
 int lcq_histogram(const void* x, int dtype, int64_t n, int64_t block_size, float quant_max, const float* weights,
                   int64_t weights_period, const float* edges, int bins, double* weight, double* total,
                   double* square, hipStream_t st);
+int gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int ncols, const float* scale,
+               const float* hinv, int64_t ldh, const uint16_t* qmap, float* out, float* deltas, hipStream_t st);
 
 }  // namespace vqx

@@ -1,5 +1,5 @@
-"""QuantizationSpec / FakeQuantize API of the hot path, and the learned-codebook
-calibration histogram."""
+"""QuantizationSpec / FakeQuantize API of the hot path, and the calibration
+consumers: the learned-codebook histogram and GPTQ weight compensation."""
 
 from .fake_quantize import (  # noqa: F401
     FakeQuantizeFunction,
@@ -7,6 +7,7 @@ from .fake_quantize import (  # noqa: F401
     MXFakeQuantizeFunction,
     get_quantization_map,
 )
+from .gptq import compensate_weight  # noqa: F401
 from .lcq import HISTOGRAM_BINS, Histogram  # noqa: F401
 from .qspec import QScheme, parse_spec_fields  # noqa: F401
 from .quantizer import QuantizationSpec  # noqa: F401
