@@ -344,6 +344,19 @@ int vqx_gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, in
                    const float* hinv, int64_t ldh, const uint16_t* qmap, float* out, float* deltas,
                    vqx_stream_t stream);
 
+/*
+ * One diagonal block of the factorisation behind GPTQ's inverse-Hessian
+ * factor (src/vc/quantization/gptq.py:32-71, which calls torch.linalg's
+ * cholesky, cholesky_inverse and cholesky).  The host factors the reversed
+ * Hessian blockwise with library GEMMs between these blocks.  a: fp32, row
+ * stride lda, its lower n x n triangle read (n <= 64); li: fp32, row stride
+ * ldl, receives the inverse of the lower Cholesky factor of that block
+ * (zeros above the diagonal); *info is set to 1 if a pivot is not positive
+ * (the matrix is not positive definite) and left alone otherwise.
+ */
+int vqx_chol_inverse_block(const float* a, int64_t lda, int32_t n, float* li, int64_t ldl, int32_t* info,
+                           vqx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

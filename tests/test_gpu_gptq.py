@@ -2,7 +2,9 @@
 column loop bit for bit against the oracle; the whole block loop bit for bit
 where the factor makes the later-column updates exact; and, with a dense
 factor (a library GEMM on each side, summed in different orders), the
-Hessian-weighted error of compensate_weight against the oracle's."""
+Hessian-weighted error of compensate_weight against the oracle's.  The
+inverse-Hessian factor (a blockwise factorisation with HIP leaves) is checked
+against the oracle's and against float64."""
 
 import types
 
@@ -103,3 +105,36 @@ def test_compensate_weight_shrink_and_scale_codebook(vqx):
         return torch.einsum("ij,jk,ik->", e, H.double() / tokens, e).item()
 
     assert err(shrunk) <= 1.05 * err(plain)
+
+
+def hessian_of(seed, n):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(4 * n, n, generator=g) * (torch.rand(n, generator=g) * 2 + 0.1)
+    return X.T @ X, 4 * n
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [40, 64, 128, 200, 1000])
+def test_factor_matches_the_reference_sequence(vqx, n):
+    # the factor is unique: the blockwise inverse factor of the reversed
+    # Hessian must equal cholesky(cholesky_inverse(cholesky(H)), upper=True)
+    H, tokens = hessian_of(n, n)
+    got = vqx.quantization.gptq.hessian_inverse_chol(H.cuda(), tokens, 0.01).cpu()
+    want = R._hessian_inverse_chol(H.double().clone(), tokens, 0.01)
+    assert torch.equal(got, torch.triu(got))
+    err = ((got.double() - want).abs().max() / want.abs().max()).item()
+    assert err < 2e-5, err
+
+
+@pytest.mark.gpu
+def test_factor_escalates_the_damping_like_the_reference(vqx):
+    # one negative diagonal entry: 1% damping leaves H indefinite, 10% does
+    # not; both sides escalate to the same damping
+    d = torch.ones(96)
+    d[5] = -0.05
+    H = torch.diag(d) * 50.0
+    got = vqx.quantization.gptq.hessian_inverse_chol(H.cuda(), 50, 0.01).cpu()
+    want = R._hessian_inverse_chol(H.clone(), 50, 0.01)
+    assert torch.allclose(got, want, rtol=1e-6, atol=0)
+    with pytest.raises(torch.linalg.LinAlgError):
+        vqx.quantization.gptq.hessian_inverse_chol((-torch.eye(70)).cuda(), 1, 0.01)

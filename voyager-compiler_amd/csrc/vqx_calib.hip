@@ -453,6 +453,100 @@ __global__ __launch_bounds__(kGptqThreads) void gptq_block_kernel(
   }
 }
 
+// Cholesky factor and its inverse for a diagonal block of at most 64 rows
+// (the leaves of the blocked factorisation of the reversed Hessian, whose
+// inverse factor is GPTQ's U; gptq.py:32-71 computes U with torch.linalg).
+// Four waves; lane i of wave w holds row i, columns 16 w .. 16 w + 15.
+//  * Factor, right-looking: for column j the owning wave publishes the
+//    updated column in LDS; after the barrier every thread reads the pivot,
+//    forms its row's L[i][j] and updates its own later columns with the
+//    published column.
+//  * L goes to LDS column-major.  Inverse, right-looking: lane c of wave w
+//    holds rows 16 w .. 16 w + 15 of column c of L^-1; for row m the owning
+//    wave finishes it with the pivot and publishes it, and every thread
+//    subtracts column m of L times it from its later rows.
+// One barrier per step (the published values alternate between two
+// buffers).  Rows n .. 63 are padded with the identity, so the block is
+// diag(A, I).  Every load reads a clamped, in-bounds address and selects, so
+// all are issued together.  A pivot that is not positive (or NaN) sets
+// *info to 1.
+constexpr int kCholLeaf = 64;
+constexpr int kCholWaves = 4;
+constexpr int kCholCols = kCholLeaf / kCholWaves;  // columns (then rows) per thread
+
+__global__ __launch_bounds__(kCholLeaf* kCholWaves) void chol_inv_leaf_kernel(const float* __restrict__ a,
+                                                                              int64_t lda, int n,
+                                                                              float* __restrict__ li, int64_t ldl,
+                                                                              int* __restrict__ info) {
+  __shared__ __align__(16) float pub[2][kCholLeaf];
+  __shared__ __align__(16) float lt[kCholLeaf * kCholLeaf];  // lt[m * 64 + q] = L[q][m]
+  __shared__ __align__(16) float rdiag[kCholLeaf];           // 1 / L[m][m]
+  const int lane = threadIdx.x % kCholLeaf;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kCholLeaf);
+  const int k0 = w * kCholCols;
+  const int ic = lane < n ? lane : n - 1;
+  float r[kCholCols];
+#pragma unroll
+  for (int t = 0; t < kCholCols; ++t) {
+    const int k = k0 + t;
+    const float v = a[ic * lda + (k < n ? k : n - 1)];
+    r[t] = (lane < n && k <= lane) ? v : (k == lane ? 1.0f : 0.0f);
+  }
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < kCholLeaf; ++j) {
+    float* cb = pub[j & 1];
+    if (w == j / kCholCols) cb[lane] = r[j % kCholCols];
+    __syncthreads();
+    // the factor needs fp32 accuracy, not correct rounding: the hardware
+    // reciprocal square root keeps the per-column chain short
+    const float djj = cb[j];
+    bad |= !(djj > 0.0f);
+    const float inv = __builtin_amdgcn_rsqf(djj);
+    const float d = djj * inv;
+    if (threadIdx.x == 0) rdiag[j] = inv;
+    const float lij = lane > j ? cb[lane] * inv : (lane == j ? d : 0.0f);
+    if (w == j / kCholCols) r[j % kCholCols] = lij;
+    if (k0 + kCholCols - 1 > j) {
+#pragma unroll
+      for (int t = 0; t < kCholCols; ++t) {
+        const float u = fmaf(-lij, cb[k0 + t] * inv, r[t]);
+        r[t] = k0 + t > j ? u : r[t];
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kCholCols; ++t) lt[(k0 + t) * kCholLeaf + lane] = r[t];
+  __syncthreads();
+  // x[t] = (L^-1)[q][c] for q = k0 + t, c = lane
+  float x[kCholCols];
+#pragma unroll
+  for (int t = 0; t < kCholCols; ++t) x[t] = k0 + t == lane ? 1.0f : 0.0f;
+#pragma unroll
+  for (int m = 0; m < kCholLeaf; ++m) {
+    float* xb = pub[m & 1];
+    if (w == m / kCholCols) {
+      x[m % kCholCols] = x[m % kCholCols] * rdiag[m];
+      xb[lane] = x[m % kCholCols];
+    }
+    __syncthreads();
+    const float xm = xb[lane];
+    if (k0 + kCholCols - 1 > m) {
+#pragma unroll
+      for (int t = 0; t < kCholCols; ++t) {
+        const float u = fmaf(-lt[m * kCholLeaf + k0 + t], xm, x[t]);
+        x[t] = k0 + t > m ? u : x[t];
+      }
+    }
+  }
+  if (lane < n) {
+#pragma unroll
+    for (int t = 0; t < kCholCols; ++t)
+      if (k0 + t < n) li[(k0 + t) * ldl + lane] = x[t];
+  }
+  if (bad && threadIdx.x == 0) info[0] = 1;
+}
+
 }  // namespace
 
 int gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int ncols, const float* scale,
@@ -471,6 +565,15 @@ int gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int nc
                      dim3(kGptqThreads), 0, st, work, rows, ld, col0,
                      ncols, scale, hinv, ldh, qmap, out, deltas);
   return check_launch("gptq_block");
+}
+
+int chol_inverse_block(const float* a, int64_t lda, int n, float* li, int64_t ldl, int* info, hipStream_t st) {
+  if (n < 1 || n > kCholLeaf)
+    return set_error(kErrInvalid, "chol_inverse_block: n must be in [1, %d] (got %d)", kCholLeaf, n);
+  if (lda < n || ldl < n) return set_error(kErrInvalid, "chol_inverse_block: leading dimension below n");
+  if (!a || !li || !info) return set_error(kErrInvalid, "chol_inverse_block: null buffer");
+  hipLaunchKernelGGL(chol_inv_leaf_kernel, dim3(1), dim3(kCholLeaf * kCholWaves), 0, st, a, lda, n, li, ldl, info);
+  return check_launch("chol_inverse_block");
 }
 
 }  // namespace vqx

@@ -296,4 +296,10 @@ int vqx_gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, in
   return gptq_block(work, rows, ld, col0, ncols, scale, hinv, ldh, qmap, out, deltas, (hipStream_t)stream);
 }
 
+int vqx_chol_inverse_block(const float* a, int64_t lda, int32_t n, float* li, int64_t ldl, int32_t* info,
+                           vqx_stream_t stream) {
+  g_err[0] = 0;
+  return chol_inverse_block(a, lda, n, li, ldl, info, (hipStream_t)stream);
+}
+
 }  // extern "C"

@@ -112,4 +112,9 @@ int lcq_histogram(const void* x, int dtype, int64_t n, int64_t block_size, float
 int gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int ncols, const float* scale,
                const float* hinv, int64_t ldh, const uint16_t* qmap, float* out, float* deltas, hipStream_t st);
 
+// Lower Cholesky factor L of the leading n x n block of a (n <= 64, lower
+// triangle read) and its inverse into li (zeros above the diagonal); *info
+// set to 1 on a non-positive pivot.
+int chol_inverse_block(const float* a, int64_t lda, int n, float* li, int64_t ldl, int* info, hipStream_t st);
+
 }  // namespace vqx

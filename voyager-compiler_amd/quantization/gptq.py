@@ -29,30 +29,58 @@ OUTER_COLUMNS = 512
 SHRINK_GRID = (1.0, 0.93, 0.86, 0.79, 0.72)
 
 
+#: Rows of the diagonal blocks the HIP kernel factors and inverts.
+FACTOR_LEAF = 64
+
+
+def _inverse_factor(a, li, info):
+    """li <- inverse of the lower Cholesky factor of the symmetric positive
+    definite ``a`` (its lower triangle; ``a`` is overwritten), blockwise:
+    with a = [[A11, .], [A21, A22]] and L11^-1 from the first half,
+    L21 = A21 L11^-T, the second half factors S = A22 - L21 L21^T, and the
+    inverse's lower-left block is -L22^-1 L21 L11^-1.  The diagonal blocks
+    of at most FACTOR_LEAF rows run in the HIP kernel, everything else is
+    library GEMMs.  ``info`` (int32, device) becomes 1 on a non-positive
+    pivot."""
+    n = a.shape[0]
+    if n <= FACTOR_LEAF:
+        _lib.call("vqx_chol_inverse_block", _lib.ptr(a), a.stride(0), n, _lib.ptr(li), li.stride(0),
+                  _lib.ptr(info), _lib.stream_of(a))
+        return
+    h = (n // 2 + FACTOR_LEAF - 1) // FACTOR_LEAF * FACTOR_LEAF
+    _inverse_factor(a[:h, :h], li[:h, :h], info)
+    l21 = a[h:, :h] @ li[:h, :h].T
+    a[h:, h:].addmm_(l21, l21.T, alpha=-1.0)
+    _inverse_factor(a[h:, h:], li[h:, h:], info)
+    li[h:, :h].addmm_(li[h:, h:], l21 @ li[:h, :h], beta=0.0, alpha=-1.0)
+
+
 def hessian_inverse_chol(hessian, tokens, damping):
     """Upper Cholesky factor U of inv(H / tokens + damping) (U^T U = inv(H)),
     the damping raised tenfold up to 10^4x while H stays indefinite
     (gptq.py:32-71).
 
     The reference factors H, forms inv(H) and factors that.  Here the same
-    (unique) factor comes from one factorisation and one triangular solve:
+    (unique) factor comes from one blockwise factorisation that also inverts:
     with J the order reversal and J H J = L L^T, H = (J L J)(J L J)^T where
-    J L J is upper triangular, so U = (J L J)^-1 = J L^-1 J.  That is one
-    O(n^3) factorisation instead of two plus an inverse, and it never forms
-    inv(H) in fp32 (closer to the fp64 factor than the three-step route).
+    J L J is upper triangular, so U = (J L J)^-1 = J L^-1 J.  inv(H) is never
+    formed in fp32.
     """
-    hessian = hessian / max(tokens, 1)
+    _lib.require_device(hessian, "hessian_inverse_chol")
+    hessian = hessian.float() / max(tokens, 1)
     damp = damping * hessian.diagonal().mean().clamp_min(EPS)
     applied = 0
     for escalation in (1, 10, 100, 1000, 10000):
         hessian.diagonal().add_((escalation - applied) * damp)
         applied = escalation
-        lower, info = torch.linalg.cholesky_ex(hessian.flip(0, 1))
-        if int(info) == 0:
+        work = hessian.flip(0, 1).contiguous()
+        li = torch.zeros_like(work)
+        info = torch.zeros(1, dtype=torch.int32, device=work.device)
+        _inverse_factor(work, li, info)
+        if int(info.item()) == 0 and bool(torch.isfinite(li).all()):
             if escalation > 1:
                 logger.warning("Hessian needed %dx the requested damping to invert", escalation)
-            eye = torch.eye(hessian.shape[0], dtype=hessian.dtype, device=hessian.device)
-            return torch.linalg.solve_triangular(lower, eye, upper=False).flip(0, 1)
+            return li.flip(0, 1)
     raise torch.linalg.LinAlgError("Hessian not positive-definite")
 
 
