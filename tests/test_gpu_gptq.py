@@ -138,3 +138,21 @@ def test_factor_escalates_the_damping_like_the_reference(vqx):
     assert torch.allclose(got, want, rtol=1e-6, atol=0)
     with pytest.raises(torch.linalg.LinAlgError):
         vqx.quantization.gptq.hessian_inverse_chol((-torch.eye(70)).cuda(), 1, 0.01)
+
+
+@pytest.mark.gpu
+def test_blocks_wider_than_the_column_loop(vqx):
+    # 128-column blocks: one scale per block, the loop in two 64-column
+    # pieces; the compensation's error matches the oracle's
+    w, H, tokens = make_problem(6, 96, 256)
+    q = qmap_of("int4")
+    fq = types.SimpleNamespace(qmap=q.cuda(), scale_qmap=None, quant_max=7.0, block_size=128, ch_axis=-1)
+    got = vqx.quantization.compensate_weight(w.cuda(), H.cuda(), tokens, fq, 0.01).cpu()
+    want = R.gptq_compensate_weight(w, H.clone(), tokens, q, 7.0, 128, 0.01)
+
+    def err(o):
+        e = (w - o).double()
+        return torch.einsum("ij,jk,ik->", e, H.double() / tokens, e).item()
+
+    assert torch.isfinite(got).all()
+    assert abs(err(got) - err(want)) <= 0.05 * err(want)

@@ -25,6 +25,9 @@ EPS = 1e-12
 #: Columns whose deltas are subtracted from the later columns in one GEMM.
 OUTER_COLUMNS = 512
 
+#: Columns the HIP column loop walks per launch (its registers hold them).
+LOOP_COLUMNS = 64
+
 #: Scale factors tried below ``amax / quant_max`` (gptq.py:75).
 SHRINK_GRID = (1.0, 0.93, 0.86, 0.79, 0.72)
 
@@ -166,11 +169,10 @@ def compensate_with_factor(weight, hinv, salience, fake_quant, shrink=False):
     span's deltas are subtracted from the columns after it in one GEMM with
     a contraction of ``OUTER_COLUMNS`` (K = 64 GEMMs run at a fifth of the
     rate).  Every block still starts from fully updated columns; only the
-    grouping of the fp32 sums differs."""
+    grouping of the fp32 sums differs.  Blocks wider than ``LOOP_COLUMNS``
+    keep one scale per block and run their column loop in pieces."""
     _lib.require_device(weight, "compensate_with_factor")
     block_size = fake_quant.block_size
-    if block_size > 64:
-        raise ValueError("vqx: the GPTQ column loop takes blocks of at most 64 columns")
     hinv = hinv.to(device=weight.device, dtype=torch.float32).contiguous()
     qmap = Q._table_bf16(fake_quant.qmap.to(weight.device))
     work = weight.float().contiguous().clone()
@@ -183,13 +185,17 @@ def compensate_with_factor(weight, hinv, salience, fake_quant, shrink=False):
         for start in range(outer, stop, block_size):
             end = min(start + block_size, stop)
             scale = block_scale(work[:, start:end], salience[start:end], fake_quant, shrink).float().contiguous()
-            d = torch.empty(R, end - start, dtype=torch.float32, device=work.device)
-            _lib.call("vqx_gptq_block", _lib.ptr(work), R, C, start, end - start, _lib.ptr(scale),
-                      _lib.ptr(hinv), hinv.shape[1], _lib.ptr(qmap), _lib.ptr(out), _lib.ptr(d),
-                      _lib.stream_of(work))
-            deltas[:, start - outer:end - outer] = d
-            if end < stop:
-                work[:, end:stop].sub_(d @ hinv[start:end, end:stop])
+            # the kernel walks at most LOOP_COLUMNS columns; a wider block's
+            # later pieces get the earlier pieces' deltas through the GEMM
+            for lo in range(start, end, LOOP_COLUMNS):
+                hi = min(lo + LOOP_COLUMNS, end)
+                d = torch.empty(R, hi - lo, dtype=torch.float32, device=work.device)
+                _lib.call("vqx_gptq_block", _lib.ptr(work), R, C, lo, hi - lo, _lib.ptr(scale),
+                          _lib.ptr(hinv), hinv.shape[1], _lib.ptr(qmap), _lib.ptr(out), _lib.ptr(d),
+                          _lib.stream_of(work))
+                deltas[:, lo - outer:hi - outer] = d
+                if hi < stop:
+                    work[:, hi:stop].sub_(d @ hinv[lo:hi, hi:stop])
         if stop < C:
             work[:, stop:].addmm_(deltas, hinv[outer:stop, stop:], alpha=-1.0)
     return out
