@@ -3,11 +3,14 @@ MI355X (src/voyager_compiler/quantization/gptq.py:32-270).
 
 The per-block column loop -- quantize a column, charge its rounding error to
 the block's later columns through the inverse-Hessian factor -- is one HIP
-kernel launch per block (``vqx_gptq_block``, one thread per output row with
-the row's block in registers) instead of a few small torch launches per
-column.  The block scale uses the library's ``calculate_mx_qparam`` and
-``vmap``; the factorisation, the permutation and the update of the columns
-after each block are library calls (rocSOLVER, rocBLAS through torch).
+kernel launch per block (``vqx_gptq_block``, each output row on a quad of
+lanes with the row's block in registers) instead of a few small torch
+launches per column.  The inverse-Hessian factor is a blockwise
+factor-and-invert of the reversed Hessian whose 64-row diagonal blocks run in
+a HIP kernel (``vqx_chol_inverse_block``).  The block scale uses the
+library's ``calculate_mx_qparam`` and ``vmap``; the permutation and the GEMMs
+(the factor's off-diagonal blocks, the update of the later columns) are
+torch calls.
 """
 
 import logging
@@ -28,12 +31,11 @@ OUTER_COLUMNS = 512
 #: Columns the HIP column loop walks per launch (its registers hold them).
 LOOP_COLUMNS = 64
 
-#: Scale factors tried below ``amax / quant_max`` (gptq.py:75).
-SHRINK_GRID = (1.0, 0.93, 0.86, 0.79, 0.72)
-
-
 #: Rows of the diagonal blocks the HIP kernel factors and inverts.
 FACTOR_LEAF = 64
+
+#: Scale factors tried below ``amax / quant_max`` (gptq.py:75).
+SHRINK_GRID = (1.0, 0.93, 0.86, 0.79, 0.72)
 
 
 def _inverse_factor(a, li, info):
@@ -46,6 +48,8 @@ def _inverse_factor(a, li, info):
     library GEMMs.  ``info`` (int32, device) becomes 1 on a non-positive
     pivot."""
     n = a.shape[0]
+    if n == 0:
+        return
     if n <= FACTOR_LEAF:
         _lib.call("vqx_chol_inverse_block", _lib.ptr(a), a.stride(0), n, _lib.ptr(li), li.stride(0),
                   _lib.ptr(info), _lib.stream_of(a))
