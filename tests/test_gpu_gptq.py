@@ -184,3 +184,34 @@ def test_compensate_weight_at_the_bench_size(vqx):
     assert torch.isfinite(got).all()
     assert abs(err(got) - err(want)) <= 0.05 * err(want)
     assert err(got) < 0.9 * err(plain)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["int4", "fp4_e2m1"])
+def test_gptq_block_special_values(vqx, dtype):
+    # NaN, +-Inf, signed zeros and huge values in the block: the column loop
+    # propagates them as the reference's torch ops do (NaN compared as a class)
+    g = torch.Generator().manual_seed(21)
+    rows, cols = 70, 64
+    work = torch.randn(rows, cols, generator=g)
+    work[3, 5] = float("nan")
+    work[7, 0] = float("inf")
+    work[9, 63] = float("-inf")
+    work[11, 10] = -0.0
+    work[12, :] = 0.0
+    work[13, 20] = 3e38
+    scale = torch.rand(rows, generator=g) * 0.5 + 0.05
+    A = torch.randn(cols, cols, generator=g) * 0.1 + torch.eye(cols)
+    hinv = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(A @ A.T + 0.1 * torch.eye(cols))),
+                                 upper=True)
+    q = qmap_of(dtype)
+    want_out, want_d = R.gptq_block(work, scale, hinv, q, 0, cols)
+    out = torch.zeros(rows, cols, device="cuda")
+    d = torch.empty(rows, cols, device="cuda")
+    L = vqx._lib
+    wk, sc, hv, qm = work.cuda(), scale.cuda(), hinv.contiguous().cuda(), q.cuda()
+    L.call("vqx_gptq_block", L.ptr(wk), rows, cols, 0, cols, L.ptr(sc), L.ptr(hv), cols, L.ptr(qm),
+           L.ptr(out), L.ptr(d), L.stream_of(wk))
+    for got, want in ((out.cpu(), want_out), (d.cpu(), want_d)):
+        same = (got.view(torch.int32) == want.view(torch.int32)) | (torch.isnan(got) & torch.isnan(want))
+        assert bool(same.all()), int((~same).sum())
