@@ -27,6 +27,25 @@ def test_library_exports_every_declared_symbol(vqx):
     assert lib.vqx_version().decode().startswith("vqx")
 
 
+def declared_arity():
+    """Parameter count of every prototype in include/vqx.h."""
+    text = open(os.path.join(ROOT, "include", "vqx.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(vqx_\w+)\s*\(([^;{]*?)\)\s*;", text, re.S):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_ctypes_signatures_match_the_header(vqx):
+    # the binding passes exactly the arguments each C prototype declares
+    arity = declared_arity()
+    assert sorted(arity) == declared_symbols()
+    for name, (args, _) in vqx._lib._SIGNATURES.items():
+        assert len(args) == arity[name], (name, len(args), arity[name])
+
+
 def test_spec_parsing(vqx):
     from voyager_compiler_amd.quantization import QScheme, QuantizationSpec, parse_spec_fields
 

@@ -327,9 +327,10 @@ int lcq_histogram(const void* x, int dtype, int64_t n, int64_t block_size, float
 //   deltas[r, j] = d
 //   w[r, c + k] -= d * hinv[c, c + k]   for the block's later columns
 // every operation rounded to fp32 as torch performs it (the product and the
-// difference rounded separately, no fused multiply-add).  One thread per
-// row holds the row's block in registers; hinv is the same for every row
-// (scalar loads).  The block's columns of w are left as they were.
+// difference rounded separately, no fused multiply-add).  Each row's block
+// sits in the registers of a quad of lanes; the table and the block's corner
+// of hinv are staged in LDS (see gptq_block_kernel).  The block's columns of
+// w are left as they were.
 // ---------------------------------------------------------------------------
 namespace vqx {
 namespace {
