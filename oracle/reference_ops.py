@@ -196,14 +196,51 @@ def codebook_decode_rows(codes, cb):
     return torch.gather(cbb, 1, codes.long())
 
 
-def linear_mx(x, weight, bias=None, weight_scale=None, block_size=None, weight_code=None):
-    """src/vc/ops/quantized.py:295-331 (dense, "kc" layout)."""
-    w = weight
-    if weight_code is not None:
-        w = weight_code[weight.to(torch.long)].to(weight.dtype)
-    if weight_scale is not None:
-        w = w * expand(weight_scale, weight.shape, block_size)
+def _decode_mx(t, code, scale, block_size):
+    """The operand decode of linear_mx / matmul_mx / conv2d_mx
+    (src/vc/ops/quantized.py:263-272, 313-326, 388-398): code lookup by the
+    integer value in t's dtype, then the product with the expanded scales."""
+    if code is not None:
+        t = code[t.to(torch.long)].to(t.dtype)
+    if scale is not None:
+        t = t * expand(scale, t.shape, block_size)
+    return t
+
+
+def linear_mx(x, weight, bias=None, weight_scale=None, block_size=None, weight_code=None, input_scale=None,
+              input_code=None, weight_layout="kc"):
+    """src/vc/ops/quantized.py:295-331 (the dense half).  "ck" is the layout
+    twin (ops/layout.py:184-198): the weight's last two dims swapped."""
+    x = _decode_mx(x, input_code, input_scale, block_size)
+    w = _decode_mx(weight, weight_code, weight_scale, block_size)
+    if weight_layout == "ck":
+        w = w.transpose(-2, -1)
     return torch.nn.functional.linear(x, w, bias)
+
+
+def matmul_mx(a, other, weight_scale=None, block_size=None, weight_code=None, input_scale=None, input_code=None,
+              weight_layout="ck"):
+    """src/vc/ops/quantized.py:371-406 (the dense half); "kc" is the layout
+    twin with the right matrix's last two dims swapped."""
+    a = _decode_mx(a, input_code, input_scale, block_size)
+    b = _decode_mx(other, weight_code, weight_scale, block_size)
+    if weight_layout == "kc":
+        b = b.transpose(-2, -1)
+    return torch.matmul(a, b)
+
+
+def conv2d_mx(x, weight, bias=None, stride=1, padding=0, dilation=1, groups=1, input_scale=None,
+              weight_scale=None, block_size=None, input_code=None, weight_code=None, layout="nchw"):
+    """src/vc/ops/quantized.py:239-284; "nhwc" is the layout twin
+    (ops/layout.py:152-170): NHWC activations, HWIO weight (OIHW when
+    grouped), NHWC result."""
+    x = _decode_mx(x, input_code, input_scale, block_size)
+    w = _decode_mx(weight, weight_code, weight_scale, block_size)
+    if layout == "nhwc":
+        x = x.permute(0, 3, 1, 2)
+        w = w.permute(3, 2, 0, 1) if groups == 1 else w
+    out = torch.nn.functional.conv2d(x, w, bias, stride, padding, dilation, groups)
+    return out.permute(0, 2, 3, 1) if layout == "nhwc" else out
 
 
 # ---------------------------------------------------------------------------

@@ -18,6 +18,7 @@ from typing import List, Optional, Tuple
 
 import torch
 from torch.library import Library
+from torch.nn.modules.utils import _pair
 
 from .. import _lib
 from ..formats import Format, parse_format
@@ -45,6 +46,12 @@ _SCHEMAS = {
         "Tensor? weight_scale=None, int? block_size=None, Tensor? input_code=None, "
         "Tensor? weight_code=None, Tensor? A_data=None, Tensor? A_indices=None, "
         'Tensor? A_indptr=None, str weight_layout="ck") -> Tensor'),
+    "conv2d_mx": (
+        "conv2d_mx(Tensor input, Tensor weight, Tensor? bias=None, "
+        "SymInt[2] stride=1, SymInt[2] padding=0, SymInt[2] dilation=1, "
+        "SymInt groups=1, *, Tensor? input_scale=None, Tensor? weight_scale=None, "
+        "int? block_size=None, Tensor? input_code=None, "
+        'Tensor? weight_code=None, str layout="nchw") -> Tensor'),
     "calculate_mx_qparam": (
         "calculate_mx_qparam(Tensor self, SymInt[] axes, int block_size, "
         "float quant_max, bool force_scale_power_of_two=False, "
@@ -94,6 +101,42 @@ for _s in _SCHEMAS.values():
 
 def _impl(name):
     return torch.library.impl(quantized_ops_lib, name, "CUDA")
+
+
+# ---------------------------------------------------------------------------
+# Hardware-layout twins of aten ops (ops/layout.py:104-200): the same name and
+# schema as the aten op, with operands stored in the layout the reference's
+# layout passes choose.  linear / matmul take the weight (right matrix) with
+# its last two dims swapped; conv2d takes NHWC activations and an HWIO weight
+# (a grouped conv keeps OIHW) and returns NHWC.  They only permute around the
+# aten op, so they are registered for every backend, as the reference's are.
+# ---------------------------------------------------------------------------
+_NHWC_TO_NCHW, _NCHW_TO_NHWC, _HWIO_TO_OIHW = (0, 3, 1, 2), (0, 2, 3, 1), (3, 2, 0, 1)
+for _op in (torch.ops.aten.linear.default, torch.ops.aten.matmul.default, torch.ops.aten.conv2d.default):
+    quantized_ops_lib.define(str(_op._schema).split("::", 1)[1])
+
+
+def _swapped(t):
+    # contiguous: batched bf16 products of transposed views are avoided
+    return t.transpose(-2, -1).contiguous()
+
+
+@torch.library.impl(quantized_ops_lib, "linear", "CompositeExplicitAutograd")
+def linear_twin(input, weight, bias=None):
+    return torch.ops.aten.linear(input, _swapped(weight), bias)
+
+
+@torch.library.impl(quantized_ops_lib, "matmul", "CompositeExplicitAutograd")
+def matmul_twin(self, other):
+    return torch.ops.aten.matmul(self, _swapped(other))
+
+
+@torch.library.impl(quantized_ops_lib, "conv2d", "CompositeExplicitAutograd")
+def conv2d_twin(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
+    w = weight.permute(_HWIO_TO_OIHW) if groups == 1 else weight
+    out = torch.ops.aten.conv2d(input.permute(_NHWC_TO_NCHW), w, bias, _pair(stride), _pair(padding),
+                                _pair(dilation), groups)
+    return out.permute(_NCHW_TO_NHWC)
 
 
 # ---------------------------------------------------------------------------
@@ -420,9 +463,31 @@ def _code_lut(code: torch.Tensor) -> torch.Tensor:
     return lut
 
 
+_BF16_EXACT = {}
+
+
+def _bf16_exact(code: torch.Tensor) -> bool:
+    """Whether every code value survives a round trip through bf16 (the
+    65536-entry table the lookup uses holds bf16 values)."""
+    key = (code.data_ptr(), code._version, code.numel(), code.dtype)
+    hit = _BF16_EXACT.get(key)
+    if hit is not None and hit[0]() is code:
+        return hit[1]
+    ok = code.dtype == torch.bfloat16 or bool(torch.equal(code.to(torch.bfloat16).to(code.dtype), code))
+    _BF16_EXACT[key] = (weakref.ref(code), ok)
+    return ok
+
+
 def _decode_operand(t, code, scale, block_size):
     if code is None and scale is None:
         return t
+    if code is not None and t.dtype != torch.bfloat16 and not _bf16_exact(code):
+        # code values finer than bf16 in a wider operand: the reference's
+        # gather by integer value (quantized.py:313-315), then the scales
+        t = code.to(t.device)[t.to(torch.long)].to(t.dtype)
+        code = None
+        if scale is None:
+            return t
     if code is not None:
         lut = _code_lut(code.to(t.device))
     else:
@@ -438,13 +503,14 @@ def linear_mx(input, weight, bias=None, *, input_scale=None, weight_scale=None, 
               weight_layout="kc"):
     assert weight_layout in ("kc", "ck"), weight_layout
     _lib.require_device(input, "linear_mx")
-    if weight_layout != "kc":
-        raise NotImplementedError("vqx: the 'ck' hardware weight layout is not implemented")
     x = _decode_operand(input, input_code, input_scale, block_size)
     w = _decode_operand(weight, weight_code, weight_scale, block_size)
     if weight_code is not None:
         w = w.to(weight.dtype)
-    dense = torch.nn.functional.linear(x, w, bias)
+    if weight_layout == "kc":
+        dense = torch.nn.functional.linear(x, w, bias)
+    else:
+        dense = torch.ops.quantized_ops.linear(x, w, bias)
     if A_data is None:
         return dense
     return _spmm(A_data, A_indices, A_indptr, weight, weight_scale, weight_code, block_size, weight_layout,
@@ -456,15 +522,33 @@ def matmul_mx(self, other, *, input_scale=None, weight_scale=None, block_size=No
               weight_code=None, A_data=None, A_indices=None, A_indptr=None, weight_layout="ck"):
     assert weight_layout in ("kc", "ck"), weight_layout
     _lib.require_device(self, "matmul_mx")
-    if weight_layout != "ck":
-        raise NotImplementedError("vqx: the 'kc' hardware layout for matmul is not implemented")
     a = _decode_operand(self, input_code, input_scale, block_size)
     b = _decode_operand(other, weight_code, weight_scale, block_size)
-    dense = torch.matmul(a, b.contiguous())
+    if weight_layout == "ck":
+        dense = torch.matmul(a, b.contiguous())
+    else:
+        dense = torch.ops.quantized_ops.matmul(a, b)
     if A_data is None:
         return dense
     return _spmm(A_data, A_indices, A_indptr, other, weight_scale, weight_code, block_size, weight_layout,
                  addend=dense)
+
+
+@_impl("conv2d_mx")
+def conv2d_mx(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1, *, input_scale=None,
+              weight_scale=None, block_size=None, input_code=None, weight_code=None, layout="nchw"):
+    """quantized.py:230-284: activations and weight decoded on the GPU as
+    linear_mx decodes them (code lookup, then the product with the expanded
+    block scales), then the convolution (MIOpen through aten), or its NHWC
+    twin for ``layout="nhwc"`` (NHWC activations, HWIO weight)."""
+    assert layout in ("nchw", "nhwc"), layout
+    _lib.require_device(input, "conv2d_mx")
+    x = _decode_operand(input, input_code, input_scale, block_size)
+    w = _decode_operand(weight, weight_code, weight_scale, block_size)
+    stride, padding, dilation = _pair(stride), _pair(padding), _pair(dilation)
+    if layout == "nhwc":
+        return torch.ops.quantized_ops.conv2d(x, w, bias, stride, padding, dilation, groups)
+    return torch.ops.aten.conv2d(x, w, bias, stride, padding, dilation, groups)
 
 
 # ---------------------------------------------------------------------------
@@ -851,14 +935,36 @@ def _(input, qmap, axes, block_size, quant_max, force_scale_power_of_two=False, 
     return input.new_empty(shape), torch.empty_like(input, memory_format=torch.contiguous_format)
 
 
+def _decoded_fake(t, scale):
+    return t if scale is None else t.to(torch.promote_types(t.dtype, scale.dtype))
+
+
 @torch.library.register_fake("quantized_ops::linear_mx")
 def _(input, weight, bias=None, **kwargs):
-    return torch.nn.functional.linear(input, weight, bias)
+    x = _decoded_fake(input, kwargs.get("input_scale"))
+    w = _decoded_fake(weight, kwargs.get("weight_scale"))
+    if kwargs.get("weight_layout", "kc") == "ck":
+        return torch.ops.quantized_ops.linear(x, w, bias)
+    return torch.nn.functional.linear(x, w, bias)
 
 
 @torch.library.register_fake("quantized_ops::matmul_mx")
 def _(self, other, **kwargs):
-    return torch.matmul(self, other)
+    a = _decoded_fake(self, kwargs.get("input_scale"))
+    b = _decoded_fake(other, kwargs.get("weight_scale"))
+    if kwargs.get("weight_layout", "ck") == "kc":
+        return torch.ops.quantized_ops.matmul(a, b)
+    return torch.matmul(a, b)
+
+
+@torch.library.register_fake("quantized_ops::conv2d_mx")
+def _(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1, **kwargs):
+    x = _decoded_fake(input, kwargs.get("input_scale"))
+    w = _decoded_fake(weight, kwargs.get("weight_scale"))
+    args = (bias, _pair(stride), _pair(padding), _pair(dilation), groups)
+    if kwargs.get("layout", "nchw") == "nhwc":
+        return torch.ops.quantized_ops.conv2d(x, w, *args)
+    return torch.ops.aten.conv2d(x, w, *args)
 
 
 def _csr_fake(input, max_pct):
