@@ -116,6 +116,21 @@ def test_fake_impls_trace(vqx):
         assert s.shape == (4, 2) and q.shape == (4, 64)
         sc, codes = torch.ops.quantized_ops.quantize_mx_packed(x, "fp4_e2m1", -1, 32)
         assert sc.shape == (4, 2) and sc.dtype == torch.uint8 and codes.numel() == 128
+        # both weight layouts of the GEMM ops, both activation layouts of conv2d_mx
+        w = torch.empty(48, 64, dtype=torch.bfloat16)
+        ws = torch.empty(48, 2, dtype=torch.bfloat16)
+        assert torch.ops.quantized_ops.linear_mx(x, w, weight_scale=ws, block_size=32).shape == (4, 48)
+        assert torch.ops.quantized_ops.linear_mx(x, w.T, weight_scale=ws.T, block_size=32,
+                                                 weight_layout="ck").shape == (4, 48)
+        assert torch.ops.quantized_ops.matmul_mx(x, w.T).shape == (4, 48)
+        assert torch.ops.quantized_ops.matmul_mx(x, w, weight_layout="kc").shape == (4, 48)
+        img = torch.empty(2, 8, 10, 12, dtype=torch.bfloat16)
+        k = torch.empty(6, 8, 3, 3, dtype=torch.bfloat16)
+        out = torch.ops.quantized_ops.conv2d_mx(img, k, None, [2, 2], [1, 1])
+        assert out.shape == (2, 6, 5, 6)
+        out = torch.ops.quantized_ops.conv2d_mx(img.permute(0, 2, 3, 1), k.permute(2, 3, 1, 0), None, [2, 2],
+                                                [1, 1], layout="nhwc")
+        assert out.shape == (2, 5, 6, 6)
 
 
 def test_fake_quantize_module_state_on_cpu(vqx):
