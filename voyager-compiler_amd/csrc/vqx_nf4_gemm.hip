@@ -97,6 +97,43 @@ __device__ __forceinline__ void decode8(uint32_t w, float s, const LevelBytes& l
   }
 }
 
+// The 16 values bf16(level[c] * s) of one scale block, as high and low byte
+// tables in the LevelBytes layout: pair p[i] holds entries 2i (low half) and
+// 2i + 1; the high bytes of entries 4j .. 4j + 3 are bytes 1, 3 of p[2j] and
+// of p[2j + 1], the low bytes bytes 0, 2.
+__device__ __forceinline__ LevelBytes scaled_levels(const float (&lv)[16], float s) {
+  uint32_t p[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p[i] = pack_bf16x2(lv[2 * i] * s, lv[2 * i + 1] * s);
+  LevelBytes t;
+  t.h0 = __builtin_amdgcn_perm(p[1], p[0], 0x07050301u);
+  t.h1 = __builtin_amdgcn_perm(p[3], p[2], 0x07050301u);
+  t.h2 = __builtin_amdgcn_perm(p[5], p[4], 0x07050301u);
+  t.h3 = __builtin_amdgcn_perm(p[7], p[6], 0x07050301u);
+  t.l0 = __builtin_amdgcn_perm(p[1], p[0], 0x06040200u);
+  t.l1 = __builtin_amdgcn_perm(p[3], p[2], 0x06040200u);
+  t.l2 = __builtin_amdgcn_perm(p[5], p[4], 0x06040200u);
+  t.l3 = __builtin_amdgcn_perm(p[7], p[6], 0x06040200u);
+  return t;
+}
+
+// decode8 with the scale already applied (tables from scaled_levels): the
+// byte lookups give the final bf16 bytes, which four pairs of v_perm
+// interleave into the same k-ascending bf16 pairs decode8 returns.
+__device__ __forceinline__ void decode8_scaled(uint32_t w, const LevelBytes& tb, uint32_t (&out)[4]) {
+  uint32_t he, le, ho, lo;
+  lookup4(w & 0x07070707u, byte_sign_mask(w << 4), tb, he, le);    // codes 0, 2, 4, 6
+  lookup4((w >> 4) & 0x07070707u, byte_sign_mask(w), tb, ho, lo);  // codes 1, 3, 5, 7
+  const uint32_t e01 = __builtin_amdgcn_perm(he, le, 0x05010400u);  // values of codes 0, 2
+  const uint32_t o01 = __builtin_amdgcn_perm(ho, lo, 0x05010400u);  // codes 1, 3
+  const uint32_t e23 = __builtin_amdgcn_perm(he, le, 0x07030602u);  // codes 4, 6
+  const uint32_t o23 = __builtin_amdgcn_perm(ho, lo, 0x07030602u);  // codes 5, 7
+  out[0] = __builtin_amdgcn_perm(o01, e01, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(o01, e01, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(o23, e23, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(o23, e23, 0x07060302u);
+}
+
 // LDS-only workgroup barrier: waits for this wave's LDS traffic, not for the
 // global loads still in flight.
 __device__ __forceinline__ void lds_barrier() {
@@ -393,18 +430,9 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uin
   const int kb = K / 64;
   const int steps = (K + 127) / 128;
   const int s0 = steps * wave / kSkinnyWaves, s1 = steps * (wave + 1) / kSkinnyWaves;
-  LevelBytes lb;
-  {
-    uint32_t hb[4] = {0, 0, 0, 0}, lbv[4] = {0, 0, 0, 0};
+  float lvf[16];  // the levels as fp32 (uniform)
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      uint32_t v = levels[c];
-      hb[c >> 2] |= ((v >> 8) & 0xFFu) << (8 * (c & 3));
-      lbv[c >> 2] |= (v & 0xFFu) << (8 * (c & 3));
-    }
-    lb.h0 = hb[0]; lb.h1 = hb[1]; lb.h2 = hb[2]; lb.h3 = hb[3];
-    lb.l0 = lbv[0]; lb.l1 = lbv[1]; lb.l2 = lbv[2]; lb.l3 = lbv[3];
-  }
+  for (int c = 0; c < 16; ++c) lvf[c] = u2f((uint32_t)levels[c] << 16);
   const uint8_t* wrow = codes + (size_t)nn * (K / 2);
   const float* srow = scale + (size_t)nn * kb;
   const uint16_t* arow = A + (size_t)mm * K;
@@ -424,10 +452,12 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uin
       a[c] = *reinterpret_cast<const u32x4*>(arow + kk + 8 * c);
       if (!kok) a[c] = u32x4{0u, 0u, 0u, 0u};
     }
+    // the lane's 32 codes share one scale block: scale the 16 levels once
+    const LevelBytes tb = scaled_levels(lvf, sc);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       uint32_t o[4];
-      decode8(w[c], sc, lb, o);
+      decode8_scaled(w[c], tb, o);
       const u32x4 b = {o[0], o[1], o[2], o[3]};
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[c]), __builtin_bit_cast(bf16x8, b),
                                                     acc, 0, 0, 0);
