@@ -163,6 +163,9 @@ __global__ __launch_bounds__(kHistThreads) void lcq_hist_kernel(const void* __re
   __syncthreads();
   const bool tight = s_loose == 0;
   const HistLds h{s_w, s_t, s_s, s_e};
+  // the vectorised unit-weight path counts in the first half of s_w's bytes
+  uint32_t* const s_n = reinterpret_cast<uint32_t*>(s_w);
+  constexpr bool kCounts = VEC && !W;
   const float eps = 1e-12f;
   if constexpr (VEC) {
     constexpr int U = 4;  // groups of 256 elements per wave in flight
@@ -221,7 +224,16 @@ __global__ __launch_bounds__(kHistThreads) void lcq_hist_kernel(const void* __re
             const float vj = ok[u] ? v[u][j] : 0.0f;
             const int c = T ? bin_tight(vj, s_e, bins, e0, elast, inv_step)
                             : min(max(edges_at_or_below(vj, s_e, bins, e0, elast, inv_step, false) - 1, 0), bins - 1);
-            add_moments(h, c, vj, ok[u] ? w[j] : 0.0f);
+            if constexpr (W) {
+              add_moments(h, c, vj, ok[u] ? w[j] : 0.0f);
+            } else if (ok[u]) {
+              // unit weights: the weight sum is a count (exact in fp64 at
+              // the flush), one 32-bit LDS atomic instead of an fp64 one
+              const double vd = (double)vj;
+              atomicAdd(&s_n[c], 1u);
+              atomicAdd(&h.t[c], vd);
+              atomicAdd(&h.s[c], vd * vd);
+            }
           }
         }
       }
@@ -257,7 +269,7 @@ __global__ __launch_bounds__(kHistThreads) void lcq_hist_kernel(const void* __re
   const int rot = (int)(((int64_t)blockIdx.x * 521) % bins);
   for (int jj = threadIdx.x; jj < bins; jj += kHistThreads) {
     const int j = jj + rot < bins ? jj + rot : jj + rot - bins;
-    const double a = s_w[j], t = s_t[j], q = s_s[j];
+    const double a = kCounts ? (double)s_n[j] : s_w[j], t = s_t[j], q = s_s[j];
     if (a != 0.0 || t != 0.0 || q != 0.0) {
       atomicAdd(gw + j, a);
       atomicAdd(gt + j, t);
