@@ -215,3 +215,18 @@ def test_gptq_block_special_values(vqx, dtype):
     for got, want in ((out.cpu(), want_out), (d.cpu(), want_d)):
         same = (got.view(torch.int32) == want.view(torch.int32)) | (torch.isnan(got) & torch.isnan(want))
         assert bool(same.all()), int((~same).sum())
+
+
+@pytest.mark.gpu
+def test_compensate_weight_with_a_fake_quantize_module(vqx):
+    # the weight's FakeQuantize module names the grid; one that has not run a
+    # forward yet still has its tables built for the compensation
+    w, H, tokens = make_problem(8, 64, 128)
+    spec = vqx.quantization.QuantizationSpec.from_str("int4,qs=microscaling,bs=64,ax=-1")
+    module = spec.make_fake_quantize()
+    got = vqx.quantization.compensate_weight(w.cuda(), H.cuda(), tokens, module, 0.01).cpu()
+    q = qmap_of("int4")
+    fq = types.SimpleNamespace(qmap=q.cuda(), scale_qmap=None, quant_max=7.0, block_size=64, ch_axis=-1)
+    want = vqx.quantization.compensate_weight(w.cuda(), H.cuda(), tokens, fq, 0.01).cpu()
+    assert module.qmap.numel() == 65536 and module.quant_max == 7.0
+    assert torch.equal(got, want)

@@ -137,6 +137,9 @@ def compensate_weight(weight, hessian, tokens, fake_quant, damping, act_order=Tr
     grid of ``fake_quant`` (its qmap, scale_qmap, quant_max, block_size and
     ch_axis), in the original column order (gptq.py:184-270)."""
     _lib.require_device(weight, "compensate_weight")
+    ensure = getattr(fake_quant, "_ensure_tables", None)
+    if ensure is not None:  # this library's FakeQuantize builds its tables on first use
+        ensure(weight.device)
     block_size = fake_quant.block_size
     axis = fake_quant.ch_axis
     axis = axis[0] if isinstance(axis, (tuple, list)) else axis
