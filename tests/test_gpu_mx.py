@@ -238,3 +238,43 @@ def test_nf4_fake_quant_module(vqx):
     qmap = R.table_tensor(F.quantization_table("nf4"))
     ws, wy = R.mx_fake_quantize(x, qmap, [-1], 64, 1.0, False)
     assert_bitexact(y.cpu(), wy, "nf4 fake-quant")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("spec", [
+    "nf4_6,qs=microscaling,bs=64,ax=-1,scale=fp8_e5m3",
+    "int6,qs=microscaling,bs=64,ax=-1,scale=fp8_e5m3",
+    "int6,qs=microscaling,bs=64,ax=-2,scale=fp8_e5m3",
+    "nf4_6,qs=microscaling,bs=64,ax=-2,scale=fp8_e5m3,othr=6.0",
+    "nf4_6,qs=microscaling,bs=64,ax=-1,scale=fp8_e5m3,opct=0.01",
+])
+def test_llama_qconfig_specs(vqx, spec):
+    # the spec strings the reference's LLaMA test quantizes with
+    # (test/test_codegen.py:126-152): scale codebook fp8_e5m3, blocks along
+    # the last or the second-to-last axis, outliers by threshold or by share
+    # (topk threshold, masked before and restored after the fake-quant,
+    # fake_quantize.py:373-432)
+    from voyager_compiler_amd.quantization import QuantizationSpec
+
+    fq = QuantizationSpec.from_str(spec).make_fake_quantize("cuda").cuda()
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(2, 128, 256, generator=g)
+    x = torch.where(torch.rand(x.shape, generator=g) < 0.01, x * 20, x).to(torch.bfloat16)
+    y = fq(x.cuda()).cpu()
+    dtype = spec.split(",")[0]
+    axis = -2 if "ax=-2" in spec else -1
+    qmax = 31.0
+    xm, skip = x, None
+    if "othr" in spec or "opct" in spec:
+        if "othr" in spec:
+            skip = x.abs() >= 6.0
+        else:
+            flat = x.abs().flatten()
+            k = max(1, math.ceil(0.01 * flat.numel()))
+            skip = x.abs() >= torch.topk(flat, k, largest=True, sorted=False).values.min()
+        xm = x.masked_fill(skip, 0.0)
+    ws, wy = R.mx_fake_quantize(xm, oracle_qmap(dtype), [axis], 64, qmax, False, oracle_qmap("fp8_e5m3"))
+    if skip is not None:
+        wy = torch.where(skip, x, wy)
+        assert bool(skip.any())
+    assert_bitexact(y, wy, spec)
