@@ -331,18 +331,23 @@ int vqx_lcq_histogram(const void* x, int32_t x_dtype, int64_t n, int64_t block_s
  * (src/vc/quantization/gptq.py:241-262).  work, out: fp32 [rows, ld] row-major;
  * the block is columns col0 .. col0 + ncols - 1 (ncols <= 64).  For each row r
  * and block column j in order, c = col0 + j:
- *   q = float(qmap[bf16(w[r, c] / scale[r])]) * scale[r];  out[r, c] = q
- *   d = (w[r, c] - q) / max(hinv[c, c], 1e-12);            deltas[r, j] = d
+ *   q = float(qmap[bf16(w[r, c] / s[r])]) * s[r];  out[r, c] = q
+ *   d = (w[r, c] - q) / max(hinv[c, c], 1e-12);    deltas[r, j] = d
  *   w[r, c + k] -= d * hinv[c, c + k] for the block's later columns (on a
  *   private copy: work is not written)
  * each operation rounded to fp32 as torch performs it (no fused multiply-add).
- * scale: fp32 [rows]; hinv: fp32 upper Cholesky factor of the inverse
- * Hessian, row stride ldh; qmap: 65536 bf16 patterns, 16-byte aligned;
- * deltas: fp32 [rows, ncols].
+ * s[r] = scale[r] when scale is given (fp32 [rows]); with scale NULL the
+ * kernel forms block_scale's unshrunk scale from the block's current weights
+ * (gptq.py:103-113 through calculate_mx_qparam, quantized.py:491-498):
+ * amax over the block (NaN propagates) / quant_max, through scale_qmap
+ * (65536 bf16 patterns) when given, 1 where not positive, at least 1e-12.
+ * hinv: fp32 upper Cholesky factor of the inverse Hessian, row stride ldh;
+ * qmap: 65536 bf16 patterns, 16-byte aligned; deltas: fp32, row stride
+ * ldd >= ncols.
  */
 int vqx_gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int32_t ncols, const float* scale,
-                   const float* hinv, int64_t ldh, const uint16_t* qmap, float* out, float* deltas,
-                   vqx_stream_t stream);
+                   float quant_max, const uint16_t* scale_qmap, const float* hinv, int64_t ldh,
+                   const uint16_t* qmap, float* out, float* deltas, int64_t ldd, vqx_stream_t stream);
 
 /*
  * One diagonal block of the factorisation behind GPTQ's inverse-Hessian

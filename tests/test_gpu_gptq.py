@@ -35,8 +35,8 @@ def test_gptq_block_matches_oracle(vqx, dtype, rows, cols, start, end):
     d = torch.empty(rows, end - start, device="cuda")
     L = vqx._lib
     wk, sc, hv, qm = work.cuda(), scale.cuda(), hinv.contiguous().cuda(), q.cuda()
-    L.call("vqx_gptq_block", L.ptr(wk), rows, cols, start, end - start, L.ptr(sc), L.ptr(hv), cols, L.ptr(qm),
-           L.ptr(out), L.ptr(d), L.stream_of(wk))
+    L.call("vqx_gptq_block", L.ptr(wk), rows, cols, start, end - start, L.ptr(sc), 0.0, None, L.ptr(hv), cols,
+           L.ptr(qm), L.ptr(out), L.ptr(d), end - start, L.stream_of(wk))
     assert torch.equal(out[:, start:end].cpu(), want_out)
     assert torch.equal(d.cpu(), want_d)
     assert torch.equal(wk.cpu(), work)       # the block's columns of work are left as they were
@@ -210,8 +210,8 @@ def test_gptq_block_special_values(vqx, dtype):
     d = torch.empty(rows, cols, device="cuda")
     L = vqx._lib
     wk, sc, hv, qm = work.cuda(), scale.cuda(), hinv.contiguous().cuda(), q.cuda()
-    L.call("vqx_gptq_block", L.ptr(wk), rows, cols, 0, cols, L.ptr(sc), L.ptr(hv), cols, L.ptr(qm),
-           L.ptr(out), L.ptr(d), L.stream_of(wk))
+    L.call("vqx_gptq_block", L.ptr(wk), rows, cols, 0, cols, L.ptr(sc), 0.0, None, L.ptr(hv), cols, L.ptr(qm),
+           L.ptr(out), L.ptr(d), cols, L.stream_of(wk))
     for got, want in ((out.cpu(), want_out), (d.cpu(), want_d)):
         same = (got.view(torch.int32) == want.view(torch.int32)) | (torch.isnan(got) & torch.isnan(want))
         assert bool(same.all()), int((~same).sum())
@@ -230,3 +230,36 @@ def test_compensate_weight_with_a_fake_quantize_module(vqx):
     want = vqx.quantization.compensate_weight(w.cuda(), H.cuda(), tokens, fq, 0.01).cpu()
     assert module.qmap.numel() == 65536 and module.quant_max == 7.0
     assert torch.equal(got, want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,qmax", [("int4", 7.0), ("nf4", 1.0)])
+@pytest.mark.parametrize("scale_dtype", [None, "fp8_e5m3"])
+@pytest.mark.parametrize("rows,cols,start,end", [(300, 128, 64, 128), (70, 64, 0, 50)])
+def test_gptq_block_forms_the_block_scale(vqx, dtype, qmax, scale_dtype, rows, cols, start, end):
+    # scale NULL: the kernel forms block_scale's plain scale from the block
+    # (calculate_mx_qparam of the block, clamped at 1e-12), NaN and zero rows
+    # included; deltas written at a row stride wider than the block
+    g = torch.Generator().manual_seed(rows + end)
+    work = torch.randn(rows, cols, generator=g) * 0.3
+    work[1, start + 3] = float("nan")
+    work[2, start:end] = 0.0
+    A = torch.randn(cols, cols, generator=g) * 0.1 + torch.eye(cols)
+    hinv = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(A @ A.T + 0.1 * torch.eye(cols))),
+                                 upper=True)
+    q = qmap_of(dtype)
+    sq = None if scale_dtype is None else qmap_of(scale_dtype)
+    scale = R.calculate_mx_qparam(work[:, start:end], [-1], end - start, qmax, False, sq).reshape(-1).clamp_min(1e-12)
+    want_out, want_d = R.gptq_block(work, scale, hinv, q, start, end)
+    n, ldd = end - start, end - start + 9
+    out = torch.zeros(rows, cols, device="cuda")
+    dbuf = torch.full((rows, ldd), 7.0, device="cuda")
+    L = vqx._lib
+    wk, hv, qm = work.cuda(), hinv.contiguous().cuda(), q.cuda()
+    sqc = None if sq is None else sq.cuda()
+    L.call("vqx_gptq_block", L.ptr(wk), rows, cols, start, n, None, qmax, L.ptr(sqc), L.ptr(hv), cols, L.ptr(qm),
+           L.ptr(out), L.ptr(dbuf), ldd, L.stream_of(wk))
+    for got, want in ((out[:, start:end].cpu(), want_out), (dbuf[:, :n].cpu(), want_d)):
+        same = (got.view(torch.int32) == want.view(torch.int32)) | (torch.isnan(got) & torch.isnan(want))
+        assert bool(same.all()), int((~same).sum())
+    assert bool((dbuf[:, n:] == 7.0).all())  # the stride's gap is not written

@@ -379,8 +379,9 @@ __device__ __forceinline__ float quad_bcast(float v, int o) {
 // Multiply and subtract round separately, as the reference's two torch ops.
 __global__ __launch_bounds__(kGptqThreads) void gptq_block_kernel(
     const float* __restrict__ work, int64_t rows, int64_t ld, int64_t col0, int ncols,
-    const float* __restrict__ scale, const float* __restrict__ hinv, int64_t ldh,
-    const uint16_t* __restrict__ qmap, float* __restrict__ out, float* __restrict__ deltas) {
+    const float* __restrict__ scale, float quant_max, const uint16_t* __restrict__ scale_qmap,
+    const float* __restrict__ hinv, int64_t ldh, const uint16_t* __restrict__ qmap, float* __restrict__ out,
+    float* __restrict__ deltas, int64_t ldd) {
 #pragma clang fp contract(off)
   __shared__ __align__(16) uint16_t lut[65536];
   __shared__ __align__(16) float hq[kGptqMaxCols * kGptqMaxCols];  // [j][lane][slot] = U[j][4 slot + lane]
@@ -423,7 +424,35 @@ __global__ __launch_bounds__(kGptqThreads) void gptq_block_kernel(
     oq[i] = 0.0f;
     od[i] = 0.0f;
   }
-  const float s = scale[r];
+  float s;
+  if (scale) {
+    s = scale[r];
+  } else {
+    // the block's scale as calculate_mx_qparam forms it from the current
+    // weights (quantized.py:491-498, gptq.py:103-113): amax of the block
+    // (NaN wins), / quant_max (IEEE), through the scale codebook, 1 where not
+    // positive, then at least 1e-12
+    float m = 0.0f;
+    int nan = 0;
+#pragma unroll
+    for (int i = 0; i < kGptqSlots; ++i) {
+      const float a = fabsf(w[i]);  // columns past ncols hold 0
+      nan |= a != a;
+      m = a > m ? a : m;
+    }
+    {  // over the quad: lanes ^1, then ^2
+      float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0xB1, 0xF, 0xF, false));
+      nan |= __builtin_amdgcn_mov_dpp(nan, 0xB1, 0xF, 0xF, false);
+      m = o > m ? o : m;
+      o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x4E, 0xF, 0xF, false));
+      nan |= __builtin_amdgcn_mov_dpp(nan, 0x4E, 0xF, 0xF, false);
+      m = o > m ? o : m;
+    }
+    float sc = nan ? __builtin_nanf("") : m / quant_max;
+    if (scale_qmap) sc = bf2f(scale_qmap[f2bf(sc)]);
+    sc = sc > 0.0f ? sc : 1.0f;
+    s = sc > 1e-12f ? sc : 1e-12f;
+  }
   const float* hl = hq + lane * kGptqSlots;
   float hr[kGptqSlots];
 #pragma unroll
@@ -455,7 +484,7 @@ __global__ __launch_bounds__(kGptqThreads) void gptq_block_kernel(
     }
   }
   float* orow = out + r * ld + col0;
-  float* drow = deltas + r * ncols;
+  float* drow = deltas + r * ldd;
 #pragma unroll
   for (int i = 0; i < kGptqSlots; ++i) {
     const int k = i * kGptqLanes + lane;
@@ -563,20 +592,24 @@ __global__ __launch_bounds__(kCholLeaf* kCholWaves) void chol_inv_leaf_kernel(co
 }  // namespace
 
 int gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int ncols, const float* scale,
-               const float* hinv, int64_t ldh, const uint16_t* qmap, float* out, float* deltas, hipStream_t st) {
+               float quant_max, const uint16_t* scale_qmap, const float* hinv, int64_t ldh, const uint16_t* qmap,
+               float* out, float* deltas, int64_t ldd, hipStream_t st) {
   if (rows < 0 || ld < 0 || col0 < 0 || ldh < 0) return set_error(kErrInvalid, "gptq_block: negative size");
   if (ncols < 1 || ncols > kGptqMaxCols)
     return set_error(kErrInvalid, "gptq_block: ncols must be in [1, %d] (got %d)", kGptqMaxCols, ncols);
   if (col0 + ncols > ld || col0 + ncols > ldh)
     return set_error(kErrInvalid, "gptq_block: columns %lld..%lld past the row length", (long long)col0,
                      (long long)(col0 + ncols));
+  if (ldd < ncols) return set_error(kErrInvalid, "gptq_block: deltas row stride below ncols");
   if (rows == 0) return kOk;
-  if (!work || !scale || !hinv || !qmap || !out || !deltas) return set_error(kErrInvalid, "gptq_block: null buffer");
+  if (!work || !hinv || !qmap || !out || !deltas) return set_error(kErrInvalid, "gptq_block: null buffer");
+  if (!scale && !(quant_max > 0.0f))
+    return set_error(kErrInvalid, "gptq_block: quant_max must be positive when the kernel forms the scale");
   if (reinterpret_cast<uintptr_t>(qmap) % 16)
     return set_error(kErrInvalid, "gptq_block: the table must be 16-byte aligned");
   hipLaunchKernelGGL(gptq_block_kernel, dim3((unsigned)((rows + kGptqRowsPerBlock - 1) / kGptqRowsPerBlock)),
-                     dim3(kGptqThreads), 0, st, work, rows, ld, col0,
-                     ncols, scale, hinv, ldh, qmap, out, deltas);
+                     dim3(kGptqThreads), 0, st, work, rows, ld, col0, ncols, scale, quant_max, scale_qmap, hinv, ldh,
+                     qmap, out, deltas, ldd);
   return check_launch("gptq_block");
 }
 

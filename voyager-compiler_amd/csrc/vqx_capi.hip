@@ -290,10 +290,11 @@ int vqx_lcq_histogram(const void* x, int32_t x_dtype, int64_t n, int64_t block_s
 }
 
 int vqx_gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int32_t ncols, const float* scale,
-                   const float* hinv, int64_t ldh, const uint16_t* qmap, float* out, float* deltas,
-                   vqx_stream_t stream) {
+                   float quant_max, const uint16_t* scale_qmap, const float* hinv, int64_t ldh,
+                   const uint16_t* qmap, float* out, float* deltas, int64_t ldd, vqx_stream_t stream) {
   g_err[0] = 0;
-  return gptq_block(work, rows, ld, col0, ncols, scale, hinv, ldh, qmap, out, deltas, (hipStream_t)stream);
+  return gptq_block(work, rows, ld, col0, ncols, scale, quant_max, scale_qmap, hinv, ldh, qmap, out, deltas, ldd,
+                    (hipStream_t)stream);
 }
 
 int vqx_chol_inverse_block(const float* a, int64_t lda, int32_t n, float* li, int64_t ldl, int32_t* info,

@@ -110,7 +110,8 @@ int lcq_histogram(const void* x, int dtype, int64_t n, int64_t block_size, float
                   int64_t weights_period, const float* edges, int bins, double* weight, double* total,
                   double* square, hipStream_t st);
 int gptq_block(const float* work, int64_t rows, int64_t ld, int64_t col0, int ncols, const float* scale,
-               const float* hinv, int64_t ldh, const uint16_t* qmap, float* out, float* deltas, hipStream_t st);
+               float quant_max, const uint16_t* scale_qmap, const float* hinv, int64_t ldh, const uint16_t* qmap,
+               float* out, float* deltas, int64_t ldd, hipStream_t st);
 
 // Lower Cholesky factor L of the leading n x n block of a (n <= 64, lower
 // triangle read) and its inverse into li (zeros above the diagonal); *info

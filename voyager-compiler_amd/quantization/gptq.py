@@ -182,25 +182,29 @@ def compensate_with_factor(weight, hinv, salience, fake_quant, shrink=False):
     block_size = fake_quant.block_size
     hinv = hinv.to(device=weight.device, dtype=torch.float32).contiguous()
     qmap = Q._table_bf16(fake_quant.qmap.to(weight.device))
+    sq = fake_quant.scale_qmap
+    sq = None if sq is None else Q._table_bf16(sq.to(weight.device))
     work = weight.float().contiguous().clone()
     out = torch.zeros_like(work)
     R, C = work.shape
+    # the kernel forms the plain block scale itself from the block it loads
+    in_kernel = not shrink and block_size <= LOOP_COLUMNS
     span = max(block_size, OUTER_COLUMNS // block_size * block_size)
     for outer in range(0, C, span):
         stop = min(outer + span, C)
         deltas = torch.empty(R, stop - outer, dtype=torch.float32, device=work.device)
         for start in range(outer, stop, block_size):
             end = min(start + block_size, stop)
-            scale = block_scale(work[:, start:end], salience[start:end], fake_quant, shrink).float().contiguous()
+            scale = None if in_kernel else \
+                block_scale(work[:, start:end], salience[start:end], fake_quant, shrink).float().contiguous()
             # the kernel walks at most LOOP_COLUMNS columns; a wider block's
             # later pieces get the earlier pieces' deltas through the GEMM
             for lo in range(start, end, LOOP_COLUMNS):
                 hi = min(lo + LOOP_COLUMNS, end)
-                d = torch.empty(R, hi - lo, dtype=torch.float32, device=work.device)
+                d = deltas[:, lo - outer:hi - outer]  # written in place, row stride stop - outer
                 _lib.call("vqx_gptq_block", _lib.ptr(work), R, C, lo, hi - lo, _lib.ptr(scale),
-                          _lib.ptr(hinv), hinv.shape[1], _lib.ptr(qmap), _lib.ptr(out), _lib.ptr(d),
-                          _lib.stream_of(work))
-                deltas[:, lo - outer:hi - outer] = d
+                          float(fake_quant.quant_max), _lib.ptr(sq), _lib.ptr(hinv), hinv.shape[1], _lib.ptr(qmap),
+                          _lib.ptr(out), _lib.ptr(d), deltas.stride(0), _lib.stream_of(work))
                 if hi < stop:
                     work[:, hi:stop].sub_(d @ hinv[lo:hi, hi:stop])
         if stop < C:
