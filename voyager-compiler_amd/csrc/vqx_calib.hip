@@ -543,11 +543,13 @@ __global__ __launch_bounds__(kCholLeaf* kCholWaves) void chol_inv_leaf_kernel(co
     // the factor needs fp32 accuracy, not correct rounding: the hardware
     // reciprocal square root keeps the per-column chain short
     const float djj = cb[j];
+    const float cl = cb[lane];  // read with the pivot, not behind it
     bad |= !(djj > 0.0f);
     const float inv = __builtin_amdgcn_rsqf(djj);
     const float d = djj * inv;
     if (threadIdx.x == 0) rdiag[j] = inv;
-    const float lij = lane > j ? cb[lane] * inv : (lane == j ? d : 0.0f);
+    const float lsc = cl * inv;
+    const float lij = lane > j ? lsc : (lane == j ? d : 0.0f);
     if (w == j / kCholCols) r[j % kCholCols] = lij;
     if (k0 + kCholCols - 1 > j) {
 #pragma unroll
