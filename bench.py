@@ -402,21 +402,19 @@ def setup_o1(vqx, torch, L, mx=False):
             name=f"O1 filter_outlier, bf16 4096x11008 N(0,1) with 0.5% x32 seed 5, |x| > {OUTLIER_THRESHOLD}, "
                  f"capacity 1% -> CSR ({nnz} outliers) + inliers",
             bytes=4 * n + csr_bytes, **common)
-    fmt = vqx.parse_format("fp8_e4m3")
-    desc = fmt.desc(x.device)
+    # the one-pass form: the split writes the quantized inliers and their
+    # block scales instead of the inliers
+    table = vqx.get_quantization_map("fp8_e4m3", "cuda")
     sc = torch.empty(R, C // 32, dtype=torch.bfloat16, device="cuda")
     qv = torch.empty_like(x)
-    mxq = L.load().vqx_mx_quantize
-    margs = (L.ptr(bufs["inl"]), L.BF16, R, C, 1, 32, L.ctypes.byref(desc), 0, 8, L.ctypes.c_float(448.0), None,
-             L.ptr(sc), None, None, L.ptr(qv), None, None, 1, L.stream_of(x))
-
-    def launch():
-        rc = filt(*fargs)
-        return rc if rc else mxq(*margs)
-    return launch, dict(
-        name=f"O2 quantize_mx_outlier: O1's split, then MX block-32 fp8_e4m3 power-of-two scales of the inliers "
-             f"-> CSR + bf16 scales + bf16 quantized inliers",
-        bytes=4 * n + n // 32 * 2 + csr_bytes, keep=(desc, fmt), **common)
+    fused = L.load().vqx_quantize_mx_outlier
+    margs = (L.ptr(x), 1, R, C, L.ctypes.c_float(OUTLIER_THRESHOLD), max_nnz, 0, 32, 0, 8, L.ctypes.c_float(448.0),
+             None, L.ptr(table), L.ptr(bufs["data"]), L.ptr(bufs["idx"]), L.ptr(bufs["ptr"]), L.ptr(sc), L.ptr(qv),
+             L.stream_of(x))
+    return (lambda: fused(*margs)), dict(
+        name=f"O2 quantize_mx_outlier: O1's CSR and, in the same split pass, MX block-32 fp8_e4m3 power-of-two "
+             f"scales and quantized values of the inliers -> CSR + bf16 scales + bf16 quantized inliers",
+        bytes=4 * n + n // 32 * 2 + csr_bytes, keep=(table, sc, qv), **common)
 
 
 def setup_o3(vqx, torch, L):
@@ -607,7 +605,7 @@ DOMINANT = {
     "c5_m1": "nf4_skinny_kernel",
     "c5_m16": "nf4_skinny_kernel",
     "o1_filter": "outlier_split_kernel<1, 8>",
-    "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8>",
+    "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8, true, 4>",
     "o3_spmm": "spmm_csr_kernel<1, 8>",
     "l1_histogram": "lcq_hist_kernel<0, true, false>",
     "g1_gptq": "gptq_block_kernel",

@@ -264,6 +264,23 @@ int vqx_filter_outlier(const void* x, int32_t x_dtype, int64_t batches, int64_t 
                        int32_t* indptr, void* inlier, vqx_stream_t stream);
 
 /*
+ * quantized_ops::quantize_mx_outlier in one pass over the inliers
+ * (src/vc/ops/quantized.py:649-699): the CSR of filter_outlier (as
+ * vqx_filter_outlier, row pointers + indptr_offset), then for each block of
+ * block_size (8, 16, 32 or 64; cols % block_size == 0) inliers along a row
+ * the block's scale as calculate_mx_qparam forms it (scale_mode 0: power of
+ * two with shift = floor(log2(quant_max)); 1: amax / quant_max through
+ * scale_qmap when given) and values = qmap[bf16(inlier / scale)], without
+ * writing the inliers.  x, data, scale, values: BF16 only; x and values
+ * 16-byte aligned; scale [batches * rows, cols / block_size]; values like x.
+ */
+int vqx_quantize_mx_outlier(const void* x, int64_t batches, int64_t rows, int64_t cols, float threshold,
+                            int64_t max_nnz, int32_t indptr_offset, int64_t block_size, int32_t scale_mode,
+                            int32_t shift, float quant_max, const uint16_t* scale_qmap, const uint16_t* qmap,
+                            void* data, int32_t* indices, int32_t* indptr, void* scale, void* values,
+                            vqx_stream_t stream);
+
+/*
  * quantized_ops::slice_csr_tensor (src/vc/ops/quantized.py:715-777) of one CSR
  * matrix: data [nnz] (F32, BF16 or F16), indices [nnz] int32, indptr [rows + 1]
  * int32 starting at 0; entries past indptr[rows] are padding (index -1).

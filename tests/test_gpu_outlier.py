@@ -247,3 +247,34 @@ def test_linear_mx_with_outliers(vqx):
                          A_indptr=p.cuda())
     sp = R.spmm_csr(d, i, p, W.T.contiguous(), sc.T.contiguous(), code, 32, "ck")
     assert_spmm_close(got_ck, sp, spmm_bound(d, i, p, Wd.T, "ck"), "matmul_mx sparse half")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bs", [8, 16, 64])
+@pytest.mark.parametrize("scale_dtype", [None, "fp8_e5m3"])
+@pytest.mark.parametrize("pow2", [True, False])
+def test_quantize_mx_outlier_fused_block_sizes(vqx, bs, scale_dtype, pow2):
+    # the one-pass form (bf16, blocks along the last axis): every block size
+    # it takes, scale codebook, special values in the input
+    x = with_specials(rand_outliers((3, 24, 384), torch.bfloat16, seed=11 + bs))
+    qm = vqx.get_quantization_map("fp8_e4m3", "cuda")
+    sq = None if scale_dtype is None else vqx.get_quantization_map(scale_dtype, "cuda")
+    got = Q.quantize_mx_outlier(x.cuda(), qm, [-1], bs, 448.0, pow2, sq, None, 4.0, 0.05, 7)
+    sq_o = None if scale_dtype is None else R.table_tensor(F.quantization_table(scale_dtype))
+    want = R.quantize_mx_outlier(x, R.table_tensor(F.quantization_table("fp8_e4m3")), [-1], bs, 448.0, pow2,
+                                 scale_qmap=sq_o, threshold=4.0, max_pct=0.05, indptr_offset=7)
+    check_all(got, want, ("data", "indices", "indptr", "scale", "inliers"))
+
+
+@pytest.mark.gpu
+def test_quantize_mx_outlier_fused_equals_two_pass_at_bench_size(vqx):
+    # O2: the fused split against filter_outlier followed by quantize_mx
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(4096, 11008, generator=g)
+    x = torch.where(torch.rand(4096, 11008, generator=g) < 0.005, x * 32, x).to(torch.bfloat16).cuda()
+    qm = vqx.get_quantization_map("fp8_e4m3", "cuda")
+    fused = Q.quantize_mx_outlier(x, qm, [-1], 32, 448.0, True, None, None, 6.0, 0.01, 0)
+    d, i, p, inl = vqx.ops.quantized._outlier_csr(x, 6.0, 0.01, 0)
+    s, v = Q.quantize_mx(inl, qm, [-1], 32, 448.0, True)
+    for a, b in zip(fused, (d, i, p, s, v)):
+        assert same(a, b)

@@ -85,6 +85,8 @@ _SIGNATURES = {
                                _I64, _I64, _P, _I32, _P], ctypes.c_int),
     "vqx_spmm_csr": ([_P, _I32, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _I64, _I64, _P, _P, _P], ctypes.c_int),
     "vqx_lcq_histogram": ([_P, _I32, _I64, _I64, _F, _P, _I64, _P, _I32, _P, _P, _P, _P], ctypes.c_int),
+    "vqx_quantize_mx_outlier": ([_P, _I64, _I64, _I64, ctypes.c_float, _I64, _I32, _I64, _I32, _I32, ctypes.c_float,
+                                 _P, _P, _P, _P, _P, _P, _P, _P], ctypes.c_int),
     "vqx_gptq_block": ([_P, _I64, _I64, _I64, _I32, _P, ctypes.c_float, _P, _P, _I64, _P, _P, _P, _I64, _P],
                        ctypes.c_int),
     "vqx_chol_inverse_block": ([_P, _I64, _I32, _P, _I64, _P, _P], ctypes.c_int),

@@ -14,6 +14,34 @@ struct ScaleParams {
   const uint16_t* scale_qmap;  // mode 1: optional bf16 table applied to the scale
 };
 
+// Device helpers shared by the MX kernels and the fused outlier split.
+// Block scale of a bf16 block, specialised by mode (branch-free).
+template <bool ABSMAX>
+__device__ __forceinline__ float block_scale_bf16(uint32_t amax, const ScaleParams& sp) {
+  if constexpr (!ABSMAX) {
+    // e = floor(bf16 log2(amax)) - shift (amax 0 -> -126); 2**e in bf16 keeps
+    // 2^-133 .. 2^127 and rounds 2^-134 and below to 0, which becomes 1
+    int e = (amax == 0 ? -126 : log2floor_bf16(amax)) - sp.shift;
+    float sc = e > 127 ? __builtin_huge_valf() : (e >= -133 ? exp2i(e) : 1.0f);
+    sc = amax == 0x7F80u ? __builtin_huge_valf() : sc;
+    return amax > 0x7F80u ? 1.0f : sc;
+  } else {
+    float sc = bf2f(f2bf(bf2f(amax) / sp.quant_max));
+    if (sp.scale_qmap) sc = bf2f(f2bf(bf2f(sp.scale_qmap[f2bf(sc)])));
+    return sc > 0.0f ? sc : 1.0f;
+  }
+}
+
+// Max over the LPB adjacent lanes of a block: DPP quad permutes for lane
+// distances 1 and 2, a shuffle beyond.
+template <int LPB>
+__device__ __forceinline__ uint32_t block_max(uint32_t v) {
+  if constexpr (LPB >= 2) v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  if constexpr (LPB >= 4) v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  if constexpr (LPB >= 8) v = umax32(v, (uint32_t)__shfl_xor((int)v, 4, 64));
+  return v;
+}
+
 struct MxOut {
   void* scale;          // input dtype [blocks]
   float* scale_f32;     // [blocks]
@@ -98,6 +126,10 @@ struct SpmmArgs {
 int filter_outlier(const void* x, int dtype, int64_t nb, int64_t rows, int64_t cols, float threshold,
                    int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices, int32_t* indptr,
                    void* inlier, hipStream_t st);
+int quantize_mx_outlier_fused(const void* x, int64_t nb, int64_t rows, int64_t cols, float threshold,
+                              int64_t max_nnz, int32_t indptr_offset, int64_t block_size, const ScaleParams& sp,
+                              const uint16_t* qmap, void* data, int32_t* indices, int32_t* indptr, void* scale,
+                              void* values, hipStream_t st);
 int csr_slice(const void* data, int dtype, const int32_t* indices, const int32_t* indptr, int64_t nnz_in,
               int64_t rows, int dim, int64_t start, int64_t end, int64_t max_nnz, void* data_out,
               int32_t* indices_out, int32_t* indptr_out, hipStream_t st);

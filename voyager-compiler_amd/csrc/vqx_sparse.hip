@@ -222,13 +222,24 @@ __device__ void pad_tail(const int32_t* __restrict__ indptr, int64_t rows, int64
 // (slot = running count + rank from the ballots) and writes them out as one
 // contiguous run when the row ends or the buffer nears full, instead of
 // scattering 2- and 4-byte stores.
-template <int DT, int V>
+// quantize_mx_outlier's inlier quantization fused into the split (bf16,
+// blocks of V * LPB along the row): the inliers' block scale as
+// calculate_mx_qparam forms it and qmap[bf16(inlier / scale)] as quantize
+// does (quantized.py:688-699), in place of the inliers themselves.
+struct MxFuse {
+  ScaleParams sp;
+  const uint16_t* qmap;  // 65536 bf16 values
+  uint16_t* scale;       // [rows, cols / (V * LPB)] bf16
+};
+
+template <int DT, int V, bool MXQ = false, int LPB = 1>
 __global__ __launch_bounds__(256) void outlier_split_kernel(const typename FT<DT>::S* __restrict__ x,
                                                             int64_t nb, int64_t rows, int64_t cols,
                                                             float t, const int32_t* __restrict__ indptr,
                                                             int64_t max_nnz, typename FT<DT>::S* __restrict__ inlier,
                                                             typename FT<DT>::S* __restrict__ data,
-                                                            int32_t* __restrict__ indices) {
+                                                            int32_t* __restrict__ indices, MxFuse mf = {}) {
+  static_assert(!MXQ || (DT == kBF16 && V == 8), "the fused MX quantization takes bf16 groups of 8");
   using S = typename FT<DT>::S;
   constexpr int U = 4;
   constexpr uint32_t CAP = 1024, FLUSH = CAP - 64 * V;  // a group adds at most 64 * V
@@ -286,7 +297,35 @@ __global__ __launch_bounds__(256) void outlier_split_kernel(const typename FT<DT
           below += lanes_below(m);
           n += (uint32_t)__popcll(m);
         }
-        if (ok[u]) store_group<S, V, true>(irow + c, keep);
+        if constexpr (MXQ) {
+          // the block's scale from its inliers' magnitudes over LPB lanes (a
+          // block is wholly inside or wholly past the row, as cols % (8 LPB)
+          // == 0), then each inlier quantized through the table
+          uint32_t am = 0;
+#pragma unroll
+          for (int j = 0; j < V; ++j) am = umax32(am, keep[j] & 0x7FFFu);
+          am = block_max<LPB>(am);
+          const float sc = mf.sp.mode == 0 ? block_scale_bf16<false>(am, mf.sp) : block_scale_bf16<true>(am, mf.sp);
+          // a power-of-two scale with a representable reciprocal divides
+          // exactly as a multiply (both round the same real x / s once)
+          const uint32_t sb = f2u(sc), se = (sb >> 23) & 0xFFu;
+          const bool p2 = (sb & 0x807FFFFFu) == 0 && se - 1u < 253u;
+          uint32_t qv[V];
+          if (__builtin_amdgcn_ballot_w64(!p2) == 0) {
+            const float rc = u2f((254u - se) << 23);
+#pragma unroll
+            for (int j = 0; j < V; ++j) qv[j] = mf.qmap[f2bf(bf2f(keep[j]) * rc)];
+          } else {
+#pragma unroll
+            for (int j = 0; j < V; ++j) qv[j] = mf.qmap[f2bf(bf2f(keep[j]) / sc)];
+          }
+          if (ok[u]) {
+            store_group<S, V, true>(irow + c, qv);
+            if (lane % LPB == 0) mf.scale[g * (cols / (V * LPB)) + c / (V * LPB)] = (uint16_t)f2bf(sc);
+          }
+        } else {
+          if (ok[u]) store_group<S, V, true>(irow + c, keep);
+        }
         if (n != 0) {
           uint32_t q = nbuf + below;
 #pragma unroll
@@ -581,6 +620,15 @@ int launch_filter(const void* x, int64_t nb, int64_t rows, int64_t cols, float t
   return check_launch("filter_outlier");
 }
 
+template <int LPB>
+void launch_split_mx(const uint16_t* x, int64_t nb, int64_t rows, int64_t cols, float t, int32_t* indptr,
+                     int64_t max_nnz, uint16_t* values, uint16_t* data, int32_t* indices, const MxFuse& mf,
+                     hipStream_t st) {
+  const int64_t nrows = nb * rows;
+  hipLaunchKernelGGL((outlier_split_kernel<kBF16, 8, true, LPB>), dim3(grid_for(nrows > 0 ? nrows : 1, 4, 16)),
+                     dim3(256), 0, st, x, nb, rows, cols, t, indptr, max_nnz, values, data, indices, mf);
+}
+
 template <int DT>
 int launch_spmm(const SpmmArgs& a, hipStream_t st) {
   constexpr int V = FT<DT>::kVec;
@@ -612,6 +660,41 @@ int filter_outlier(const void* x, int dtype, int64_t nb, int64_t rows, int64_t c
     case kF16: return launch_filter<kF16>(x, nb, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr, inlier, st);
     default: return set_error(kErrInvalid, "filter_outlier: dtype %d not supported (fp32, bf16, fp16)", dtype);
   }
+}
+
+int quantize_mx_outlier_fused(const void* x, int64_t nb, int64_t rows, int64_t cols, float threshold,
+                              int64_t max_nnz, int32_t indptr_offset, int64_t block_size, const ScaleParams& sp,
+                              const uint16_t* qmap, void* data, int32_t* indices, int32_t* indptr, void* scale,
+                              void* values, hipStream_t st) {
+  if (nb < 0 || rows < 0 || cols < 0 || max_nnz < 0)
+    return set_error(kErrInvalid, "quantize_mx_outlier: negative size");
+  if (block_size != 8 && block_size != 16 && block_size != 32 && block_size != 64)
+    return set_error(kErrUnsupported, "quantize_mx_outlier: fused form takes blocks of 8, 16, 32 or 64");
+  if (cols % block_size) return set_error(kErrUnsupported, "quantize_mx_outlier: cols must be whole blocks");
+  if (nb == 0) return kOk;
+  if (!indptr || !qmap || (max_nnz > 0 && (!data || !indices)) ||
+      (rows * cols > 0 && (!x || !values || !scale)))
+    return set_error(kErrInvalid, "quantize_mx_outlier: null buffer");
+  if (max_nnz > INT32_MAX || rows >= INT32_MAX || cols > INT32_MAX)
+    return set_error(kErrInvalid, "quantize_mx_outlier: sizes beyond int32 indices");
+  if (!aligned(x, 16) || !aligned(values, 16))
+    return set_error(kErrInvalid, "quantize_mx_outlier: input and values must be 16-byte aligned");
+  const int64_t nrows = nb * rows;
+  const uint16_t* xs = (const uint16_t*)x;
+  if (nrows > 0)
+    hipLaunchKernelGGL((outlier_count_kernel<kBF16, 8>), dim3(grid_for(nrows, 4, 16)), dim3(256), 0, st, xs, nrows,
+                       rows, cols, threshold, indptr);
+  hipLaunchKernelGGL(csr_scan_kernel, dim3((unsigned)nb), dim3(1024), 0, st, indptr, rows, max_nnz, indptr_offset);
+  MxFuse mf{sp, qmap, (uint16_t*)scale};
+  uint16_t* v = (uint16_t*)values;
+  uint16_t* d = (uint16_t*)data;
+  switch (block_size) {
+    case 8: launch_split_mx<1>(xs, nb, rows, cols, threshold, indptr, max_nnz, v, d, indices, mf, st); break;
+    case 16: launch_split_mx<2>(xs, nb, rows, cols, threshold, indptr, max_nnz, v, d, indices, mf, st); break;
+    case 32: launch_split_mx<4>(xs, nb, rows, cols, threshold, indptr, max_nnz, v, d, indices, mf, st); break;
+    default: launch_split_mx<8>(xs, nb, rows, cols, threshold, indptr, max_nnz, v, d, indices, mf, st); break;
+  }
+  return check_launch("quantize_mx_outlier");
 }
 
 int csr_slice(const void* data, int dtype, const int32_t* indices, const int32_t* indptr, int64_t nnz_in,

@@ -614,9 +614,45 @@ def quantize_mx_outlier(input, qmap, axes, block_size, quant_max, force_scale_po
                         scale_qmap=None, output_code=None, threshold=None, max_pct=0.01, indptr_offset=0):
     """filter_outlier, row pointers + indptr_offset, then quantize_mx of the
     inliers (quantized.py:642-691): (data, indices, indptr, scale, inliers)."""
+    seq = isinstance(axes, (list, tuple))
+    ax = (axes[0] if len(axes) == 1 else None) if seq else axes
+    if (ax in (-1, input.ndim - 1) and input.dtype == torch.bfloat16 and input.ndim >= 2 and threshold is not None
+            and block_size in (8, 16, 32, 64) and input.shape[-1] % block_size == 0):
+        return _quantize_mx_outlier_fused(input, qmap, block_size, quant_max, force_scale_power_of_two, scale_qmap,
+                                          threshold, max_pct, indptr_offset)
     data, indices, indptr, inliers = _outlier_csr(input, threshold, max_pct, indptr_offset)
     scale, q = quantize_mx(inliers, qmap, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap)
     return data, indices, indptr, scale, q
+
+
+def _quantize_mx_outlier_fused(input, qmap, block_size, quant_max, force_pow2, scale_qmap, threshold, max_pct,
+                               indptr_offset):
+    """quantize_mx_outlier for bf16 blocks along the last axis in one pass:
+    the split writes the quantized inliers and their block scales directly."""
+    _lib.require_device(input, "quantize_mx_outlier")
+    x = input.contiguous()
+    batch_shape = x.shape[:-2]
+    R, C = x.shape[-2:]
+    max_nnz = int(math.prod(x.shape[-2:]) * max_pct)
+    if max_nnz < 0:
+        raise ValueError(f"filter_outlier: max_pct {max_pct} gives a negative capacity")
+    if not -(1 << 31) <= indptr_offset < (1 << 31):
+        raise ValueError(f"indptr_offset {indptr_offset} does not fit the int32 row pointers")
+    t = torch.tensor(float(threshold), dtype=x.dtype).item()
+    nb = math.prod(batch_shape)
+    dev = x.device
+    data = torch.empty((*batch_shape, max_nnz), dtype=x.dtype, device=dev)
+    indices = torch.empty((*batch_shape, max_nnz), dtype=torch.int32, device=dev)
+    indptr = torch.empty((*batch_shape, R + 1), dtype=torch.int32, device=dev)
+    scale = torch.empty((*x.shape[:-1], C // block_size), dtype=x.dtype, device=dev)
+    values = torch.empty_like(x)
+    table = _table_bf16(qmap.to(dev))
+    sq = _table_bf16(scale_qmap.to(dev)) if (scale_qmap is not None and not force_pow2) else None
+    shift = math.floor(math.log2(quant_max)) if force_pow2 else 0
+    _lib.call("vqx_quantize_mx_outlier", _lib.ptr(x), nb, R, C, t, max_nnz, int(indptr_offset), block_size,
+              0 if force_pow2 else 1, shift, float(quant_max), _lib.ptr(sq), _lib.ptr(table), _lib.ptr(data),
+              _lib.ptr(indices), _lib.ptr(indptr), _lib.ptr(scale), _lib.ptr(values), _lib.stream_of(x))
+    return data, indices, indptr, scale, values
 
 
 @_impl("slice_csr_tensor")
