@@ -260,9 +260,9 @@ def setup_c4(vqx, torch, L, K, decode=False):
         elements=n, bytes=algo, bound="hbm", dtype="u8->f32", cpu=cpu_c4(torch, xc, cbc, True))
 
 
-def setup_c5(vqx, torch, L):
+def setup_c5(vqx, torch, L, whole_tiles=False, M=2048):
     g = torch.Generator().manual_seed(4)
-    M, N, K = 2048, 11008, 4096
+    N, K = 11008, 4096
     Ac = torch.randn(M, K, generator=g).to(torch.bfloat16)
     A = Ac.cuda()
     W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).cuda()
@@ -272,12 +272,27 @@ def setup_c5(vqx, torch, L):
     lv = vqx.parse_format("nf4").tables(A.device)["levels_bf16"]
     out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
     st = L.stream_of(A)
-    fn = L.load().vqx_nf4_linear
-    args = (L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), M, N, K, st)
+    if whole_tiles:
+        fn = L.load().vqx_nf4_linear
+        args = (L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), M, N, K, st)
+        how, launches, keep = "whole 256x128 tiles only", 1, (A, codes, sc, lv, out)
+    else:
+        import ctypes
+        n = ctypes.c_int64(0)
+        L.call("vqx_nf4_linear_workspace_size", M, N, K, ctypes.byref(n))
+        ws = torch.empty(n.value, dtype=torch.uint8, device="cuda")
+        fn = L.load().vqx_nf4_linear_ws
+        args = (L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), M, N, K, L.ptr(ws), n.value, st)
+        if n.value:
+            how, launches = "whole tiles in full rounds of the CUs, the last round's tiles split along K (stream-K)", 2
+        else:
+            how, launches = "whole 256x128 tiles (the last round is too full for a K split to pay)", 1
+        keep = (A, codes, sc, lv, out, ws)
     return (lambda: fn(*args)), dict(
-        name="C5 NF4-dequant linear: A bf16 [2048,4096] x W NF4 block-64 [11008,4096]^T -> bf16, fp32 accumulate",
+        name=f"C5 NF4-dequant linear: A bf16 [{M},4096] x W NF4 block-64 [11008,4096]^T -> bf16, fp32 accumulate; "
+             + how,
         elements=M * N, flops=2 * M * N * K, bytes=M * K * 2 + N * K // 2 + N * K // 64 * 4 + M * N * 2,
-        bound="mfma", dtype="bf16", cpu=cpu_c5(torch, Ac, N))
+        bound="mfma", dtype="bf16", cpu=cpu_c5(torch, Ac, N), launches=launches, keep=keep)
 
 
 def setup_c5_skinny(vqx, torch, L, M):
@@ -453,6 +468,8 @@ CONFIGS = {
     "c4_k256": lambda v, t, L: setup_c4(v, t, L, 256),
     "c4_k16_decode": lambda v, t, L: setup_c4(v, t, L, 16, decode=True),
     "c5": lambda v, t, L: setup_c5(v, t, L),
+    "c5_m256": lambda v, t, L: setup_c5(v, t, L, M=256),
+    "c5_m256_whole_tiles": lambda v, t, L: setup_c5(v, t, L, whole_tiles=True, M=256),
     "c5_m1": lambda v, t, L: setup_c5_skinny(v, t, L, 1),
     "c5_m16": lambda v, t, L: setup_c5_skinny(v, t, L, 16),
     "o1_filter": lambda v, t, L: setup_o1(v, t, L),
@@ -602,6 +619,8 @@ DOMINANT = {
     "c4_k256": "cb_encode_kernel<float, 8>",
     "c4_k16_decode": "cb_decode_kernel<float>",
     "c5": "nf4_gemm_kernel",
+    "c5_m256": "nf4_gemm_sk_kernel",
+    "c5_m256_whole_tiles": "nf4_gemm_kernel",
     "c5_m1": "nf4_skinny_kernel",
     "c5_m16": "nf4_skinny_kernel",
     "o1_filter": "outlier_split_kernel<1, 8>",
@@ -720,6 +739,8 @@ def main():
             "hbm_traffic_bytes": measured_traffic(k),
             "algorithmic_bytes": info["bytes"], "achieved_GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
             "dtype": info["dtype"]}
+        if info.get("launches", 1) > 1:
+            results[k]["launches_per_step"] = info["launches"]
         if info.get("multi_launch"):
             # one step is a whole host routine of many launches: the
             # bandwidth fields of a single kernel do not apply to it

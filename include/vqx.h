@@ -246,6 +246,24 @@ int vqx_nf4_linear(const uint16_t* A, const uint8_t* codes, const float* scale, 
                    vqx_stream_t stream);
 
 /*
+ * The same product (src/vc/ops/quantized.py:286-348) with a caller-owned
+ * workspace, which lets the M > 16 tile kernel balance its last round: when
+ * the count of 256 x 128 tiles is not a multiple of the CU count, the last
+ * round's tiles are split along K over all CUs (stream-K) and their fp32
+ * partial sums meet in the workspace.  Sums are added in a fixed order, so
+ * the result is deterministic; it can differ from vqx_nf4_linear's in the
+ * last bf16 bit where the fp32 grouping of a sum differs.
+ * vqx_nf4_linear_workspace_size gives the bytes needed on the current device
+ * (0: the shape runs whole tiles only and workspace may be NULL).  workspace:
+ * 256-byte aligned device memory, no initial contents needed; calls that
+ * share one workspace must be ordered (one stream).
+ */
+int vqx_nf4_linear_workspace_size(int64_t M, int64_t N, int64_t K, int64_t* bytes);
+int vqx_nf4_linear_ws(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
+                      const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, void* workspace,
+                      int64_t workspace_bytes, vqx_stream_t stream);
+
+/*
  * quantized_ops::filter_outlier (src/vc/ops/quantized.py:532-630, with
  * _pad_csr at :537-569), and the outlier half of quantize_mx_outlier
  * (:633-712, indptr_offset added to the row pointers).

@@ -144,3 +144,34 @@ def test_fake_quantize_module_state_on_cpu(vqx):
     assert fq.amax_history.shape == (16, 1) and fq.scale.item() == 2.0
     fq2 = FusedAmaxObsFakeQuantize("posit8_1")
     assert not bool(fq2.observer_enabled[0])
+
+
+def _stream_k_bytes(M, N, K, cus=256):
+    """The NF4 tile kernel's balanced-last-round plan, restated: split the
+    tiles of the last partly filled round along K when each CU's share is at
+    least max(16, nk / 4) steps and at least 24 steps shorter than a tile,
+    with at most 6 ranges meeting one tile."""
+    if M <= 16 or N % 128 or K % 64:
+        return 0
+    tiles, nk = (M // 256) * (N // 128), K // 64
+    rem = tiles % cus
+    if rem == 0:
+        return 0
+    U = rem * nk
+    g = min(cus, U // max(16, nk // 4))
+    if g < 1 or -(-U // g) + 24 > nk or -(-nk // (U // g)) + 1 > 6:
+        return 0
+    return -(-rem * 4 // 256) * 256 + 2 * g * 256 * 128 * 4
+
+
+def test_nf4_linear_workspace_size(vqx):
+    # without a GPU the library assumes MI355X's 256 CUs
+    import ctypes
+    L = vqx._lib
+    for shape in [(2048, 11008, 4096), (4096, 4096, 4096), (512, 4096, 4096), (16, 4096, 4096), (300, 512, 2048),
+                  (256, 11008, 4096), (808, 11008, 4096), (768, 1024, 8192), (256, 128, 64), (4096, 11008, 128)]:
+        n = ctypes.c_int64(-1)
+        L.call("vqx_nf4_linear_workspace_size", *shape, ctypes.byref(n))
+        assert n.value == _stream_k_bytes(*shape), shape
+    assert _stream_k_bytes(2048, 11008, 4096) == 0  # C5: 688 tiles, whole tiles
+    assert _stream_k_bytes(256, 11008, 4096) == 512 + 2 * 256 * 131072

@@ -114,3 +114,78 @@ def test_nf4_linear_rejects_unsupported_shape(vqx):
     sc, codes = Q.quantize_mx_packed(W.cuda(), "nf4", -1, 64, False, 1.0, "float32")
     with pytest.raises(RuntimeError, match="nf4_gemm"):
         Q.linear_nf4(A, codes, sc, None, 64, "nf4")
+
+
+def _nf4_operands(M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    sc, codes = Q.quantize_mx_packed(make_weight(N, K, seed).cuda(), "nf4", -1, 64, False, 1.0, "float32")
+    return A, codes, sc
+
+
+def _whole_tiles(vqx, A, codes, sc, N):
+    """The product through the entry point without a workspace (whole tiles)."""
+    L = vqx._lib
+    M, K = A.shape
+    lv = vqx.parse_format("nf4").tables(A.device)["levels_bf16"]
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=A.device)
+    L.call("vqx_nf4_linear", L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), M, N, K,
+           L.stream_of(A))
+    return out
+
+
+# Shapes whose 256 x 128 tile count is not a multiple of the CU count, so
+# linear_nf4 splits the last round's tiles along K (stream-K): 64 and 86
+# tiles (no whole-tile launch, counters cleared by their own launch), 258
+# full tiles plus a partial row tile, 344 tiles (256 whole, 88 split), and 24
+# tiles of a long K.
+SK_SHAPES = [(512, 4096, 4096), (256, 11008, 4096), (808, 11008, 4096), (1024, 11008, 4096), (768, 1024, 8192)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", SK_SHAPES)
+def test_nf4_linear_stream_k(vqx, M, N, K):
+    print(f"stream-K NF4 linear M={M} N={N} K={K}", flush=True)
+    L = vqx._lib
+    import ctypes
+    n = ctypes.c_int64(0)
+    L.call("vqx_nf4_linear_workspace_size", M, N, K, ctypes.byref(n))
+    assert n.value > 0  # these shapes do take the split path on a 256-CU device
+    A, codes, sc = _nf4_operands(M, N, K, M + K)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(N)).to(torch.bfloat16).cuda()
+    # a call on other activations of the same shape first: a workspace slot
+    # read before its contributor wrote it would hold that call's sums
+    Q.linear_nf4(torch.randn_like(A), codes, sc, bias, 64, "nf4")
+    out = Q.linear_nf4(A, codes, sc, bias, 64, "nf4")
+    again = Q.linear_nf4(A, codes, sc, bias, 64, "nf4")
+    # fixed summation order: identical on every call
+    assert torch.equal(out, again)
+    Wd = decode_reference(codes, sc, N, K).cuda()
+    ref = (A.float() @ Wd.float().t() + bias.float()).to(torch.bfloat16).float()
+    err = (out.float() - ref).abs()
+    tol = 1e-2 * ref.abs() + 1e-2 * ref.abs().mean()
+    assert (err.norm() / ref.norm()).item() < 1e-2 and (err > tol).float().mean().item() < 1e-3
+    # against whole tiles: only the grouping of the fp32 sums differs, so the
+    # fp32 results are within 2 K u sum|a w| of each other (u = 2^-24) and
+    # the bf16 outputs within that plus one bf16 spacing
+    whole = _whole_tiles(vqx, A, codes, sc, N)
+    out_nb = Q.linear_nf4(A, codes, sc, None, 64, "nf4")
+    S = A.float().abs() @ Wd.float().abs().t()
+    diff = (out_nb.float() - whole.float()).abs()
+    bound = torch.maximum(whole.float().abs(), out_nb.float().abs()) * 2.0 ** -7 + 2 * K * 2.0 ** -24 * S
+    assert bool((diff <= bound).all()), float((diff - bound).max())
+
+
+@pytest.mark.gpu
+def test_nf4_linear_ws_rejects_small_workspace(vqx):
+    L = vqx._lib
+    A, codes, sc = _nf4_operands(512, 4096, 4096, 1)
+    lv = vqx.parse_format("nf4").tables(A.device)["levels_bf16"]
+    out = torch.empty(512, 4096, dtype=torch.bfloat16, device=A.device)
+    ws = torch.empty(1024, dtype=torch.uint8, device=A.device)
+    with pytest.raises(ValueError, match="workspace"):
+        L.call("vqx_nf4_linear_ws", L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), 512, 4096, 4096,
+               L.ptr(ws), 1024, L.stream_of(A))
+    with pytest.raises(ValueError, match="workspace"):
+        L.call("vqx_nf4_linear_ws", L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), 512, 4096, 4096,
+               None, 0, L.stream_of(A))

@@ -242,7 +242,25 @@ int vqx_nf4_linear(const uint16_t* A, const uint8_t* codes, const float* scale, 
                    vqx_stream_t stream) {
   g_err[0] = 0;
   if (!A || !codes || !scale || !levels || !out) return set_error(kErrInvalid, "nf4_linear: null buffer");
-  return nf4_gemm(A, codes, scale, levels, bias, out, M, N, K, (hipStream_t)stream);
+  return nf4_gemm(A, codes, scale, levels, bias, out, M, N, K, nullptr, 0, (hipStream_t)stream);
+}
+
+int vqx_nf4_linear_workspace_size(int64_t M, int64_t N, int64_t K, int64_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return set_error(kErrInvalid, "nf4_linear_workspace_size: null bytes");
+  *bytes = nf4_gemm_workspace(M, N, K);
+  return kOk;
+}
+
+int vqx_nf4_linear_ws(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
+                      const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, void* workspace,
+                      int64_t workspace_bytes, vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (!A || !codes || !scale || !levels || !out) return set_error(kErrInvalid, "nf4_linear: null buffer");
+  if (!workspace && nf4_gemm_workspace(M, N, K) > 0)
+    return set_error(kErrInvalid, "nf4_linear_ws: null workspace (this shape needs %lld bytes)",
+                     (long long)nf4_gemm_workspace(M, N, K));
+  return nf4_gemm(A, codes, scale, levels, bias, out, M, N, K, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int vqx_filter_outlier(const void* x, int32_t x_dtype, int64_t batches, int64_t rows, int64_t cols,

@@ -92,7 +92,9 @@ int codebook_decode(const uint8_t* codes, int64_t rows, int64_t cols, const floa
 
 // vqx_nf4_gemm.hip
 int nf4_gemm(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
-             const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, hipStream_t st);
+             const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, void* workspace,
+             int64_t workspace_bytes, hipStream_t st);
+int64_t nf4_gemm_workspace(int64_t M, int64_t N, int64_t K);
 
 // vqx_sparse.hip
 struct CsrDecode {

@@ -36,6 +36,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 256, kBN = 128, kBK = 64;
 constexpr int kThreads = 512;
@@ -142,17 +143,30 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// PARTIAL: the launch covers one row tile starting at row m_base with fewer
-// than 256 rows left; the full tiles run in a launch of their own without
-// the row clamping.
+// The 16 levels' bf16 high and low bytes as v_perm tables (uniform).
+__device__ __forceinline__ LevelBytes level_bytes(const uint16_t* __restrict__ levels) {
+  uint32_t hb[4] = {0, 0, 0, 0}, lbv[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    uint32_t v = levels[c];
+    hb[c >> 2] |= ((v >> 8) & 0xFFu) << (8 * (c & 3));
+    lbv[c >> 2] |= (v & 0xFFu) << (8 * (c & 3));
+  }
+  LevelBytes lb;
+  lb.h0 = hb[0]; lb.h1 = hb[1]; lb.h2 = hb[2]; lb.h3 = hb[3];
+  lb.l0 = lbv[0]; lb.l1 = lbv[1]; lb.l2 = lbv[2]; lb.l3 = lbv[3];
+  return lb;
+}
+
+// k-steps ks0 .. ks0 + nk - 1 of the 256 x 128 tile at rows m0, columns n0,
+// into acc (zeroed here).  PARTIAL: rows past M load row M - 1.  Ends with
+// an LDS barrier after the last fragment read, so the rings can be refilled
+// for another tile right away.  The rings are declared here, so their LDS
+// addresses are constants and fold into the instructions' offsets.
 template <bool PARTIAL>
-__global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __restrict__ A,
-                                                             const uint8_t* __restrict__ codes,
-                                                             const float* __restrict__ scale,
-                                                             const uint16_t* __restrict__ levels,
-                                                             const uint16_t* __restrict__ bias,
-                                                             uint16_t* __restrict__ out, int M, int N, int K,
-                                                             int m_base) {
+__device__ __forceinline__ void tile_steps(const uint16_t* __restrict__ A, const uint8_t* __restrict__ codes,
+                                           const float* __restrict__ scale, const LevelBytes& lb, int M, int K,
+                                           int m0, int n0, int ks0, int nk, f32x16 (&acc)[2][2]) {
   __shared__ __attribute__((aligned(16))) uint8_t wl[3 * kWTile];
   __shared__ __attribute__((aligned(16))) uint8_t al[3 * kATile];
   const int tid = threadIdx.x;
@@ -162,41 +176,12 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
   const int wn = wave & 1;   // 64-column block
   const int lr = lane & 31;  // fragment row within a 32-tile
   const int lk = lane >> 5;  // which 8-wide k group
-
-  // XCD-aware tile order: consecutive workgroup ids go round-robin over the 8
-  // XCDs; give each XCD a contiguous range of tiles, M-major, so an XCD works
-  // through whole A slabs.
-  const int ntn = N / kBN, ntm = PARTIAL ? 1 : (M - m_base) / kBM;
-  const int ntiles = ntn * ntm;
-  int bid = blockIdx.x;
-  int per_xcd = (ntiles + 7) / 8;
-  int tile = (bid & 7) * per_xcd + (bid >> 3);
-  if (ntiles % 8 != 0) tile = bid;  // uneven split: plain order
-  if (tile >= ntiles) return;
-  const int tm = tile / ntn, tn = tile % ntn;
-  const int m0 = m_base + tm * kBM, n0 = tn * kBN;
-
-  // level byte tables (uniform)
-  LevelBytes lb;
-  {
-    uint32_t hb[4] = {0, 0, 0, 0}, lbv[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      uint32_t v = levels[c];
-      hb[c >> 2] |= ((v >> 8) & 0xFFu) << (8 * (c & 3));
-      lbv[c >> 2] |= (v & 0xFFu) << (8 * (c & 3));
-    }
-    lb.h0 = hb[0]; lb.h1 = hb[1]; lb.h2 = hb[2]; lb.h3 = hb[3];
-    lb.l0 = lbv[0]; lb.l1 = lbv[1]; lb.l2 = lbv[2]; lb.l3 = lbv[3];
-  }
-
-  const int nk = K / kBK;
   const int kb = K / 64;  // scale blocks per row
 
   // A staging: load q (0..3) of a step covers rows 32 wave + 8 q .. +7, lane
   // L chunk L % 8 of row 32 wave + 8 q + L / 8.  In a partial tile, rows
   // past M load row M - 1 instead; their outputs are not stored.
-  const uint16_t* asrc = A + (size_t)(m0 + wave * 32 + (lane >> 3)) * K + (lane & 7) * 8;
+  const uint16_t* asrc = A + (size_t)(m0 + wave * 32 + (lane >> 3)) * K + (lane & 7) * 8 + (size_t)ks0 * kBK;
   int aoff[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -220,8 +205,8 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
   };
   // W decode assignment: row wr, codes for k 16 wq .. 16 wq + 15 of a step
   const int wr = tid >> 2, wq = tid & 3;
-  const uint8_t* wsrc = codes + (size_t)(n0 + wr) * (K / 2) + wq * 8;
-  const float* ssrc = scale + (size_t)(n0 + wr) * kb;
+  const uint8_t* wsrc = codes + (size_t)(n0 + wr) * (K / 2) + wq * 8 + (size_t)ks0 * (kBK / 2);
+  const float* ssrc = scale + (size_t)(n0 + wr) * kb + ks0;
 
   auto decode_store = [&](uint32_t base, uint32_t w, float s, int j) {
     uint32_t o[4];
@@ -242,7 +227,6 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
                                 *reinterpret_cast<const u32x4*>(al + base + swz(wm * 64 + i * 32 + lr, kk * 2 + lk)));
   };
 
-  f32x16 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -369,8 +353,17 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
     if (ks + 2 < nk) step(kChecked, k2, ks + 2, wc2, ws2);
   }
 
-  // epilogue: lane holds output row m = lr of each A fragment and columns
-  // 8 g + 4 lk .. +3 (g = 0..3) of each W fragment, in acc[i][j][4 g .. 4 g + 3]
+}
+
+// Output of one tile: lane holds output row m = lr of each A fragment and
+// columns 8 g + 4 lk .. +3 (g = 0..3) of each W fragment, in
+// acc[i][j][4 g .. 4 g + 3]; bf16 (RNE) of acc + bias, rows < M only when
+// PARTIAL.
+template <bool PARTIAL>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[2][2], const uint16_t* __restrict__ bias,
+                                           uint16_t* __restrict__ out, int M, int N, int m0, int n0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lk = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -395,6 +388,150 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
   }
 }
 
+// Whole tiles, one per workgroup.  PARTIAL: the launch covers the one row
+// tile starting at row m_base with fewer than 256 rows left; otherwise it
+// covers the first ntiles full tiles from row m_base, M-major.  zero/nzero:
+// counters of a stream-K launch that follows on the same stream, cleared by
+// workgroup 0 after its tile (stores ahead of the k loop would make the
+// compiler's memory-counter waits inside it more conservative).
+template <bool PARTIAL>
+__global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __restrict__ A,
+                                                             const uint8_t* __restrict__ codes,
+                                                             const float* __restrict__ scale,
+                                                             const uint16_t* __restrict__ levels,
+                                                             const uint16_t* __restrict__ bias,
+                                                             uint16_t* __restrict__ out, int M, int N, int K,
+                                                             int m_base, int ntiles, int* __restrict__ zero,
+                                                             int nzero) {
+  // XCD-aware tile order: consecutive workgroup ids go round-robin over the 8
+  // XCDs; give each XCD a contiguous range of tiles, M-major, so an XCD works
+  // through whole A slabs.
+  const int ntn = N / kBN;
+  int bid = blockIdx.x;
+  int per_xcd = (ntiles + 7) / 8;
+  int tile = (bid & 7) * per_xcd + (bid >> 3);
+  if (ntiles % 8 != 0) tile = bid;  // uneven split: plain order
+  if (tile >= ntiles) return;
+  const int m0 = m_base + (tile / ntn) * kBM, n0 = (tile % ntn) * kBN;
+  const LevelBytes lb = level_bytes(levels);
+  f32x16 acc[2][2];
+  tile_steps<PARTIAL>(A, codes, scale, lb, M, K, m0, n0, 0, K / kBK, acc);
+  store_tile<PARTIAL>(acc, bias, out, M, N, m0, n0);
+  if (zero && blockIdx.x == 0)
+    for (int i = threadIdx.x; i < nzero; i += kThreads) zero[i] = 0;
+}
+
+// Stream-K tail: the last sk_tiles full tiles (from tile index tile_base,
+// M-major) as sk_tiles * nk k-steps split evenly over the gridDim.x
+// workgroups: workgroup i takes steps [U i / g, U (i + 1) / g) of the
+// tile-major step sequence (U = sk_tiles * nk, g = gridDim.x), i.e. the end
+// of one tile, possibly whole tiles, and the start of another.  A whole tile
+// is stored directly.  A piece of a tile leaves its fp32 sums in the
+// workspace, slot 2 i for the workgroup's first tile and 2 i + 1 for its last
+// (slot layout: float pair q of thread t at (q * 512 + t) * 2), then bumps the
+// tile's counter; the workgroup that brings the counter to the number of
+// contributors adds the slots in contributor order (so the result does not
+// depend on which one arrives last), adds the bias and stores the tile.
+// Nothing waits on another workgroup.  The counters start at zero (cleared
+// by the launch before this one on the stream).
+//
+// The slots are written and read with device-scope atomic stores and loads,
+// which the hardware keeps coherent across the XCDs' separate L2 caches at
+// the access itself (the sc1 policy).  A device-scope fence would instead
+// write back (release) or invalidate (acquire) the whole L2 of the XCD, in
+// every wave of every piece, and cost the other workgroups there their
+// cached operands.  Each wave waits for its slot stores to complete before
+// the workgroup barrier that precedes the counter increment, and the
+// finisher issues its slot loads only after it has read the counter.
+constexpr int kPartFloats = kBM * kBN;  // one tile of fp32 sums
+constexpr int kMaxContrib = 6;          // workgroups sharing one tile, at most (the plan ensures it)
+
+__device__ __forceinline__ int sk_group_of(int64_t step, int g, int64_t U) {
+  return (int)(((step + 1) * g - 1) / U);  // the workgroup whose range holds step
+}
+
+__global__ __launch_bounds__(kThreads) void nf4_gemm_sk_kernel(const uint16_t* __restrict__ A,
+                                                                const uint8_t* __restrict__ codes,
+                                                                const float* __restrict__ scale,
+                                                                const uint16_t* __restrict__ levels,
+                                                                const uint16_t* __restrict__ bias,
+                                                                uint16_t* __restrict__ out, int M, int N, int K,
+                                                                int tile_base, int sk_tiles, float* __restrict__ part,
+                                                                int* __restrict__ cnt) {
+  __shared__ int s_arrived;
+  const int tid = threadIdx.x;
+  // workgroup ids go round-robin over the 8 XCDs: renumber them so each XCD
+  // runs a contiguous run of ranges (the pieces of one tile on one XCD, its
+  // operands in that XCD's L2)
+  const int g = gridDim.x;
+  const int me = g % 8 == 0 ? (int)(blockIdx.x & 7) * (g >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int nk = K / kBK, ntn = N / kBN;
+  const int64_t U = (int64_t)sk_tiles * nk;
+  const int64_t u0 = U * me / g, u1 = U * (me + 1) / g;
+  const int t_first = (int)(u0 / nk);
+  const LevelBytes lb = level_bytes(levels);
+  for (int64_t u = u0; u < u1;) {
+    const int t = (int)(u / nk);
+    const int k_lo = (int)(u - (int64_t)t * nk);
+    const int k_hi = (int)((u1 - (int64_t)t * nk) < nk ? (u1 - (int64_t)t * nk) : nk);
+    const int tile = tile_base + t;
+    const int m0 = (tile / ntn) * kBM, n0 = (tile % ntn) * kBN;
+    f32x16 acc[2][2];
+    tile_steps<false>(A, codes, scale, lb, M, K, m0, n0, k_lo, k_hi - k_lo, acc);
+    u = (int64_t)(t + 1) * nk;
+    if (k_lo == 0 && k_hi == nk) {
+      store_tile<false>(acc, bias, out, M, N, m0, n0);
+      continue;
+    }
+    uint64_t* mine = reinterpret_cast<uint64_t*>(part + (size_t)(2 * me + (t == t_first ? 0 : 1)) * kPartFloats);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const f32x2 v = {acc[i][j][2 * q], acc[i][j][2 * q + 1]};
+          __hip_atomic_store(mine + (size_t)((i * 2 + j) * 8 + q) * kThreads + tid, __builtin_bit_cast(uint64_t, v),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's slot stores have completed
+    __syncthreads();
+    const int c_first = sk_group_of((int64_t)t * nk, g, U);
+    const int c_last = sk_group_of((int64_t)t * nk + nk - 1, g, U);
+    if (tid == 0) s_arrived = __hip_atomic_fetch_add(cnt + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_arrived != c_last - c_first) continue;  // another contributor is still running
+    // the slots in contributor order (32 loads of one slot in flight at a time)
+    f32x16 tot[2][2] = {};
+    for (int c = c_first; c <= c_last; ++c) {
+      const int tf = (int)((U * c / g) / nk);
+      const uint64_t* src = reinterpret_cast<const uint64_t*>(part + (size_t)(2 * c + (t == tf ? 0 : 1)) * kPartFloats);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            f32x2 v;
+            if (c == me) {
+              v = f32x2{acc[i][j][2 * q], acc[i][j][2 * q + 1]};
+            } else {
+              v = __builtin_bit_cast(f32x2, __hip_atomic_load(src + (size_t)((i * 2 + j) * 8 + q) * kThreads + tid,
+                                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            }
+#pragma unroll
+            for (int e = 0; e < 2; ++e) tot[i][j][2 * q + e] = c == c_first ? v[e] : tot[i][j][2 * q + e] + v[e];
+          }
+    }
+    store_tile<false>(tot, bias, out, M, N, m0, n0);
+  }
+}
+
+__global__ void nf4_zero_counters(int* __restrict__ cnt, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) cnt[i] = 0;
+}
+
 // ---------------------------------------------------------------------------
 // Skinny form for M <= 16 (decode-time batches).  Each wave computes a
 // 16 x 16 output tile (all of A's rows, padded to 16; 16 output columns)
@@ -409,8 +546,6 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
 // are idle most of the time: the decode's VALU and the weight's bytes bound
 // the kernel.
 // ---------------------------------------------------------------------------
-typedef float f32x4v __attribute__((ext_vector_type(4)));
-
 constexpr int kSkinnyWaves = 4;
 
 __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uint16_t* __restrict__ A,
@@ -480,8 +615,48 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uin
   }
 }
 
+// Stream-K plan for the full tiles of an M > 16 product: when the tile count
+// is not a multiple of the CU count, the tiles of the last, partly filled
+// round are split into k-step ranges over up to one workgroup per CU, at
+// least max(16, nk / 4) steps each.  A split tile costs each workgroup a
+// second pipeline fill and the fp32 exchange, about 20 us at K = 4096
+// (measured: 81 us for 44-step ranges against 61 us of steps), so the split
+// is taken only when a range is at least kSkSaving steps shorter than a
+// whole tile: C5's last round (176 of 256 CUs, 44-step ranges) stays whole
+// tiles (measured even), a 256-row product (86 tiles, 22-step ranges) splits
+// (51 us against 66 us).  dp_tiles run first, one per workgroup.
+struct SkPlan {
+  int64_t dp_tiles = 0, sk_tiles = 0, groups = 0, bytes = 0;
+};
+
+constexpr int64_t kCounterBytes = 256;  // alignment of the counter block
+constexpr int64_t kSkSaving = 24;       // k-steps a split must save over a whole tile
+
+static SkPlan plan_stream_k(int64_t M, int64_t N, int64_t K) {
+  SkPlan p;
+  if (M <= 16 || N % kBN || K % kBK || K <= 0) return p;
+  const int64_t tiles = (M / kBM) * (N / kBN), nk = K / kBK;
+  const int64_t cus = num_cus();
+  p.dp_tiles = tiles;
+  const int64_t rem = tiles % cus;
+  if (rem == 0) return p;
+  const int64_t U = rem * nk, min_steps = nk / 4 > 16 ? nk / 4 : 16;
+  const int64_t g = U / min_steps < cus ? U / min_steps : cus;
+  if (g < 1 || (U + g - 1) / g + kSkSaving > nk) return p;
+  // a tile meets at most ceil(nk / shortest range) + 1 ranges
+  if ((nk + U / g - 1) / (U / g) + 1 > kMaxContrib) return p;
+  p.dp_tiles = tiles - rem;
+  p.sk_tiles = rem;
+  p.groups = g;
+  p.bytes = (rem * 4 + kCounterBytes - 1) / kCounterBytes * kCounterBytes + 2 * g * kPartFloats * 4;
+  return p;
+}
+
+int64_t nf4_gemm_workspace(int64_t M, int64_t N, int64_t K) { return plan_stream_k(M, N, K).bytes; }
+
 int nf4_gemm(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
-             const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+             const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, void* workspace,
+             int64_t workspace_bytes, hipStream_t st) {
   if (M <= 0 || N <= 0 || K <= 0) return set_error(kErrInvalid, "nf4_gemm: empty shape");
   if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) return set_error(kErrInvalid, "nf4_gemm: shape too large");
   if (K % kBK) return set_error(kErrUnsupported, "nf4_gemm: needs K %% 64 == 0 (got K = %lld)", (long long)K);
@@ -495,12 +670,32 @@ int nf4_gemm(const uint16_t* A, const uint8_t* codes, const float* scale, const 
   if (N % kBN)
     return set_error(kErrUnsupported, "nf4_gemm: needs N %% 128 == 0 for M > 16 (got N = %lld)", (long long)N);
   const int64_t mfull = M / kBM * kBM;
-  if (mfull > 0)
-    hipLaunchKernelGGL(nf4_gemm_kernel<false>, dim3((unsigned)(mfull / kBM * (N / kBN))), dim3(kThreads), 0, st, A,
-                       codes, scale, levels, bias, out, (int)M, (int)N, (int)K, 0);
+  const int64_t ntiles = mfull / kBM * (N / kBN);
+  SkPlan plan;
+  plan.dp_tiles = ntiles;
+  if (workspace) {
+    plan = plan_stream_k(M, N, K);
+    if (plan.sk_tiles > 0 && workspace_bytes < plan.bytes)
+      return set_error(kErrInvalid, "nf4_gemm: workspace of %lld bytes, this shape needs %lld",
+                       (long long)workspace_bytes, (long long)plan.bytes);
+    if (!aligned(workspace, 256)) return set_error(kErrInvalid, "nf4_gemm: workspace must be 256-byte aligned");
+  }
+  int* cnt = plan.sk_tiles > 0 ? static_cast<int*>(workspace) : nullptr;
+  if (cnt && plan.dp_tiles == 0)
+    hipLaunchKernelGGL(nf4_zero_counters, dim3((unsigned)((plan.sk_tiles + 255) / 256)), dim3(256), 0, st, cnt,
+                       (int)plan.sk_tiles);
+  if (plan.dp_tiles > 0)
+    hipLaunchKernelGGL(nf4_gemm_kernel<false>, dim3((unsigned)plan.dp_tiles), dim3(kThreads), 0, st, A, codes, scale,
+                       levels, bias, out, (int)M, (int)N, (int)K, 0, (int)plan.dp_tiles, cnt, (int)plan.sk_tiles);
+  if (plan.sk_tiles > 0) {
+    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                           (plan.sk_tiles * 4 + kCounterBytes - 1) / kCounterBytes * kCounterBytes);
+    hipLaunchKernelGGL(nf4_gemm_sk_kernel, dim3((unsigned)plan.groups), dim3(kThreads), 0, st, A, codes, scale, levels,
+                       bias, out, (int)M, (int)N, (int)K, (int)plan.dp_tiles, (int)plan.sk_tiles, part, cnt);
+  }
   if (mfull < M)
     hipLaunchKernelGGL(nf4_gemm_kernel<true>, dim3((unsigned)(N / kBN)), dim3(kThreads), 0, st, A, codes, scale,
-                       levels, bias, out, (int)M, (int)N, (int)K, (int)mfull);
+                       levels, bias, out, (int)M, (int)N, (int)K, (int)mfull, (int)(N / kBN), nullptr, 0);
   return check_launch("nf4_gemm");
 }
 

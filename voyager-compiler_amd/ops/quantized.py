@@ -12,6 +12,7 @@ Ops beyond the reference's (packed storage is this build's own):
 ``codebook_encode``, ``codebook_decode``, ``linear_nf4``.
 """
 
+import ctypes
 import math
 import weakref
 from typing import List, Optional, Tuple
@@ -930,10 +931,27 @@ def linear_nf4(input, codes, scale, bias=None, block_size=64, dtype="nf4"):
     lv = fmt.tables(x.device)["levels_bf16"]
     out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
     b = None if bias is None else bias.to(device=x.device, dtype=torch.bfloat16).contiguous()
-    _lib.call("vqx_nf4_linear", _lib.ptr(x), _lib.ptr(codes.contiguous()),
+    ws_bytes = _nf4_workspace_bytes(M, N, K, x.device)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    _lib.call("vqx_nf4_linear_ws", _lib.ptr(x), _lib.ptr(codes.contiguous()),
               _lib.ptr(scale.to(torch.float32).contiguous()), _lib.ptr(lv), _lib.ptr(b), _lib.ptr(out),
-              M, N, K, _lib.stream_of(x))
+              M, N, K, _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
     return out.reshape(*input.shape[:-1], N)
+
+
+_NF4_WS = {}
+
+
+def _nf4_workspace_bytes(M, N, K, device):
+    """Workspace the NF4 tile kernel's balanced last round needs for this
+    shape on ``device`` (0: whole tiles only), cached per shape."""
+    key = (M, N, K, device.index)
+    if key not in _NF4_WS:
+        n = ctypes.c_int64(0)
+        with torch.cuda.device(device):
+            _lib.call("vqx_nf4_linear_workspace_size", M, N, K, ctypes.byref(n))
+        _NF4_WS[key] = n.value
+    return _NF4_WS[key]
 
 
 # ---------------------------------------------------------------------------
