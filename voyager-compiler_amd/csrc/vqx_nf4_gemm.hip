@@ -15,9 +15,11 @@
 //    32 w .. 32 w + 31) into registers, written in the swizzled layout one
 //    step after the load.
 //  * W: decoded once per workgroup into a ring of three LDS buffers two
-//    steps ahead (128 x 64 bf16 per step; each thread 16 codes: v_perm
-//    byte-table lookup of the levels, fp32 product with the block scale,
-//    RNE).  One barrier per step publishes both rings.
+//    steps ahead (128 x 64 bf16 per step; each thread 16 codes of one row).
+//    The quad of lanes on a row shares the row's scale: each lane scales
+//    four of the 16 levels (fp32 product, RNE to bf16), DPP broadcasts give
+//    every lane the 16 scaled values as v_perm byte tables, and the codes
+//    are byte lookups into them.  One barrier per step publishes both rings.
 //  * Fragments of both operands are read from LDS one 16-deep k slice ahead
 //    of their MFMAs (16-byte chunks XOR-swizzled by row: conflict-free).
 //  * The MFMA takes the W fragment as its first operand, so each lane ends
@@ -81,23 +83,6 @@ __device__ __forceinline__ uint32_t byte_sign_mask(uint32_t y) {
   return __builtin_amdgcn_perm(y, y << 8, 0x0B090A08u);
 }
 
-// 8 codes -> 4 dwords of bf16 pairs = bf16(level * s), k ascending.
-__device__ __forceinline__ void decode8(uint32_t w, float s, const LevelBytes& lb, uint32_t (&out)[4]) {
-  // byte b of w holds codes 2b (low nibble) and 2b + 1 (high nibble); bit 3
-  // of the even codes moves to bit 7 with w << 4, the odd ones' is there
-  uint32_t he, le, ho, lo;
-  lookup4(w & 0x07070707u, byte_sign_mask(w << 4), lb, he, le);         // even k: codes 0, 2, 4, 6
-  lookup4((w >> 4) & 0x07070707u, byte_sign_mask(w), lb, ho, lo);       // odd k:  codes 1, 3, 5, 7
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    // fp32 of the levels: level bf16 in the high half
-    uint32_t se = 0x00000C0Cu | ((4u + i) << 24) | ((uint32_t)i << 16);  // bytes: 0, 0, le[i], he[i]
-    float ve = u2f(__builtin_amdgcn_perm(he, le, se));
-    float vo = u2f(__builtin_amdgcn_perm(ho, lo, se));
-    out[i] = pack_bf16x2(ve * s, vo * s);
-  }
-}
-
 // The 16 values bf16(level[c] * s) of one scale block, as high and low byte
 // tables in the LevelBytes layout: pair p[i] holds entries 2i (low half) and
 // 2i + 1; the high bytes of entries 4j .. 4j + 3 are bytes 1, 3 of p[2j] and
@@ -115,6 +100,26 @@ __device__ __forceinline__ LevelBytes scaled_levels(const float (&lv)[16], float
   t.l1 = __builtin_amdgcn_perm(p[3], p[2], 0x06040200u);
   t.l2 = __builtin_amdgcn_perm(p[5], p[4], 0x06040200u);
   t.l3 = __builtin_amdgcn_perm(p[7], p[6], 0x06040200u);
+  return t;
+}
+
+// scaled_levels for the four lanes of a DPP quad that share one scale: lane
+// q of the quad scales levels 4 q .. 4 q + 3 (lq, its own four) and builds
+// byte tables h_q, l_q; quad broadcasts give every lane all eight.  The
+// same bytes as scaled_levels, for a quarter of its products and
+// conversions plus 8 DPP moves.
+__device__ __forceinline__ LevelBytes quad_scaled_levels(const float (&lq)[4], float s) {
+  const uint32_t pa = pack_bf16x2(lq[0] * s, lq[1] * s), pb = pack_bf16x2(lq[2] * s, lq[3] * s);
+  const int h = (int)__builtin_amdgcn_perm(pb, pa, 0x07050301u), l = (int)__builtin_amdgcn_perm(pb, pa, 0x06040200u);
+  LevelBytes t;
+  t.h0 = (uint32_t)__builtin_amdgcn_mov_dpp(h, 0x00, 0xF, 0xF, true);  // quad_perm [0,0,0,0]
+  t.h1 = (uint32_t)__builtin_amdgcn_mov_dpp(h, 0x55, 0xF, 0xF, true);  // [1,1,1,1]
+  t.h2 = (uint32_t)__builtin_amdgcn_mov_dpp(h, 0xAA, 0xF, 0xF, true);  // [2,2,2,2]
+  t.h3 = (uint32_t)__builtin_amdgcn_mov_dpp(h, 0xFF, 0xF, 0xF, true);  // [3,3,3,3]
+  t.l0 = (uint32_t)__builtin_amdgcn_mov_dpp(l, 0x00, 0xF, 0xF, true);
+  t.l1 = (uint32_t)__builtin_amdgcn_mov_dpp(l, 0x55, 0xF, 0xF, true);
+  t.l2 = (uint32_t)__builtin_amdgcn_mov_dpp(l, 0xAA, 0xF, 0xF, true);
+  t.l3 = (uint32_t)__builtin_amdgcn_mov_dpp(l, 0xFF, 0xF, 0xF, true);
   return t;
 }
 
@@ -143,21 +148,6 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// The 16 levels' bf16 high and low bytes as v_perm tables (uniform).
-__device__ __forceinline__ LevelBytes level_bytes(const uint16_t* __restrict__ levels) {
-  uint32_t hb[4] = {0, 0, 0, 0}, lbv[4] = {0, 0, 0, 0};
-#pragma unroll
-  for (int c = 0; c < 16; ++c) {
-    uint32_t v = levels[c];
-    hb[c >> 2] |= ((v >> 8) & 0xFFu) << (8 * (c & 3));
-    lbv[c >> 2] |= (v & 0xFFu) << (8 * (c & 3));
-  }
-  LevelBytes lb;
-  lb.h0 = hb[0]; lb.h1 = hb[1]; lb.h2 = hb[2]; lb.h3 = hb[3];
-  lb.l0 = lbv[0]; lb.l1 = lbv[1]; lb.l2 = lbv[2]; lb.l3 = lbv[3];
-  return lb;
-}
-
 // k-steps ks0 .. ks0 + nk - 1 of the 256 x 128 tile at rows m0, columns n0,
 // into acc (zeroed here).  PARTIAL: rows past M load row M - 1.  Ends with
 // an LDS barrier after the last fragment read, so the rings can be refilled
@@ -165,8 +155,8 @@ __device__ __forceinline__ LevelBytes level_bytes(const uint16_t* __restrict__ l
 // addresses are constants and fold into the instructions' offsets.
 template <bool PARTIAL>
 __device__ __forceinline__ void tile_steps(const uint16_t* __restrict__ A, const uint8_t* __restrict__ codes,
-                                           const float* __restrict__ scale, const LevelBytes& lb, int M, int K,
-                                           int m0, int n0, int ks0, int nk, f32x16 (&acc)[2][2]) {
+                                           const float* __restrict__ scale, const uint16_t* __restrict__ levels,
+                                           int M, int K, int m0, int n0, int ks0, int nk, f32x16 (&acc)[2][2]) {
   __shared__ __attribute__((aligned(16))) uint8_t wl[3 * kWTile];
   __shared__ __attribute__((aligned(16))) uint8_t al[3 * kATile];
   const int tid = threadIdx.x;
@@ -203,14 +193,19 @@ __device__ __forceinline__ void tile_steps(const uint16_t* __restrict__ A, const
     for (int q = 0; q < 4; ++q)
       *reinterpret_cast<u32x4*>(al + stage + swz(wave * 32 + 8 * q + (lane >> 3), lane & 7)) = areg[q];
   };
-  // W decode assignment: row wr, codes for k 16 wq .. 16 wq + 15 of a step
+  // W decode assignment: row wr, codes for k 16 wq .. 16 wq + 15 of a step.
+  // The quad of lanes on one row shares the row's scale: each lane scales
+  // four of the levels (lq) and the quad shares the byte tables.
   const int wr = tid >> 2, wq = tid & 3;
+  float lq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lq[i] = u2f((uint32_t)levels[4 * wq + i] << 16);
   const uint8_t* wsrc = codes + (size_t)(n0 + wr) * (K / 2) + wq * 8 + (size_t)ks0 * (kBK / 2);
   const float* ssrc = scale + (size_t)(n0 + wr) * kb + ks0;
 
-  auto decode_store = [&](uint32_t base, uint32_t w, float s, int j) {
+  auto decode_store = [&](uint32_t base, uint32_t w, const LevelBytes& tb, int j) {
     uint32_t o[4];
-    decode8(w, s, lb, o);
+    decode8_scaled(w, tb, o);
     u32x4 v = {o[0], o[1], o[2], o[3]};
     *reinterpret_cast<u32x4*>(wl + base + swz(wr, wq * 2 + j)) = v;
   };
@@ -270,11 +265,13 @@ __device__ __forceinline__ void tile_steps(const uint16_t* __restrict__ A, const
     if (nk > 2) load_codes(wc0, ws0, 2);
     if (nk > 3) load_codes(wc1, ws1, 3);
     if (nk > 4) load_codes(wc2, ws2, 4);
-    decode_store(0, c0.x, s0, 0);
-    decode_store(0, c0.y, s0, 1);
+    const LevelBytes t0 = quad_scaled_levels(lq, s0);
+    decode_store(0, c0.x, t0, 0);
+    decode_store(0, c0.y, t0, 1);
     if (nk > 1) {
-      decode_store(kWTile, c1.x, s1, 0);
-      decode_store(kWTile, c1.y, s1, 1);
+      const LevelBytes t1 = quad_scaled_levels(lq, s1);
+      decode_store(kWTile, c1.x, t1, 0);
+      decode_store(kWTile, c1.y, t1, 1);
     }
   }
   lds_barrier();
@@ -300,7 +297,7 @@ __device__ __forceinline__ void tile_steps(const uint16_t* __restrict__ A, const
     const bool more = kFull || ks + 1 < nk;
     const bool ahead2 = kFull || ks + 2 < nk;
     const uint32_t w0 = wc.x, w1 = wc.y;
-    const float s = ws;
+    LevelBytes tb;  // the step's scaled tables, built before its first decode
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       bf16x8(&bcur)[2] = (kk & 1) ? bB : bA;
@@ -315,8 +312,11 @@ __device__ __forceinline__ void tile_steps(const uint16_t* __restrict__ A, const
         read_a(anext, a_nxt, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (kk == 0 && ahead2) decode_store(w_new, w0, s, 0);
-      if (kk == 2 && ahead2) decode_store(w_new, w1, s, 1);
+      if (kk == 0 && ahead2) {
+        tb = quad_scaled_levels(lq, ws);
+        decode_store(w_new, w0, tb, 0);
+      }
+      if (kk == 2 && ahead2) decode_store(w_new, w1, tb, 1);
       mma(bcur, acur);
       if (kk == 1) {
         if (ahead2) store_a(a_new);  // A of step ks + 2, loaded during step ks - 1
@@ -413,9 +413,8 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_kernel(const uint16_t* __re
   if (ntiles % 8 != 0) tile = bid;  // uneven split: plain order
   if (tile >= ntiles) return;
   const int m0 = m_base + (tile / ntn) * kBM, n0 = (tile % ntn) * kBN;
-  const LevelBytes lb = level_bytes(levels);
   f32x16 acc[2][2];
-  tile_steps<PARTIAL>(A, codes, scale, lb, M, K, m0, n0, 0, K / kBK, acc);
+  tile_steps<PARTIAL>(A, codes, scale, levels, M, K, m0, n0, 0, K / kBK, acc);
   store_tile<PARTIAL>(acc, bias, out, M, N, m0, n0);
   if (zero && blockIdx.x == 0)
     for (int i = threadIdx.x; i < nzero; i += kThreads) zero[i] = 0;
@@ -469,7 +468,6 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_sk_kernel(const uint16_t* _
   const int64_t U = (int64_t)sk_tiles * nk;
   const int64_t u0 = U * me / g, u1 = U * (me + 1) / g;
   const int t_first = (int)(u0 / nk);
-  const LevelBytes lb = level_bytes(levels);
   for (int64_t u = u0; u < u1;) {
     const int t = (int)(u / nk);
     const int k_lo = (int)(u - (int64_t)t * nk);
@@ -477,7 +475,7 @@ __global__ __launch_bounds__(kThreads) void nf4_gemm_sk_kernel(const uint16_t* _
     const int tile = tile_base + t;
     const int m0 = (tile / ntn) * kBM, n0 = (tile % ntn) * kBN;
     f32x16 acc[2][2];
-    tile_steps<false>(A, codes, scale, lb, M, K, m0, n0, k_lo, k_hi - k_lo, acc);
+    tile_steps<false>(A, codes, scale, levels, M, K, m0, n0, k_lo, k_hi - k_lo, acc);
     u = (int64_t)(t + 1) * nk;
     if (k_lo == 0 && k_hi == nk) {
       store_tile<false>(acc, bias, out, M, N, m0, n0);
