@@ -469,7 +469,6 @@ CONFIGS = {
     "c4_k16_decode": lambda v, t, L: setup_c4(v, t, L, 16, decode=True),
     "c5": lambda v, t, L: setup_c5(v, t, L),
     "c5_m256": lambda v, t, L: setup_c5(v, t, L, M=256),
-    "c5_m256_whole_tiles": lambda v, t, L: setup_c5(v, t, L, whole_tiles=True, M=256),
     "c5_m1": lambda v, t, L: setup_c5_skinny(v, t, L, 1),
     "c5_m16": lambda v, t, L: setup_c5_skinny(v, t, L, 16),
     "o1_filter": lambda v, t, L: setup_o1(v, t, L),
@@ -607,6 +606,12 @@ def _cpu_model():
 
 
 # Kernel that dominates each config's launch (rocprofv3 names it this way).
+# configs run only when named with --only: comparison points that would
+# share a kernel name with a default config in a rocprof run of all of them
+ON_REQUEST = {
+    "c5_m256_whole_tiles": lambda v, t, L: setup_c5(v, t, L, whole_tiles=True, M=256),
+}
+
 DOMINANT = {
     "c1": "fq_lut_kernel<float, 1>",
     "c2": "mx_lut_kernel<4, 4, true, 0, true>",
@@ -721,13 +726,16 @@ def main():
     vqx = __graft_entry__.load_package()
     L = vqx._lib
     keys = list(CONFIGS) if a.only is None else a.only.split(",")
+    for k in keys:
+        if k not in CONFIGS and k not in ON_REQUEST:
+            sys.exit(f"bench.py: unknown config {k!r}")
     if HEADLINE not in keys:
         keys = [HEADLINE] + keys
     results = {}
     info_head = None
     for k in keys:
         print(f"[bench] {k}: setup", file=sys.stderr, flush=True)
-        launch, info = CONFIGS[k](vqx, torch, L)
+        launch, info = {**CONFIGS, **ON_REQUEST}[k](vqx, torch, L)
         tm = time_config(torch, launch, a.steps, a.warmup)
         ms = tm["kernel_ms_avg"]
         gbs = info["bytes"] / (ms * 1e-3) / 1e9
