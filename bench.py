@@ -129,6 +129,35 @@ def cpu_c5(torch, Ac, N):
 # ---------------------------------------------------------------------------
 # configs: setup() -> (launch callable, info)
 # ---------------------------------------------------------------------------
+def cpu_f3(torch, xc):
+    def run():
+        from oracle import reference_ops as R
+        rows = 512
+        dt = _timed(lambda: R.group_wise_affine_fake_quant(xc[:rows], [-1], 64, 0.0, 3.0))
+        return dt * xc.shape[0] / rows, \
+            f"rows 0-{rows - 1} (1/{xc.shape[0] // rows}), scaled: GroupWiseAffineFakeQuantFunction.forward"
+    return run
+
+
+def setup_f3(vqx, torch, L):
+    """Group-wise affine fake-quant (uint2, blocks of 64 along the last
+    axis, as for a KV cache) of C2's bf16 input."""
+    xc = c2_input(torch)
+    x = xc.cuda()
+    rows, cols = x.shape
+    y = torch.empty_like(x)
+    sc = torch.empty(rows, cols // 64, dtype=x.dtype, device="cuda")
+    zp = torch.empty_like(sc)
+    args = (L.ptr(x), L.BF16, rows, cols, 1, 64, 0.0, 3.0, None, L.ptr(sc), L.ptr(zp), L.ptr(y), L.stream_of(x))
+    fn = L.load().vqx_gwa_fake_quant
+    n = x.numel()
+    return (lambda: fn(*args)), dict(
+        name="F3 group-wise affine fake-quant, uint2 (0..3), blocks of 64 along the last axis: bf16 [4096,11008] "
+             "-> bf16 values + bf16 scale and zero point per block",
+        elements=n, bytes=4 * n + 2 * 2 * (n // 64), bound="hbm", dtype="bf16", keep=(x, y, sc, zp),
+        cpu=cpu_f3(torch, xc))
+
+
 def setup_c1(vqx, torch, L):
     torch.manual_seed(0)
     xc = torch.randn(4096, 4096, dtype=torch.float32)
@@ -471,6 +500,7 @@ CONFIGS = {
     "c5_m256": lambda v, t, L: setup_c5(v, t, L, M=256),
     "c5_m1": lambda v, t, L: setup_c5_skinny(v, t, L, 1),
     "c5_m16": lambda v, t, L: setup_c5_skinny(v, t, L, 16),
+    "f3_gwa": lambda v, t, L: setup_f3(v, t, L),
     "o1_filter": lambda v, t, L: setup_o1(v, t, L),
     "o2_quantize_mx_outlier": lambda v, t, L: setup_o1(v, t, L, mx=True),
     "o3_spmm": lambda v, t, L: setup_o3(v, t, L),
@@ -628,6 +658,7 @@ DOMINANT = {
     "c5_m256_whole_tiles": "nf4_gemm_kernel",
     "c5_m1": "nf4_skinny_kernel",
     "c5_m16": "nf4_skinny_kernel",
+    "f3_gwa": "gwa_fq_kernel<unsigned short>",
     "o1_filter": "outlier_split_kernel<1, 8>",
     "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8, true, 4>",
     "o3_spmm": "spmm_csr_kernel<1, 8>",

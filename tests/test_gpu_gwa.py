@@ -32,7 +32,8 @@ def gwa_inputs(shape, dt, seed):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape,axis,bs", [((64, 256), -1, 64), ((8, 100), -1, 32), ((4, 37, 6), 1, 8),
-                                           ((33, 5), 0, 16), ((3, 7), -1, 64)])
+                                           ((33, 5), 0, 16), ((3, 7), -1, 64), ((16, 128), -1, 8),
+                                           ((16, 96), -1, 16)])
 @pytest.mark.parametrize("qrange", [(0, 3), (-8, 7), (0, 255)])
 def test_gwa_fake_quant_matches_oracle(vqx, dt, shape, axis, bs, qrange):
     from importlib import import_module
@@ -80,3 +81,17 @@ def test_gwa_fakequantize_module(vqx):
     xg = x.cuda().requires_grad_(True)
     m(xg).sum().backward()
     assert torch.equal(xg.grad, torch.ones_like(xg))
+
+
+@pytest.mark.gpu
+def test_gwa_bench_shape_bit_exact(vqx):
+    # the bench's F3 workload: C2's bf16 [4096, 11008] input, uint2, blocks of
+    # 64 along the last axis (the coalesced last-axis kernel)
+    from importlib import import_module
+
+    qops = import_module(vqx.__name__ + ".ops.quantized")
+    g = torch.Generator().manual_seed(1)
+    x = (0.02 * torch.randn(4096, 11008, generator=g)).to(torch.bfloat16)
+    sf, zp, y = qops.gwa_fake_quantize(x.cuda(), -1, 64, 0, 3)
+    rsf, rzp, ry = R.group_wise_affine_fake_quant(x, -1, 64, 0, 3)
+    assert same(sf.cpu(), rsf) and same(zp.cpu(), rzp) and same(y.cpu(), ry)

@@ -357,6 +357,100 @@ __global__ __launch_bounds__(256) void gwa_fq_kernel(const T* __restrict__ x, in
   }
 }
 
+// Blocks along the last axis (inner == 1, L % bs == 0, bs = 8 G with G in
+// 1, 2, 4, 8): G consecutive lanes share a block, each loading 8 consecutive
+// elements with vector loads, and reduce min / max / NaN with XOR shuffles.
+// The per-element arithmetic is gwa_fq_kernel's.  The only freedom the tree
+// order adds is which of +0 and -0 a min or max keeps, and neither sf
+// (max - min, then 1 where not > 0) nor zp (-min / sf + qmin) nor y changes
+// with it.
+template <typename T, int G>
+__global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ x, int64_t nchunks, float qmin,
+                                                          float qmax, const uint16_t* __restrict__ scale_qmap,
+                                                          T* scale_out, T* zp_out, T* __restrict__ y) {
+  const float qrange = qmax - qmin;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  // every lane runs the same number of iterations (nchunks is a multiple of
+  // G and the stride of 256), so the shuffles see whole groups
+  for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c - threadIdx.x % 64 < nchunks; c += stride) {
+    const bool live = c < nchunks;
+    const int64_t cc = live ? c : nchunks - 1;
+    float v[8];
+    if constexpr (sizeof(T) == 2) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(x + cc * 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = u2f(w[i] << 16);
+        v[2 * i + 1] = u2f(w[i] & 0xFFFF0000u);
+      }
+    } else {
+      const float4 a = *reinterpret_cast<const float4*>(x + cc * 8);
+      const float4 b = *reinterpret_cast<const float4*>(x + cc * 8 + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    int nan = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      nan |= v[i] != v[i];
+      mn = v[i] < mn ? v[i] : mn;
+      mx = v[i] > mx ? v[i] : mx;
+    }
+#pragma unroll
+    for (int m = 1; m < G; m <<= 1) {
+      const float omn = __shfl_xor(mn, m, 64), omx = __shfl_xor(mx, m, 64);
+      nan |= __shfl_xor(nan, m, 64);
+      mn = omn < mn ? omn : mn;
+      mx = omx > mx ? omx : mx;
+    }
+    if (nan) mn = mx = __builtin_nanf("");
+    float sf = round_to<T>(round_to<T>(mx - mn) / qrange);
+    sf = sf > 0.0f ? sf : 1.0f;
+    float zp = round_to<T>(round_to<T>(-mn / sf) + qmin);
+    if (scale_qmap) {
+      sf = round_to<T>(bf2f(scale_qmap[f2bf(sf)]));
+      zp = round_to<T>(bf2f(scale_qmap[f2bf(zp)]));
+    }
+    if (!live) continue;
+    if (c % G == 0) {
+      if (scale_out) BT<T>::put(scale_out + c / G, BT<T>::round_bits(sf));
+      if (zp_out) BT<T>::put(zp_out + c / G, BT<T>::round_bits(zp));
+    }
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float q = __builtin_rintf(round_to<T>(round_to<T>(v[i] / sf) + zp));
+      q = q < qmin ? qmin : (q > qmax ? qmax : q);  // NaN stays NaN
+      o[i] = round_to<T>(q - zp) * sf;
+    }
+    if constexpr (sizeof(T) == 2) {
+      u32x4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)BT<T>::round_bits(o[2 * i]) | ((uint32_t)BT<T>::round_bits(o[2 * i + 1]) << 16);
+      *reinterpret_cast<u32x4*>(y + c * 8) = w;
+    } else {
+      *reinterpret_cast<float4*>(y + c * 8) = float4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<float4*>(y + c * 8 + 4) = float4{o[4], o[5], o[6], o[7]};
+    }
+  }
+}
+
+template <typename T>
+static void launch_gwa_rows(const void* x, int64_t n, int64_t bs, float qmin, float qmax, const uint16_t* sq,
+                            void* sc, void* zp, void* y, hipStream_t st) {
+  const int64_t nchunks = n / 8;
+  const unsigned grid = grid_for(nchunks, 256);
+  const T* xx = static_cast<const T*>(x);
+  T *s = static_cast<T*>(sc), *z = static_cast<T*>(zp), *yy = static_cast<T*>(y);
+  switch (bs) {
+    case 8: hipLaunchKernelGGL((gwa_fq_rows_kernel<T, 1>), dim3(grid), dim3(256), 0, st, xx, nchunks, qmin, qmax, sq, s, z, yy); break;
+    case 16: hipLaunchKernelGGL((gwa_fq_rows_kernel<T, 2>), dim3(grid), dim3(256), 0, st, xx, nchunks, qmin, qmax, sq, s, z, yy); break;
+    case 32: hipLaunchKernelGGL((gwa_fq_rows_kernel<T, 4>), dim3(grid), dim3(256), 0, st, xx, nchunks, qmin, qmax, sq, s, z, yy); break;
+    default: hipLaunchKernelGGL((gwa_fq_rows_kernel<T, 8>), dim3(grid), dim3(256), 0, st, xx, nchunks, qmin, qmax, sq, s, z, yy); break;
+  }
+}
+
 int gwa_fake_quant(const void* x, int dtype, int64_t outer, int64_t L, int64_t inner, int64_t bs, float qmin,
                    float qmax, const uint16_t* scale_qmap, void* scale_out, void* zp_out, void* y,
                    hipStream_t st) {
@@ -366,6 +460,15 @@ int gwa_fake_quant(const void* x, int dtype, int64_t outer, int64_t L, int64_t i
   const int64_t total = outer * ((L + bs - 1) / bs) * inner;
   if (total == 0) return kOk;
   if (!x || !y) return set_error(kErrInvalid, "gwa_fake_quant: null tensor");
+  const bool rows = inner == 1 && (bs == 8 || bs == 16 || bs == 32 || bs == 64) && L % bs == 0 &&
+                    aligned(x, 32) && aligned(y, 32) && (dtype == kBF16 || dtype == kF32);
+  if (rows) {
+    if (dtype == kBF16)
+      launch_gwa_rows<uint16_t>(x, outer * L, bs, qmin, qmax, scale_qmap, scale_out, zp_out, y, st);
+    else
+      launch_gwa_rows<float>(x, outer * L, bs, qmin, qmax, scale_qmap, scale_out, zp_out, y, st);
+    return check_launch("gwa_fake_quant");
+  }
   const unsigned grid = grid_for(total, 256);
   if (dtype == kBF16)
     hipLaunchKernelGGL(gwa_fq_kernel<uint16_t>, dim3(grid), dim3(256), 0, st, (const uint16_t*)x, outer, L, inner,
