@@ -171,7 +171,8 @@ def setup_c1(vqx, torch, L):
     n = x.numel()
     return (lambda: fn(*args)), dict(
         name="C1 posit8_1 fake-quant + uint8 codes, fp32 4096x4096 N(0,1) seed 0",
-        elements=n, bytes=9 * n, bound="hbm", dtype="f32->u8", cpu=cpu_c1(torch, xc))
+        elements=n, bytes=9 * n, bound="hbm", dtype="f32->u8", cpu=cpu_c1(torch, xc),
+        check=dict(x=xc, out=y, codes=codes))
 
 
 def c2_input(torch, rows=4096, cols=11008, seed=1):
@@ -201,7 +202,8 @@ def setup_c2(vqx, torch, L, decode=False):
         return (lambda: enc(*eargs)), dict(
             name="C2 NF4 block-64 absmax encode, bf16 4096x11008 N(0,0.02)+0.1% outliers seed 1 "
                  "-> packed 4-bit codes + fp32 scales",
-            elements=n, bytes=algo, bound="hbm", dtype="bf16->u4", cpu_input=xc)
+            elements=n, bytes=algo, bound="hbm", dtype="bf16->u4", cpu_input=xc,
+            check=dict(x=xc, codes=codes, scale=scale))
     enc(*eargs)
     out = torch.empty_like(x)
     dtab = fmt.tables(x.device)["decode"]
@@ -209,7 +211,8 @@ def setup_c2(vqx, torch, L, decode=False):
     dargs = (L.ptr(codes), 4, L.ptr(dtab), dtab.numel(), L.ptr(scale), 0, n, 64, L.ptr(out), L.BF16, st)
     return (lambda: dec(*dargs)), dict(
         name="C2 NF4 block-64 decode: packed codes + fp32 scales -> bf16 4096x11008",
-        elements=n, bytes=algo, bound="hbm", dtype="u4->bf16", cpu=cpu_c2_decode(torch, xc))
+        elements=n, bytes=algo, bound="hbm", dtype="u4->bf16", cpu=cpu_c2_decode(torch, xc),
+        check=dict(x=xc, codes=codes, scale=scale, out=out))
 
 
 def c3_input(torch, rows=8192, cols=8192, seed=2):
@@ -242,7 +245,8 @@ def setup_c3(vqx, torch, L, dtype, qmax, fake=False):
                 None, L.ptr(sc), None, None, None, L.ptr(y), None, 1, st)
         return (lambda: fn(*args)), dict(
             name=f"C3 MX block-32 {dtype} fake-quant (bf16 values + bf16 scales), bf16 8192x8192 Laplace seed 2",
-            elements=n, bytes=n * 4 + sc.numel() * 2, bound="hbm", dtype="bf16", cpu=cpu)
+            elements=n, bytes=n * 4 + sc.numel() * 2, bound="hbm", dtype="bf16", cpu=cpu,
+            check=dict(x=_C3_X["xc"], out=y, scale=sc))
     cb = fmt.code_bits
     codes = torch.empty(n * cb // 8, dtype=torch.uint8, device="cuda")
     e8 = torch.empty(8192, 256, dtype=torch.uint8, device="cuda")
@@ -250,7 +254,8 @@ def setup_c3(vqx, torch, L, dtype, qmax, fake=False):
             None, None, None, L.ptr(e8), None, None, L.ptr(codes), 0, st)
     return (lambda: fn(*args)), dict(
         name=f"C3 MX block-32 {dtype} + E8M0 scales, bf16 8192x8192 Laplace x 10^U(-1,1) seed 2 -> packed codes",
-        elements=n, bytes=n * 2 + n * cb // 8 + e8.numel(), bound="hbm", dtype=f"bf16->{dtype}", cpu=cpu)
+        elements=n, bytes=n * 2 + n * cb // 8 + e8.numel(), bound="hbm", dtype=f"bf16->{dtype}", cpu=cpu,
+        check=dict(x=_C3_X["xc"], codes=codes, scale=e8))
 
 
 def c4_codebooks(torch, rows, K, seed=3):
@@ -279,14 +284,16 @@ def setup_c4(vqx, torch, L, K, decode=False):
     if not decode:
         return (lambda: enc(*eargs)), dict(
             name=f"C4 per-channel codebook encode K={K}, fp32 4096x4096 N(0,1) seed 3 -> uint8 indices",
-            elements=n, bytes=algo, bound="hbm", dtype="f32->u8", cpu=cpu_c4(torch, xc, cbc, False))
+            elements=n, bytes=algo, bound="hbm", dtype="f32->u8", cpu=cpu_c4(torch, xc, cbc, False),
+            check=dict(x=xc, codebooks=cbc, codes=codes))
     enc(*eargs)
     out = torch.empty_like(x)
     dec = L.load().vqx_codebook_decode
     dargs = (L.ptr(codes), 4096, 4096, L.ptr(cb), K, L.ptr(out), L.F32, st)
     return (lambda: dec(*dargs)), dict(
         name=f"C4 per-channel codebook decode K={K}: uint8 indices -> fp32 4096x4096",
-        elements=n, bytes=algo, bound="hbm", dtype="u8->f32", cpu=cpu_c4(torch, xc, cbc, True))
+        elements=n, bytes=algo, bound="hbm", dtype="u8->f32", cpu=cpu_c4(torch, xc, cbc, True),
+        check=dict(x=xc, codebooks=cbc, codes=codes, out=out))
 
 
 def setup_c5(vqx, torch, L, whole_tiles=False, M=2048):
@@ -322,6 +329,36 @@ def setup_c5(vqx, torch, L, whole_tiles=False, M=2048):
              + how,
         elements=M * N, flops=2 * M * N * K, bytes=M * K * 2 + N * K // 2 + N * K // 64 * 4 + M * N * 2,
         bound="mfma", dtype="bf16", cpu=cpu_c5(torch, Ac, N), launches=launches, keep=keep)
+
+
+def setup_c5_linear_mx(vqx, torch, L, M=2048):
+    """C5 through the reference's own op: quantized_ops::linear_mx with the
+    operands convert_pt2e writes (bf16 code indices [11008, 4096], the 16 NF4
+    levels as weight_code, bf16 scales [11008, 64]).  The first call packs the
+    weight (cached); each step is one torch op call, whose fused kernel is
+    what the HIP events time (with the op's host dispatch hidden behind the
+    previous launch)."""
+    g = torch.Generator().manual_seed(4)
+    N, K = 11008, 4096
+    Ac = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    A = Ac.cuda()
+    idx = torch.randint(0, 16, (N, K), generator=g).to(torch.bfloat16).cuda()
+    scale = (torch.rand(N, K // 64, generator=g) * 0.05 + 0.001).to(torch.bfloat16).cuda()
+    # the 16 NF4 levels, ascending, as convert_pt2e's weight_code
+    code = vqx.parse_format("nf4").tables(A.device)["levels_bf16"].clone()
+    Q = torch.ops.quantized_ops
+
+    def launch():
+        Q.linear_mx(A, idx, None, weight_scale=scale, weight_code=code, block_size=64)
+        return 0
+
+    launch()  # packs the weight once
+    return launch, dict(
+        name=f"C5 via quantized_ops::linear_mx on convert-format operands: A bf16 [{M},4096], weight = bf16 NF4 "
+             f"indices [11008,4096] + weight_code (16 bf16 levels) + bf16 weight_scale [11008,64], block 64 -> bf16; "
+             f"the fused dequant MFMA kernel (weight packed once, cached)",
+        elements=M * N, flops=2 * M * N * K, bytes=M * K * 2 + N * K // 2 + N * K // 64 * 4 + M * N * 2,
+        bound="mfma", dtype="bf16", cpu=cpu_c5(torch, Ac, N), keep=(A, idx, scale, code))
 
 
 def setup_c5_skinny(vqx, torch, L, M):
@@ -497,6 +534,7 @@ CONFIGS = {
     "c4_k256": lambda v, t, L: setup_c4(v, t, L, 256),
     "c4_k16_decode": lambda v, t, L: setup_c4(v, t, L, 16, decode=True),
     "c5": lambda v, t, L: setup_c5(v, t, L),
+    "c5_linear_mx": lambda v, t, L: setup_c5_linear_mx(v, t, L),
     "c5_m256": lambda v, t, L: setup_c5(v, t, L, M=256),
     "c5_m1": lambda v, t, L: setup_c5_skinny(v, t, L, 1),
     "c5_m16": lambda v, t, L: setup_c5_skinny(v, t, L, 16),
@@ -654,11 +692,12 @@ DOMINANT = {
     "c4_k256": "cb_encode_kernel<float, 8>",
     "c4_k16_decode": "cb_decode_kernel<float>",
     "c5": "nf4_gemm_kernel",
+    "c5_linear_mx": "nf4_gemm_kernel",
     "c5_m256": "nf4_gemm_sk_kernel",
     "c5_m256_whole_tiles": "nf4_gemm_kernel",
     "c5_m1": "nf4_skinny_kernel",
     "c5_m16": "nf4_skinny_kernel",
-    "f3_gwa": "gwa_fq_kernel<unsigned short>",
+    "f3_gwa": "gwa_fq_rows_kernel<unsigned short, 8>",
     "o1_filter": "outlier_split_kernel<1, 8>",
     "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8, true, 4>",
     "o3_spmm": "spmm_csr_kernel<1, 8>",

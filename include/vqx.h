@@ -264,6 +264,26 @@ int vqx_nf4_linear_ws(const uint16_t* A, const uint8_t* codes, const float* scal
                       int64_t workspace_bytes, vqx_stream_t stream);
 
 /*
+ * The operands of vqx_nf4_linear from the convert format that linear_mx /
+ * matmul_mx receive after convert_pt2e (src/vc/quantization/quantize_pt2e.py:
+ * 456-508 stores the weight as integer-valued code indices in a float tensor,
+ * the levels as weight_code and one scale per 64-element block along K;
+ * src/vc/ops/quantized.py:319-326 decodes them as
+ * weight_code[weight.to(long)] * expand(weight_scale)).
+ * weight: [N, K] (transposed = 0, linear_mx "kc" / matmul_mx "kc") or [K, N]
+ * (transposed = 1, "ck"), dtype F32, BF16 or F16; scale: [N, K/64] or
+ * [K/64, N] in F32, BF16 or F16, or NULL (all ones).  Writes codes: packed
+ * 4-bit [N, K/2] (8-byte aligned) and scale_out: fp32 [N, K/64], which widen
+ * the scale exactly.  Index = trunc(w), a negative index counting from the
+ * end of the ncode-entry table (1..16); a NaN, an infinity or an index out of
+ * range sets *bad to 1 (device int, cleared by the caller; the reference
+ * raises IndexError there).  K % 64 == 0.
+ */
+int vqx_nf4_pack_weight(const void* weight, int32_t w_dtype, const void* scale, int32_t s_dtype, int64_t N,
+                        int64_t K, int32_t transposed, int32_t ncode, uint8_t* codes, float* scale_out,
+                        int32_t* bad, vqx_stream_t stream);
+
+/*
  * quantized_ops::filter_outlier (src/vc/ops/quantized.py:532-630, with
  * _pad_csr at :537-569), and the outlier half of quantize_mx_outlier
  * (:633-712, indptr_offset added to the row pointers).

@@ -28,6 +28,7 @@ __all__ = [
     "group_wise_affine_fake_quant",
     "fake_quantize_per_tensor",
     "codebook_encode_rows",
+    "convert_weight",
     "codebook_decode_rows",
     "linear_mx",
     "filter_outlier",
@@ -205,6 +206,20 @@ def _decode_mx(t, code, scale, block_size):
     if scale is not None:
         t = t * expand(scale, t.shape, block_size)
     return t
+
+
+def convert_weight(weight, table, axes, block_size, quant_max, force_scale_power_of_two=False, scale_qmap=None):
+    """Convert-time quantization of a weight parameter with a codebook-style
+    (NF) table, src/vc/quantization/quantize_pt2e.py:456-500: the table's
+    distinct values become the code (``unique``), the table becomes an index
+    table (``searchsorted``), the scale comes from calculate_mx_qparam and the
+    stored weight is quantize() through the index table, i.e. integer-valued
+    indices in the weight's dtype.  Returns (weight indices, scale, code)."""
+    values = torch.unique(table)
+    indices = torch.searchsorted(values, table).to(torch.int64)
+    scale = calculate_mx_qparam(weight, axes, block_size, quant_max, force_scale_power_of_two, scale_qmap)
+    w = quantize(weight, scale, None, axes, block_size, indices)
+    return w, scale, values
 
 
 def linear_mx(x, weight, bias=None, weight_scale=None, block_size=None, weight_code=None, input_scale=None,

@@ -263,6 +263,15 @@ int vqx_nf4_linear_ws(const uint16_t* A, const uint8_t* codes, const float* scal
   return nf4_gemm(A, codes, scale, levels, bias, out, M, N, K, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
+int vqx_nf4_pack_weight(const void* weight, int32_t w_dtype, const void* scale, int32_t s_dtype, int64_t N,
+                        int64_t K, int32_t transposed, int32_t ncode, uint8_t* codes, float* scale_out,
+                        int32_t* bad, vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (!weight || !codes || !scale_out || !bad) return set_error(kErrInvalid, "nf4_pack_weight: null buffer");
+  return nf4_pack(weight, w_dtype, scale, s_dtype, N, K, transposed, ncode, codes, scale_out, bad,
+                  (hipStream_t)stream);
+}
+
 int vqx_filter_outlier(const void* x, int32_t x_dtype, int64_t batches, int64_t rows, int64_t cols,
                        float threshold, int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices,
                        int32_t* indptr, void* inlier, vqx_stream_t stream) {

@@ -652,6 +652,104 @@ static SkPlan plan_stream_k(int64_t M, int64_t N, int64_t K) {
 
 int64_t nf4_gemm_workspace(int64_t M, int64_t N, int64_t K) { return plan_stream_k(M, N, K).bytes; }
 
+// ---------------------------------------------------------------------------
+// The packed operands from linear_mx's convert format
+// (src/vc/quantization/quantize_pt2e.py:456-508: the weight holds integer-
+// valued code indices in a float tensor, weight_code the levels, weight_scale
+// one value per 64-element block along K).  The index of element (n, k) is
+// trunc(w) (torch's .to(long)); a negative index counts from the end of the
+// code table, as torch's indexing does (quantized.py:319-320).  A NaN, an
+// infinity or an index outside the table sets *bad: the reference raises
+// IndexError there, and the caller takes the unfused path.  transposed: the
+// weight is stored [K, N] ("ck") with its scale [K/64, N]; otherwise [N, K]
+// and [N, K/64].  One 64 (n) x 64 (k) tile per loop trip: thread t packs 16
+// codes of column n0 + t / 4, from its own loads ([N, K]) or through an LDS
+// transpose ([K, N]); threads 0-63 convert the tile's 64 scales to fp32.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float elem_as_f32(const void* p, int dt, int64_t i) {
+  if (dt == kF32) return static_cast<const float*>(p)[i];
+  const uint32_t h = static_cast<const uint16_t*>(p)[i];
+  return dt == kBF16 ? bf2f(h) : h2f_exact(h);
+}
+
+__device__ __forceinline__ uint32_t code_index(float v, int ncode, bool& bad) {
+  // |v| < ncode + 1 keeps the truncation in int range and fails NaN / Inf
+  if (!(__builtin_fabsf(v) < (float)(ncode + 1))) {
+    bad = true;
+    return 0;
+  }
+  int k = (int)v;  // toward zero
+  if (k < 0) k += ncode;
+  if (k < 0 || k >= ncode) {
+    bad = true;
+    return 0;
+  }
+  return (uint32_t)k;
+}
+
+__global__ __launch_bounds__(256) void nf4_pack_kernel(const void* __restrict__ w, int wdt,
+                                                       const void* __restrict__ s, int sdt, int N, int K,
+                                                       int transposed, int ncode, uint8_t* __restrict__ codes,
+                                                       float* __restrict__ scale_out, int* __restrict__ bad) {
+  __shared__ uint8_t idx[64][65];  // [k][n] of a transposed tile
+  const int t = threadIdx.x;
+  const int tn = (N + 63) / 64, kb = K / 64;
+  const int64_t ntiles = (int64_t)tn * kb;
+  bool my_bad = false;
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int n0 = (int)(tile % tn) * 64, b = (int)(tile / tn), k0 = b * 64;
+    const int n = n0 + (t >> 2), kq = 16 * (t & 3);
+    uint32_t c[16];
+    if (!transposed) {
+      if (n < N) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) c[j] = code_index(elem_as_f32(w, wdt, (int64_t)n * K + k0 + kq + j), ncode, my_bad);
+      }
+    } else {
+      // load: row k0 + t / 4 of [K, N], columns n0 + 16 (t % 4) .. + 15
+      const int kr = k0 + (t >> 2);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int nc = n0 + kq + j;
+        idx[t >> 2][kq + j] = nc < N ? (uint8_t)code_index(elem_as_f32(w, wdt, (int64_t)kr * N + nc), ncode, my_bad) : 0;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 16; ++j) c[j] = idx[kq + j][t >> 2];
+      __syncthreads();
+    }
+    if (n < N) {
+      u32x2 v = {0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j >> 2] |= (c[2 * j] | c[2 * j + 1] << 4) << (8 * (j & 3));
+      *reinterpret_cast<u32x2*>(codes + (size_t)n * (K / 2) + (k0 + kq) / 2) = v;
+    }
+    if (t < 64 && n0 + t < N) {
+      const int sn = n0 + t;
+      scale_out[(size_t)sn * kb + b] =
+          s ? elem_as_f32(s, sdt, transposed ? (int64_t)b * N + sn : (int64_t)sn * kb + b) : 1.0f;
+    }
+  }
+  if (my_bad) atomicOr(bad, 1);
+}
+
+int nf4_pack(const void* weight, int w_dtype, const void* scale, int s_dtype, int64_t N, int64_t K, int transposed,
+             int ncode, uint8_t* codes, float* scale_out, int* bad, hipStream_t st) {
+  if (N <= 0 || K <= 0) return set_error(kErrInvalid, "nf4_pack: empty shape");
+  if (N > (1 << 30) || K > (1 << 30)) return set_error(kErrInvalid, "nf4_pack: shape too large");
+  if (K % 64) return set_error(kErrUnsupported, "nf4_pack: needs K %% 64 == 0 (got K = %lld)", (long long)K);
+  if (ncode < 1 || ncode > 16) return set_error(kErrInvalid, "nf4_pack: code tables of 1..16 entries (got %d)", ncode);
+  if (w_dtype != kF32 && w_dtype != kBF16 && w_dtype != kF16)
+    return set_error(kErrInvalid, "nf4_pack: weight dtype must be F32, BF16 or F16");
+  if (scale && s_dtype != kF32 && s_dtype != kBF16 && s_dtype != kF16)
+    return set_error(kErrInvalid, "nf4_pack: scale dtype must be F32, BF16 or F16");
+  if (!aligned(codes, 8) || !aligned(scale_out, 4)) return set_error(kErrInvalid, "nf4_pack: codes must be 8-byte aligned");
+  const int64_t tiles = (N + 63) / 64 * (K / 64);
+  hipLaunchKernelGGL(nf4_pack_kernel, dim3(grid_for(tiles, 1, 8)), dim3(256), 0, st, weight, w_dtype, scale, s_dtype,
+                     (int)N, (int)K, transposed, ncode, codes, scale_out, bad);
+  return check_launch("nf4_pack");
+}
+
 int nf4_gemm(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
              const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, void* workspace,
              int64_t workspace_bytes, hipStream_t st) {

@@ -440,15 +440,19 @@ def gwa_fake_quantize(input, axis, block_size, quant_min, quant_max, scale_qmap=
 
 
 # ---------------------------------------------------------------------------
-# linear_mx / matmul_mx  (quantized.py:286-432): decode on the GPU, then the
-# dense product (hipBLASLt).  The fused NF4 product is linear_nf4.
+# linear_mx / matmul_mx  (quantized.py:286-432): a convert-format weight
+# with up to 16 levels and blocks of 64 runs the fused dequant product;
+# other operands decode on the GPU, then the dense product (hipBLASLt).
 # ---------------------------------------------------------------------------
 _CODE_LUTS = {}
 
 
 def _code_lut(code: torch.Tensor) -> torch.Tensor:
-    """65536-entry table sending the bf16 pattern of k to code[k] (the
-    reference indexes ``code[x.long()]`` with integer-valued x)."""
+    """65536-entry table sending each bf16 pattern x to code[x.long()] as the
+    reference indexes it (quantized.py:313-320): x truncated toward zero, a
+    negative index counting from the end.  Patterns whose index falls outside
+    the table (and NaN / Inf) map to NaN, where the reference raises
+    IndexError."""
     key = (code.data_ptr(), code._version, code.numel(), code.dtype)
     hit = _CODE_LUTS.get(key)
     if hit is not None and hit[0]() is code:
@@ -456,10 +460,11 @@ def _code_lut(code: torch.Tensor) -> torch.Tensor:
     K = code.numel()
     if K > 256:
         raise ValueError("code tables hold at most 256 entries")
-    lut = torch.zeros(65536, dtype=torch.bfloat16, device=code.device)
-    ks = torch.arange(K, device=code.device, dtype=torch.float32).to(torch.bfloat16)
-    idx = ks.view(torch.int16).to(torch.int64) & 0xFFFF
-    lut[idx] = code.reshape(-1).to(torch.bfloat16)
+    v = torch.arange(65536, dtype=torch.int32, device=code.device).to(torch.int16).view(torch.bfloat16).float()
+    t = torch.trunc(v)
+    ok = torch.isfinite(v) & (t >= -K) & (t < K)
+    idx = torch.where(ok, t, torch.zeros_like(t)).to(torch.int64) % K
+    lut = torch.where(ok, code.reshape(-1).to(torch.bfloat16)[idx], torch.full_like(v, float("nan")).to(torch.bfloat16))
     _CODE_LUTS[key] = (weakref.ref(code), lut)
     return lut
 
@@ -484,8 +489,13 @@ def _decode_operand(t, code, scale, block_size):
         return t
     if code is not None and t.dtype != torch.bfloat16 and not _bf16_exact(code):
         # code values finer than bf16 in a wider operand: the reference's
-        # gather by integer value (quantized.py:313-315), then the scales
-        t = code.to(t.device)[t.to(torch.long)].to(t.dtype)
+        # gather by integer value (quantized.py:313-315), then the scales;
+        # indices outside the table give NaN (the reference raises there)
+        K = code.numel()
+        tr = torch.trunc(t.float())
+        ok = torch.isfinite(tr) & (tr >= -K) & (tr < K)
+        idx = torch.where(ok, tr, torch.zeros_like(tr)).to(torch.long) % K
+        t = torch.where(ok, code.to(t.device).reshape(-1)[idx].to(t.dtype), torch.full_like(t, float("nan")))
         code = None
         if scale is None:
             return t
@@ -498,20 +508,132 @@ def _decode_operand(t, code, scale, block_size):
     return dequantize(t, scale, None, None, block_size, lut, None)
 
 
+# The fused product.  A converted model's GEMM arrives as linear_mx /
+# matmul_mx with the weight in convert format (quantize_pt2e.py:456-508, the
+# rewrite at :592-645): integer-valued code indices in a bf16 tensor, at most
+# 16 bf16 levels in weight_code, bf16 scales with blocks of 64 along K.  The
+# reference decodes that into a dense bf16 weight, bf16(level * scale), and
+# calls aten.linear / aten.matmul.  Here the operands are packed once per
+# weight (4-bit codes, the scales widened exactly to fp32) and the decode runs
+# inside the bf16 MFMA product (vqx_nf4_linear_ws), which computes the same
+# bf16(level * scale) values.  The packing is cached per weight tensor and
+# redone when any of the three operands changes (tensor version counters).
+class _Packed:
+    __slots__ = ("refs", "versions", "codes", "scale", "levels")
+
+
+_PACKED = {}
+
+
+def _release_packed(key):
+    _PACKED.pop(key, None)
+
+
+def _packed_weight(weight, weight_code, weight_scale, transposed):
+    """Packed (codes, fp32 scales, 16 bf16 levels) of a convert-format weight,
+    or None when an index is out of the code table's range (the unfused
+    path then reproduces the reference's behaviour)."""
+    key = (id(weight), bool(transposed))
+    deps = (weight, weight_code, weight_scale)
+    versions = tuple(None if t is None else (t.data_ptr(), t._version) for t in deps)
+    hit = _PACKED.get(key)
+    if hit is not None and hit.versions == versions and all(
+            (r is None and t is None) or (r is not None and r() is t) for r, t in zip(hit.refs, deps)):
+        return None if hit.codes is None else (hit.codes, hit.scale, hit.levels)
+    K, N = weight.shape if transposed else weight.shape[::-1]
+    dev = weight.device
+    w = weight.contiguous()
+    s = None if weight_scale is None else weight_scale.to(dev).contiguous()
+    ncode = weight_code.numel()
+    codes = torch.empty(N, K // 2, dtype=torch.uint8, device=dev)
+    scale32 = torch.empty(N, K // 64, dtype=torch.float32, device=dev)
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.call("vqx_nf4_pack_weight", _lib.ptr(w), _lib.dtype_tag(w.dtype), _lib.ptr(s),
+              0 if s is None else _lib.dtype_tag(s.dtype), N, K, 1 if transposed else 0, ncode, _lib.ptr(codes),
+              _lib.ptr(scale32), _lib.ptr(bad), _lib.stream_of(w))
+    levels = torch.zeros(16, dtype=torch.bfloat16, device=dev)
+    levels[:ncode] = weight_code.reshape(-1).to(device=dev, dtype=torch.bfloat16)
+    entry = _Packed()
+    entry.refs = tuple(None if t is None else weakref.ref(t) for t in deps)
+    entry.versions = versions
+    # one host read per packing (not per call): whether every index was valid
+    if int(bad.item()):
+        entry.codes = entry.scale = entry.levels = None
+    else:
+        entry.codes, entry.scale, entry.levels = codes, scale32, levels
+    if hit is None:
+        weakref.finalize(weight, _release_packed, key)
+    _PACKED[key] = entry
+    return None if entry.codes is None else (entry.codes, entry.scale, entry.levels)
+
+
+def _fusable(x, weight, bias, weight_scale, block_size, weight_code, transposed):
+    """Whether the product of x with this weight can run fused: bf16
+    activations, a 2-D bf16 index weight with a code table of at most 16
+    entries, bf16 scales in blocks of 64 along K (the reference's decoded
+    weight is then bf16, as aten.linear needs), a bf16 bias, K % 64, and for
+    more than 16 rows N % 128 (the tile kernel's column tiles)."""
+    if weight_code is None or weight.dim() != 2 or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        return False
+    if weight_code.dim() != 1 or not 1 <= weight_code.numel() <= 16 or weight_code.device != weight.device:
+        return False
+    K, N = weight.shape if transposed else weight.shape[::-1]
+    if x.shape[-1] != K or K % 64 or not x.is_cuda or weight.device != x.device:
+        return False
+    if weight_scale is not None:
+        want = (K // 64, N) if transposed else (N, K // 64)
+        if block_size != 64 or weight_scale.dtype != torch.bfloat16 or tuple(weight_scale.shape) != want:
+            return False
+    if bias is not None and (bias.dtype != torch.bfloat16 or tuple(bias.shape) != (N,) or bias.device != x.device):
+        return False
+    M = x.numel() // K
+    return M > 0 and (M <= 16 or N % 128 == 0)
+
+
+def _nf4_product(x2d, codes, scale32, levels, bias, N):
+    """out[M, N] = x2d . decode(codes, scale32, levels)^T (+ bias) through the
+    fused kernel, launched on x's current stream."""
+    M, K = x2d.shape
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=x2d.device)
+    ws_bytes = _nf4_workspace_bytes(M, N, K, x2d.device)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x2d.device) if ws_bytes else None
+    _lib.call("vqx_nf4_linear_ws", _lib.ptr(x2d), _lib.ptr(codes), _lib.ptr(scale32), _lib.ptr(levels),
+              _lib.ptr(bias), _lib.ptr(out), M, N, K, _lib.ptr(ws), ws_bytes, _lib.stream_of(x2d))
+    return out
+
+
+def _fused_linear(x, weight, bias, weight_scale, weight_code, transposed):
+    packed = _packed_weight(weight, weight_code, weight_scale, transposed)
+    if packed is None:
+        return None
+    K = x.shape[-1]
+    N = weight.shape[1] if transposed else weight.shape[0]
+    b = None if bias is None else bias.contiguous()
+    out = _nf4_product(x.reshape(-1, K).contiguous(), *packed, b, N)
+    return out.reshape(*x.shape[:-1], N)
+
+
 @_impl("linear_mx")
 def linear_mx(input, weight, bias=None, *, input_scale=None, weight_scale=None, block_size=None,
               input_code=None, weight_code=None, A_data=None, A_indices=None, A_indptr=None,
               weight_layout="kc"):
+    """quantized.py:295-348.  A convert-format weight (bf16 indices, up to 16
+    bf16 levels, bf16 scales in blocks of 64 along K) with bf16 activations
+    runs the fused NF4-style product; anything else decodes on the GPU and
+    calls the library GEMM."""
     assert weight_layout in ("kc", "ck"), weight_layout
     _lib.require_device(input, "linear_mx")
     x = _decode_operand(input, input_code, input_scale, block_size)
-    w = _decode_operand(weight, weight_code, weight_scale, block_size)
-    if weight_code is not None:
-        w = w.to(weight.dtype)
-    if weight_layout == "kc":
-        dense = torch.nn.functional.linear(x, w, bias)
-    else:
-        dense = torch.ops.quantized_ops.linear(x, w, bias)
+    transposed = weight_layout == "ck"
+    dense = None
+    if _fusable(x, weight, bias, weight_scale, block_size, weight_code, transposed):
+        dense = _fused_linear(x, weight, bias, weight_scale, weight_code, transposed)
+    if dense is None:
+        w = _decode_operand(weight, weight_code, weight_scale, block_size)
+        if weight_layout == "kc":
+            dense = torch.nn.functional.linear(x, w, bias)
+        else:
+            dense = torch.ops.quantized_ops.linear(x, w, bias)
     if A_data is None:
         return dense
     return _spmm(A_data, A_indices, A_indptr, weight, weight_scale, weight_code, block_size, weight_layout,
@@ -521,14 +643,22 @@ def linear_mx(input, weight, bias=None, *, input_scale=None, weight_scale=None, 
 @_impl("matmul_mx")
 def matmul_mx(self, other, *, input_scale=None, weight_scale=None, block_size=None, input_code=None,
               weight_code=None, A_data=None, A_indices=None, A_indptr=None, weight_layout="ck"):
+    """quantized.py:371-421.  A 2-D convert-format right operand ([K, N] for
+    "ck", [N, K] for "kc") with bf16 left operands runs the fused product, as
+    in linear_mx; anything else decodes and calls the library GEMM."""
     assert weight_layout in ("kc", "ck"), weight_layout
     _lib.require_device(self, "matmul_mx")
     a = _decode_operand(self, input_code, input_scale, block_size)
-    b = _decode_operand(other, weight_code, weight_scale, block_size)
-    if weight_layout == "ck":
-        dense = torch.matmul(a, b.contiguous())
-    else:
-        dense = torch.ops.quantized_ops.matmul(a, b)
+    transposed = weight_layout == "ck"
+    dense = None
+    if a.dim() >= 1 and _fusable(a, other, None, weight_scale, block_size, weight_code, transposed):
+        dense = _fused_linear(a, other, None, weight_scale, weight_code, transposed)
+    if dense is None:
+        b = _decode_operand(other, weight_code, weight_scale, block_size)
+        if weight_layout == "ck":
+            dense = torch.matmul(a, b.contiguous())
+        else:
+            dense = torch.ops.quantized_ops.matmul(a, b)
     if A_data is None:
         return dense
     return _spmm(A_data, A_indices, A_indptr, other, weight_scale, weight_code, block_size, weight_layout,
@@ -929,13 +1059,8 @@ def linear_nf4(input, codes, scale, bias=None, block_size=64, dtype="nf4"):
     if scale.shape[-1] * 64 != K or codes.numel() * 2 != N * K:
         raise ValueError("codes / scale shapes do not match the input's K")
     lv = fmt.tables(x.device)["levels_bf16"]
-    out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
     b = None if bias is None else bias.to(device=x.device, dtype=torch.bfloat16).contiguous()
-    ws_bytes = _nf4_workspace_bytes(M, N, K, x.device)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
-    _lib.call("vqx_nf4_linear_ws", _lib.ptr(x), _lib.ptr(codes.contiguous()),
-              _lib.ptr(scale.to(torch.float32).contiguous()), _lib.ptr(lv), _lib.ptr(b), _lib.ptr(out),
-              M, N, K, _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
+    out = _nf4_product(x, codes.contiguous(), scale.to(torch.float32).contiguous(), lv, b, N)
     return out.reshape(*input.shape[:-1], N)
 
 
