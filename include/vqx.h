@@ -264,6 +264,22 @@ int vqx_nf4_linear_ws(const uint16_t* A, const uint8_t* codes, const float* scal
                       int64_t workspace_bytes, vqx_stream_t stream);
 
 /*
+ * vqx_nf4_linear_ws without a workspace argument and without any allocation:
+ * the same product, the same stream-K plan and therefore the same bits.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The workspace is a device array of the library,
+ * 64 MiB + 1 KiB, which each GPU the library runs on holds until the process
+ * ends; a shape whose plan needs more (a device with more than 256 CUs)
+ * returns VQX_ERR_UNSUPPORTED.  Every call on one GPU shares that array: the
+ * call clears what must start at zero on `stream` before using it, and calls
+ * that overlap on one GPU (other streams, other threads) race.
+ */
+int vqx_nf4_linear_noalloc(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
+                           const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K,
+                           vqx_stream_t stream);
+
+/*
  * The operands of vqx_nf4_linear from the convert format that linear_mx /
  * matmul_mx receive after convert_pt2e (src/vc/quantization/quantize_pt2e.py:
  * 456-508 stores the weight as integer-valued code indices in a float tensor,

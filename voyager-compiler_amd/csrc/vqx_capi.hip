@@ -263,6 +263,14 @@ int vqx_nf4_linear_ws(const uint16_t* A, const uint8_t* codes, const float* scal
   return nf4_gemm(A, codes, scale, levels, bias, out, M, N, K, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
+int vqx_nf4_linear_noalloc(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
+                           const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K,
+                           vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (!A || !codes || !scale || !levels || !out) return set_error(kErrInvalid, "nf4_linear: null buffer");
+  return nf4_gemm_noalloc(A, codes, scale, levels, bias, out, M, N, K, (hipStream_t)stream);
+}
+
 int vqx_nf4_pack_weight(const void* weight, int32_t w_dtype, const void* scale, int32_t s_dtype, int64_t N,
                         int64_t K, int32_t transposed, int32_t ncode, uint8_t* codes, float* scale_out,
                         int32_t* bad, vqx_stream_t stream) {

@@ -95,6 +95,8 @@ int nf4_gemm(const uint16_t* A, const uint8_t* codes, const float* scale, const 
              const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, void* workspace,
              int64_t workspace_bytes, hipStream_t st);
 int64_t nf4_gemm_workspace(int64_t M, int64_t N, int64_t K);
+int nf4_gemm_noalloc(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
+                     const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, hipStream_t st);
 int nf4_pack(const void* weight, int w_dtype, const void* scale, int s_dtype, int64_t N, int64_t K, int transposed,
              int ncode, uint8_t* codes, float* scale_out, int* bad, hipStream_t st);
 

@@ -28,6 +28,7 @@
 // in its L2 while W streams past.  A partial last row tile runs as a launch
 // of its own that loads row M - 1 in place of the missing rows and stores
 // only rows < M.  M <= 16 takes the skinny kernel further down instead.
+#include <mutex>
 #include <type_traits>
 
 #include "vqx_kernels.h"
@@ -651,6 +652,56 @@ static SkPlan plan_stream_k(int64_t M, int64_t N, int64_t K) {
 }
 
 int64_t nf4_gemm_workspace(int64_t M, int64_t N, int64_t K) { return plan_stream_k(M, N, K).bytes; }
+
+// ---------------------------------------------------------------------------
+// Allocation-free form of nf4_gemm with a workspace: the workspace is
+// `scratch`, a device array of this library that each GPU holds for the
+// life of the process.  Its size covers every stream-K plan on a device of up
+// to 256 CUs: two 256 x 128 fp32 partial tiles per CU plus the tile counters
+// (64 MiB + 1 KiB).  A plan that needs more (a device with more CUs) is
+// rejected.  In host code `scratch` names a host-side stand-in, so kernels get
+// its device address, looked up once per device with that device current.
+// Every call on one device shares the array: the counters are cleared on the
+// stream ahead of the split launch (by nf4_gemm, as with a caller's
+// workspace), the partial slots need no initial contents, and calls that
+// overlap on one device race.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchBytes = (64ll << 20) + 1024;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(kErrLaunch, "nf4_linear_noalloc: no current device (or device index >= %d)", kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(kErrLaunch, "nf4_linear_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return kOk;
+}
+
+int nf4_gemm_noalloc(const uint16_t* A, const uint8_t* codes, const float* scale, const uint16_t* levels,
+                     const uint16_t* bias, uint16_t* out, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  const int64_t need = plan_stream_k(M, N, K).bytes;
+  if (need > kScratchBytes)
+    return set_error(kErrUnsupported, "nf4_linear_noalloc: this shape needs %lld bytes of scratch, the maximum is %lld",
+                     (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(&ws);
+  if (rc != kOk) return rc;
+  return nf4_gemm(A, codes, scale, levels, bias, out, M, N, K, need > 0 ? ws : nullptr, need > 0 ? kScratchBytes : 0,
+                  st);
+}
 
 // ---------------------------------------------------------------------------
 // The packed operands from linear_mx's convert format
