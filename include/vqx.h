@@ -102,6 +102,26 @@ int vqx_vmap(const void* x, int32_t x_dtype, int64_t n, const uint16_t* table, v
              vqx_stream_t stream);
 
 /*
+ * FusedAmaxObsFakeQuantize.forward with the observer on, per-tensor or
+ * per-channel qscheme (src/vc/quantization/fake_quantize.py:308-341 observer
+ * step, :418-426 forward, :112-115 fake-quant), on the device and without a
+ * host synchronisation.  Element i of x belongs to channel
+ * (i / inner) % channels (channels = 1: per-tensor).  amax_history: fp32
+ * [history_len, channels] and scale: fp32 [channels], read and updated in
+ * place exactly as the reference updates its buffers: the scale is the
+ * history's maximum from before this step divided by quant_max (IEEE fp32),
+ * kept where that maximum is not positive or not finite, optionally
+ * 2 ** ceil(log2(scale)) as torch computes it on the CPU; the history is
+ * rolled by one and row 0 becomes this step's max |x| per channel (NaN if
+ * any element is NaN).  y (NULL: observe only) = vmap(x / s, qmap) * s with
+ * the new scale s in x's dtype.  Two launches (the scales, then one pass over
+ * x).  n > 0, a multiple of channels * inner.
+ */
+int vqx_amax_observe_fake_quant(const void* x, int32_t x_dtype, int64_t n, int64_t channels, int64_t inner,
+                                const vqx_format* fmt, float* amax_history, int32_t history_len, float* scale,
+                                float quant_max, int32_t force_scale_power_of_two, void* y, vqx_stream_t stream);
+
+/*
  * FakeQuantizeFunction.forward  (src/vc/quantization/fake_quantize.py:101-115)
  * and quantized_ops::quantize without block_size (src/vc/ops/quantized.py:131-172):
  *   y = vmap(x / s, qmap) * s   (mul_back = 1)   or   y = vmap(x / s, qmap)

@@ -29,6 +29,7 @@ __all__ = [
     "fake_quantize_per_tensor",
     "codebook_encode_rows",
     "convert_weight",
+    "AmaxObserverFakeQuantize",
     "codebook_decode_rows",
     "linear_mx",
     "filter_outlier",
@@ -173,6 +174,59 @@ def fake_quantize_per_tensor(x, qmap, scale):
     """FakeQuantizeFunction.forward (src/vc/quantization/fake_quantize.py:112-115)."""
     s = scale.to(x.dtype)
     return vmap(x / s, qmap) * s
+
+
+class AmaxObserverFakeQuantize:
+    """The per-tensor / per-channel branch of FusedAmaxObsFakeQuantize
+    (src/vc/quantization/fake_quantize.py:219-463) on CPU tensors: state
+    (amax_history, scale, the two enable flags) and forward (:404-432), with
+    the observer step _update_amax_scale (:308-341) and FakeQuantizeFunction
+    (:112-115).  The amax is taken over every axis, or every axis but ch_axis
+    when per_channel; the scale comes from the history's maximum before this
+    step's amax goes in."""
+
+    def __init__(self, qmap, quant_max, amax_history_len, per_channel=False, ch_axis=None,
+                 force_scale_power_of_two=False):
+        self.qmap = qmap
+        self.quant_max = quant_max
+        self.amax_history_len = amax_history_len
+        self.per_channel = per_channel
+        self.ch_axis = ch_axis
+        self.force_scale_power_of_two = force_scale_power_of_two
+        self.amax_history = torch.tensor([], dtype=torch.float32)
+        self.scale = torch.tensor([1.0], dtype=torch.float32)
+        self.observer_enabled = True
+        self.fake_quant_enabled = True
+
+    @torch.no_grad()
+    def update(self, x):
+        """src/vc/quantization/fake_quantize.py:318-341."""
+        if self.per_channel:
+            ch_axis = self.ch_axis % x.ndim
+            dim = tuple(i for i in range(x.ndim) if i != ch_axis)
+            amax_cur = torch.amax(torch.abs(x), dim=dim, keepdim=True)
+        else:
+            amax_cur = torch.amax(torch.abs(x))
+        if self.amax_history.numel() == 0:
+            self.amax_history = torch.zeros((self.amax_history_len,) + amax_cur.shape, dtype=torch.float32)
+            self.scale = torch.ones(amax_cur.shape, dtype=torch.float32)
+        amax = torch.amax(self.amax_history, dim=0)
+        self.amax_history = torch.roll(self.amax_history, -1, 0)
+        self.amax_history[0] = amax_cur
+        sf = amax / self.quant_max
+        sf = torch.where(amax > 0.0, sf, self.scale)
+        sf = torch.where(torch.isfinite(amax), sf, self.scale)
+        if self.force_scale_power_of_two:
+            sf = torch.pow(2, torch.ceil(torch.log2(sf)))
+        self.scale = sf.clone()
+
+    def __call__(self, x):
+        """src/vc/quantization/fake_quantize.py:418-426."""
+        if self.observer_enabled:
+            self.update(x)
+        if not self.fake_quant_enabled:
+            return x
+        return fake_quantize_per_tensor(x, self.qmap, self.scale)
 
 
 def codebook_encode_rows(x, cb):

@@ -5,6 +5,12 @@
 
 extern "C" {
 
+// 2 ** ceil(log2(f)) of fp32 bit patterns (the observer's power-of-two scale).
+int vqx_host_pow2_ceil_log2(const uint32_t* in, int64_t n, uint32_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = vqx::pow2_ceil_log2_f32(in[i]);
+  return 0;
+}
+
 // kind/params follow vqx::FormatKind; levels/boundaries for kFmtLevels.
 int vqx_host_encode(int kind, int p0, int p1, float max_norm, int flags,
                     const float* boundaries, const uint16_t* levels, int nlev,

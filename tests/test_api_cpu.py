@@ -146,6 +146,31 @@ def test_fake_quantize_module_state_on_cpu(vqx):
     assert not bool(fq2.observer_enabled[0])
 
 
+def test_fake_quantize_flags_follow_the_buffers(vqx):
+    # the enable flags are buffers: a loaded state_dict, an in-place write
+    # (lcq.py writes fake_quant_enabled.zero_() / .copy_()) and the enable /
+    # disable methods all take effect on the next forward
+    from voyager_compiler_amd.quantization import QuantizationSpec
+
+    spec = QuantizationSpec.from_str("int8,qs=per_tensor_symmetric,ahl=2")
+    fq = spec.make_fake_quantize()
+    assert fq._observer_on() and fq._fake_quant_on()
+    sd = {k: v.clone() for k, v in fq.state_dict().items()}
+    sd["observer_enabled"].zero_()
+    sd["fake_quant_enabled"].zero_()
+    fq.load_state_dict(sd)
+    assert not fq._observer_on() and not fq._fake_quant_on()
+    fq.fake_quant_enabled.copy_(torch.ones(1, dtype=torch.uint8))
+    assert fq._fake_quant_on() and not fq._observer_on()
+    fq.observer_enabled[0] = 1
+    assert fq._observer_on()
+    fq.disable_observer()
+    fq.fake_quant_enabled.zero_()
+    assert not fq._observer_on() and not fq._fake_quant_on()
+    fq.enable_fake_quant()
+    assert fq._fake_quant_on()
+
+
 def _stream_k_bytes(M, N, K, cus=256):
     """The NF4 tile kernel's balanced-last-round plan, restated: split the
     tiles of the last partly filled round along K when each CU's share is at

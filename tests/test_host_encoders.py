@@ -109,3 +109,40 @@ def test_levels_boundaries(host, k, ib):
     c, v = enc(host, 6, b=b, lv=lv)
     assert np.array_equal(c, idx)
     assert np.array_equal(v, lv[idx])
+
+
+def pow2_ceil_inputs():
+    """fp32 patterns around every power of two: the lowest and highest 64
+    mantissas of every binade, random mantissas, subnormals near each power of
+    two, zeros, negatives, Inf and NaN."""
+    g = np.random.default_rng(5)
+    E = np.arange(1, 255, dtype=np.int64)[:, None] << 23
+    low = (E | np.arange(64)).reshape(-1)
+    high = (E | (0x7FFFFF - np.arange(64))).reshape(-1)
+    rnd = (E | g.integers(0, 1 << 23, (254, 8))).reshape(-1)
+    sub = np.concatenate([(1 << k) + np.arange(min(64, 1 << k)) for k in range(23)])
+    special = np.array([0, 0x80000000, 0xBF800000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x7F7FFFFF], np.int64)
+    return np.concatenate([low, high, rnd, sub, special]).astype(np.uint32)
+
+
+def test_pow2_ceil_log2_matches_torch_cpu(host):
+    # the observer's force_scale_power_of_two (fake_quantize.py:339-340):
+    # torch.pow(2, torch.ceil(torch.log2(sf))) on the CPU, both through
+    # torch's vectorised path (a long tensor) and its scalar path (1 element)
+    import torch
+
+    bits = pow2_ceil_inputs()
+    out = np.zeros_like(bits)
+    host.vqx_host_pow2_ceil_log2(bits.ctypes.data_as(P), ctypes.c_int64(bits.size), out.ctypes.data_as(P))
+    x = torch.from_numpy(bits.view(np.int32)).view(torch.float32)
+    want = torch.pow(2, torch.ceil(torch.log2(x))).numpy().view(np.uint32)
+    got_f, want_f = out.view(np.float32), want.view(np.float32)
+    ok = (out == want) | (np.isnan(got_f) & np.isnan(want_f))
+    assert ok.all(), [(hex(b), hex(o), hex(w)) for b, o, w in zip(bits[~ok][:8], out[~ok][:8], want[~ok][:8])]
+    one = np.array([torch.pow(2, torch.ceil(torch.log2(x[i:i + 1])))[0].item() for i in range(0, x.numel(), 7)],
+                   np.float32)
+    sel = got_f[::7]
+    assert ((sel.view(np.uint32) == one.view(np.uint32)) | (np.isnan(sel) & np.isnan(one))).all()
+    # the rule keeps 2^p for the first mantissas above 2^p at larger |p|
+    # (e.g. 16 * (1 + 2^-23)), where the exact ceiling would be 2^(p+1)
+    assert out[np.where(bits == ((4 + 127) << 23 | 1))[0][0]] == (4 + 127) << 23

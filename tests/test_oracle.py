@@ -294,3 +294,20 @@ def test_gwa_matches_a_per_block_loop():
                 for i in range(col.numel()):
                     q = torch.clamp(torch.round(col[i] / s + z), 0, 3)
                     assert y[4 * b + i, j, k] == (q - z) * s
+
+
+def test_int_table_wide_formats_match_the_reference_expression():
+    # get_quantization_map for int<n> / uint<n> (fake_quantize.py:42-52) is
+    # torch.clamp(torch.round(values), qmin, qmax) on the bf16 patterns; the
+    # golden tables hold 4 and 8 bits, this covers the bias widths
+    import torch
+
+    vals = torch.arange(2**16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    def same(got_u16, want_bf16):
+        w = want_bf16.view(torch.int16).numpy().view(np.uint16)
+        nan = np.isnan(F.bf16_to_f32(got_u16)) & torch.isnan(want_bf16).numpy()  # NaN as a class
+        return bool(((got_u16 == w) | nan).all())
+
+    for n in (12, 16, 24, 31):
+        assert same(F.int_table(n), torch.clamp(torch.round(vals), -(2 ** (n - 1)), 2 ** (n - 1) - 1)), n
+        assert same(F.int_table(n, signed=False), torch.clamp(torch.round(vals), 0, 2**n - 1)), n

@@ -63,6 +63,8 @@ _SIGNATURES = {
     "vqx_vmap": ([_P, _I32, _I64, _P, _P, _P], ctypes.c_int),
     "vqx_fake_quant": ([_P, _I32, _I64, ctypes.POINTER(VqxFormat), _P, _I64, _I64, _I32, _P, _P,
                         _I32, _P], ctypes.c_int),
+    "vqx_amax_observe_fake_quant": ([_P, _I32, _I64, _I64, _I64, ctypes.POINTER(VqxFormat), _P, _I32, _P, _F, _I32,
+                                     _P, _P], ctypes.c_int),
     "vqx_quantize_mapped": ([_P, _I32, _I64, ctypes.POINTER(VqxFormat), ctypes.POINTER(VqxScaleMap),
                              _I32, _P, _P, _I32, _P], ctypes.c_int),
     "vqx_dequantize_mapped": ([_P, _I32, _I64, _P, ctypes.POINTER(VqxScaleMap), _P, _P, _P],

@@ -133,6 +133,17 @@ int vqx_fake_quant(const void* x, int32_t x_dtype, int64_t n, const vqx_format* 
                     codes, code_bytes, (hipStream_t)stream);
 }
 
+int vqx_amax_observe_fake_quant(const void* x, int32_t x_dtype, int64_t n, int64_t channels, int64_t inner,
+                                const vqx_format* fmt, float* amax_history, int32_t history_len, float* scale,
+                                float quant_max, int32_t force_scale_power_of_two, void* y, vqx_stream_t stream) {
+  g_err[0] = 0;
+  FormatDesc d;
+  VQX_TRY(to_desc(fmt, &d));
+  if (!x || !amax_history || !scale) return set_error(kErrInvalid, "amax_observe_fake_quant: null buffer");
+  return amax_observe_fake_quant(x, x_dtype, n, channels, inner, d, amax_history, history_len, scale, quant_max,
+                                 force_scale_power_of_two != 0, y, (hipStream_t)stream);
+}
+
 int vqx_quantize_mapped(const void* x, int32_t x_dtype, int64_t n, const vqx_format* fmt,
                         const vqx_scale_map* sm, int32_t mul_back, void* y, void* codes,
                         int32_t code_bytes, vqx_stream_t stream) {

@@ -416,6 +416,201 @@ int lut_gather(const void* x, int dtype, int64_t n, const uint16_t* table, void*
 }
 
 // ---------------------------------------------------------------------------
+// FusedAmaxObsFakeQuantize.forward for the per-tensor and per-channel
+// qschemes (src/vc/quantization/fake_quantize.py:308-341, :418-426), without
+// a host synchronisation.  Channel of element i: (i / inner) % C (C == 1 is
+// per-tensor).  history: fp32 [H, C]; scale: fp32 [C]; both updated in place.
+//  1. obs_prepare_kernel, one thread per channel: the new scale from the
+//     history's maximum before this step (torch.amax over dim 0, a NaN
+//     anywhere giving NaN), divided by quant_max in IEEE fp32 (the CPU's
+//     tensor / Python-scalar division), the previous scale where that
+//     maximum is not positive or not finite, optionally 2 ** ceil(log2) as
+//     the CPU evaluates it; then torch.roll(history, -1, 0) with row 0
+//     cleared for this step's amax.
+//  2. obs_fq_kernel: y = vmap(x / s, qmap) * s with s the channel's new scale
+//     in x's dtype (FakeQuantizeFunction; skipped when y is null), and |x|
+//     folded into history row 0 by integer atomic max on fp32 bit patterns
+//     (non-negative floats order as their patterns, and a NaN pattern beats
+//     every number, as torch.amax propagates NaN).  A thread keeps a running
+//     maximum for its current channel and folds it in when the channel
+//     changes and at the end, with the atomic skipped when row 0 already
+//     holds at least as much (row 0 only grows during the launch, so a
+//     stale read can only cost an unneeded atomic).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void obs_prepare_kernel(float* __restrict__ hist, int H, int64_t C,
+                                                          float* __restrict__ scale, float quant_max, bool pow2) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  const float first = hist[c];
+  float amax = first;
+  bool nan = first != first;
+#pragma unroll 4
+  for (int h = 1; h < H; ++h) {
+    const float v = hist[(int64_t)h * C + c];
+    nan |= v != v;
+    amax = __builtin_fmaxf(amax, v);
+  }
+  if (nan) amax = __builtin_nanf("");
+  const float prev = scale[c];
+  float sf = amax / quant_max;
+  sf = amax > 0.0f ? sf : prev;
+  sf = __builtin_isfinite(amax) ? sf : prev;
+  if (pow2) sf = u2f(pow2_ceil_log2_f32(f2u(sf)));
+  scale[c] = sf;
+  // roll by -1: row h takes row h + 1, the last row takes row 0
+  for (int h = 1; h + 1 < H; ++h) hist[(int64_t)h * C + c] = hist[(int64_t)(h + 1) * C + c];
+  if (H > 1) hist[(int64_t)(H - 1) * C + c] = first;
+  hist[c] = 0.0f;
+}
+
+__device__ __forceinline__ void fold_amax(uint32_t* __restrict__ row, int64_t c, uint32_t m) {
+  uint32_t* p = row + c;
+  if (m > __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(p, m);
+}
+
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = umax32(v, (uint32_t)__shfl_xor((int)v, d, 64));
+  return v;
+}
+
+// VEC: 8 elements per thread and step with 16-byte loads / stores, every
+// group of 8 within one channel (C == 1, or inner % 8 == 0).  Otherwise one
+// element per step, with a grid stride the host makes a multiple of
+// inner * C when it can, which keeps each thread on one channel.
+template <typename T, typename Enc, bool VEC>
+__global__ __launch_bounds__(256) void obs_fq_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n,
+                                                     int64_t inner, int64_t C, int64_t stride,
+                                                     const float* __restrict__ scale, uint32_t* __restrict__ row,
+                                                     Enc enc) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t run = 0;
+  int64_t run_c = -1;
+  auto fold = [&](int64_t c, uint32_t m) {
+    if (c != run_c) {
+      if (run_c >= 0) fold_amax(row, run_c, run);
+      run_c = c;
+      run = m;
+    } else {
+      run = umax32(run, m);
+    }
+  };
+  if constexpr (VEC) {
+    const int64_t nvec = n / 8;
+    for (int64_t g = t; g < nvec; g += stride) {
+      float v[8];
+      IO<T>::load(x + g * 8, v);
+      const int64_t c = C > 1 ? (g * 8 / inner) % C : 0;
+      uint32_t m = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = umax32(m, f2u(v[j]) & 0x7FFFFFFFu);
+      if (y) {
+        const float s = to_dtype<T>(scale[c]);
+        uint32_t code;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = fq_one<T>(v[j], s, s == 1.0f, true, enc, code);
+        IO<T>::store(y + g * 8, v);
+      }
+      if (C == 1) {
+        run = umax32(run, m);
+        run_c = 0;
+      } else {
+        // when the whole wave is active and on one channel (rows of a
+        // weight), reduce over the wave and let lane 0 fold; the condition
+        // is uniform over the wave, so every lane takes the same branch
+        const int lane = threadIdx.x & 63;
+        const bool full = g - lane + 64 <= nvec;
+        const int ci = (int)c;
+        if (full && __all(ci == __builtin_amdgcn_readfirstlane(ci))) {
+          m = wave_umax(m);
+          if (lane == 0) fold(c, m);
+        } else {
+          fold(c, m);
+        }
+      }
+    }
+    // the < 8-element tail, one element per thread
+    const int64_t i = nvec * 8 + t;
+    if (i < n) {
+      const float xv = IO<T>::get(x + i);
+      const int64_t c = C > 1 ? (i / inner) % C : 0;
+      if (y) {
+        const float s = to_dtype<T>(scale[c]);
+        uint32_t code;
+        IO<T>::put(y + i, fq_one<T>(xv, s, s == 1.0f, true, enc, code));
+      }
+      fold(c, f2u(xv) & 0x7FFFFFFFu);
+    }
+  } else {
+    for (int64_t i = t; i < n; i += stride) {
+      const float xv = IO<T>::get(x + i);
+      const int64_t c = C > 1 ? (i / inner) % C : 0;
+      if (y) {
+        const float s = to_dtype<T>(scale[c]);
+        uint32_t code;
+        IO<T>::put(y + i, fq_one<T>(xv, s, s == 1.0f, true, enc, code));
+      }
+      fold(c, f2u(xv) & 0x7FFFFFFFu);
+    }
+  }
+  if (C == 1) {
+    // per-tensor: one fold per wave
+    const uint32_t m = wave_umax(run_c >= 0 ? run : 0u);
+    if ((threadIdx.x & 63) == 0) fold_amax(row, 0, m);
+  } else if (run_c >= 0) {
+    fold_amax(row, run_c, run);
+  }
+}
+
+template <typename T, typename Enc>
+static int launch_obs_fq(const T* x, T* y, int64_t n, int64_t inner, int64_t C, const float* scale,
+                         uint32_t* row, const Enc& enc, hipStream_t st) {
+  const int bs = 256;
+  const bool vec = (C == 1 || inner % 8 == 0) && aligned(x, 16) && (!y || aligned(y, 16));
+  if (vec) {
+    const unsigned grid = grid_for(n / 8 + 1, bs);
+    hipLaunchKernelGGL((obs_fq_kernel<T, Enc, true>), dim3(grid), dim3(bs), 0, st, x, y, n, inner, C,
+                       (int64_t)grid * bs, scale, row, enc);
+  } else {
+    // a stride that is a multiple of inner * C keeps each thread on one
+    // channel; the cap keeps the grid within a few waves per SIMD
+    const int64_t period = inner * C;
+    const int64_t target = (int64_t)num_cus() * 8 * bs;
+    int64_t threads = target;
+    if (period <= target) threads = target / period * period;
+    else if (period <= (int64_t)1 << 22) threads = period;
+    const int64_t need = n < threads ? ((n + bs - 1) / bs) * bs : threads;
+    const unsigned grid = (unsigned)((need + bs - 1) / bs);
+    hipLaunchKernelGGL((obs_fq_kernel<T, Enc, false>), dim3(grid), dim3(bs), 0, st, x, y, n, inner, C, threads, scale,
+                       row, enc);
+  }
+  return check_launch("amax_observe_fake_quant");
+}
+
+int amax_observe_fake_quant(const void* x, int dtype, int64_t n, int64_t C, int64_t inner, const FormatDesc& fmt,
+                            float* history, int H, float* scale, float quant_max, bool pow2, void* y,
+                            hipStream_t st) {
+  if (n <= 0) return set_error(kErrInvalid, "amax_observe_fake_quant: empty input (torch.amax of an empty tensor)");
+  if (C < 1 || inner < 1 || H < 1) return set_error(kErrInvalid, "amax_observe_fake_quant: C, inner, H must be >= 1");
+  if (C > 1 && (n % (C * inner)) != 0)
+    return set_error(kErrInvalid, "amax_observe_fake_quant: n = %lld is not a multiple of C * inner", (long long)n);
+  if (C > (int64_t)1 << 30) return set_error(kErrInvalid, "amax_observe_fake_quant: too many channels");
+  hipLaunchKernelGGL(obs_prepare_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, st, history, H, C, scale,
+                     quant_max, pow2);
+  int rc = check_launch("amax_observe_fake_quant(prepare)");
+  if (rc != kOk) return rc;
+  uint32_t* row = reinterpret_cast<uint32_t*>(history);
+  return with_encoder(fmt, [&](auto enc) {
+    switch (dtype) {
+      case kF32: return launch_obs_fq((const float*)x, (float*)y, n, inner, C, scale, row, enc, st);
+      case kBF16: return launch_obs_fq((const uint16_t*)x, (uint16_t*)y, n, inner, C, scale, row, enc, st);
+      case kF16: return launch_obs_fq((const __half*)x, (__half*)y, n, inner, C, scale, row, enc, st);
+      default: return set_error(kErrInvalid, "input dtype %d not supported (float32, bfloat16, float16)", dtype);
+    }
+  });
+}
+
+// ---------------------------------------------------------------------------
 // quantize / dequantize with any scale layout (vqx_scale_map)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int64_t scale_index(int64_t i, const ScaleMap& m) {

@@ -131,8 +131,8 @@ int with_encoder(const FormatDesc& d, F&& f) {
       if (d.p0 == 5) return f(EncNvFp8{NvFp8::e5m2()});
       return set_error(kErrInvalid, "NVIDIA fp8 expects e4m3 or e5m2");
     case kFmtInt:
-      if (d.p0 < 1 || d.p0 > 16)
-        return set_error(kErrInvalid, "int%d outside [1,16]", d.p0);
+      if (d.p0 < 1 || d.p0 > 31)
+        return set_error(kErrInvalid, "int%d outside [1,31]", d.p0);
       return f(EncInt{IntFmt{d.p0, d.p1 != 0}});
     case kFmtLevels:
       if (!d.code_table || !d.levels)

@@ -107,6 +107,43 @@ VQX_HD int log2floor_bf16(uint32_t mag) {
   return E == 0 ? sub : nrm;
 }
 
+// 2 ** ceil(log2(f)) for an fp32 bit pattern f, as torch evaluates
+// torch.pow(2, torch.ceil(torch.log2(sf))) on the CPU
+// (src/vc/quantization/fake_quantize.py:339-340).  The CPU's fp32 log2 is
+// correctly rounded, so for f = 2^p (1 + d 2^-q) just above a power of two
+// (q = 23 for a normal f, q = the bit length - 1 of a subnormal's mantissa)
+// the log rounds down to the integer p while log2(1 + d 2^-q) is below half
+// the fp32 spacing next to p: the ceiling then stays p for d <= J.  J depends
+// on p's band (normal f) or on q (subnormal f) only.  Zero gives +0,
+// negative or NaN gives NaN, +Inf stays +Inf.
+VQX_HD uint32_t pow2_ceil_log2_f32(uint32_t b) {
+  if ((b & 0x7FFFFFFFu) == 0) return 0u;                // log2(0) = -inf, 2^-inf = 0
+  if ((b >> 31) || b > 0x7F800000u) return 0x7FC00000u;  // log2 < 0 or NaN: NaN
+  if (b == 0x7F800000u) return b;
+  const uint32_t E = b >> 23, m = b & 0x7FFFFFu;
+  int p;
+  uint32_t d, J;
+  if (E != 0) {
+    p = (int)E - 127;
+    d = m;
+    // band of the integer p: floor(log2 p) above 0, floor(log2(-p - 1))
+    // below (the spacing just above a negative power of two is the finer
+    // one of the binade below it); J by band 2 .. 6
+    const uint32_t n = p > 0 ? (uint32_t)p : (p < -1 ? (uint32_t)(-p - 1) : 0u);
+    const int band = n ? 31 - clz32(n) : -1;
+    J = band >= 2 && band <= 6 ? (0x16'0B'05'02'01ull >> (8 * (band - 2))) & 0xFFu : 0u;
+  } else {
+    const int k = 31 - clz32(m);  // m = 2^k + d
+    p = k - 149;
+    d = m - (1u << k);
+    J = k >= 18 ? (0x0B'05'05'02'01ull >> (8 * (k - 18))) & 0xFFu : 0u;
+  }
+  if (d == 0) return b;  // an exact power of two
+  const int e = d <= J ? p : p + 1;
+  if (e >= 128) return 0x7F800000u;
+  return e >= -126 ? (uint32_t)(e + 127) << 23 : 1u << (e + 149);
+}
+
 // Round-to-nearest-even of mant / 2^sh for sh >= 0 (sh may exceed 31).
 VQX_HD uint32_t rne_shift(uint32_t mant, int sh) {
   if (sh <= 0) return mant << (-sh);

@@ -67,6 +67,9 @@ int fake_quant(const void* x, int dtype, int64_t n, const FormatDesc& fmt, const
                int64_t scale_numel, int64_t scale_inner, bool mul, void* y, void* codes, int code_bytes,
                hipStream_t st);
 int lut_gather(const void* x, int dtype, int64_t n, const uint16_t* table, void* y, hipStream_t st);
+int amax_observe_fake_quant(const void* x, int dtype, int64_t n, int64_t C, int64_t inner, const FormatDesc& fmt,
+                            float* history, int H, float* scale, float quant_max, bool pow2, void* y,
+                            hipStream_t st);
 int build_table(const FormatDesc& fmt, uint16_t* values, uint16_t* codes, hipStream_t st);
 int build_lut(const FormatDesc& fmt, uint32_t* blob, hipStream_t st);
 int level_tables(const float* levels, int K, int mode, uint8_t* index_table, float* boundaries,

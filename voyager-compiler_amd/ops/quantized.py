@@ -927,6 +927,13 @@ def spmm_csr(data, indices, indptr, B, B_scale=None, B_code=None, block_size=Non
 # ---------------------------------------------------------------------------
 # this build's own ops
 # ---------------------------------------------------------------------------
+def _codes_fit(fmt: Format):
+    """Codes are at most 16 bits wide: int / uint formats beyond that (such as
+    the int24 of a bias) have values but no code output."""
+    if fmt.kind == _lib.FMT_INT and fmt.p0 > 16:
+        raise ValueError(f"vqx: {fmt.dtype} values are supported, its codes are not (codes are at most 16 bits)")
+
+
 @_impl("fake_quant")
 def fake_quant(input, dtype, scale=None, mul_back=True, return_codes=False):
     """Closed-form FakeQuantizeFunction (fake_quantize.py:101-115) with an
@@ -936,6 +943,8 @@ def fake_quant(input, dtype, scale=None, mul_back=True, return_codes=False):
     x = input.contiguous()
     if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         raise ValueError(f"vqx: fake_quant input must be float32/bfloat16/float16, not {x.dtype}")
+    if return_codes:
+        _codes_fit(fmt)
     y = torch.empty_like(x)
     cb = 1 if fmt.code_bits <= 8 else 2
     codes = (torch.empty(x.shape, dtype=torch.uint8 if cb == 1 else torch.int16, device=x.device)
@@ -965,6 +974,7 @@ def quantize_mx_packed(input, dtype, axis, block_size, force_scale_power_of_two=
     [cb*i, cb*i+cb) of a little-endian bitstream) along the last axis."""
     _lib.require_device(input, "quantize_mx_packed")
     fmt = parse_format(dtype)
+    _codes_fit(fmt)
     if quant_max is None:
         from ..formats import quant_range
         quant_max = float(quant_range(dtype)[1])

@@ -5,7 +5,10 @@ Same constructor arguments, buffers and state_dict behaviour as the
 reference's ``FusedAmaxObsFakeQuantize``; the arithmetic runs in the HIP
 kernels:
 
-* per-tensor / per-channel / no qscheme: the closed-form fake-quant kernel
+* per-tensor / per-channel / no qscheme: with the observer on, the device
+  observer (``vqx_amax_observe_fake_quant``: scales from the amax history,
+  then one pass that fake-quantizes and folds the input's amax into the
+  history); otherwise the closed-form fake-quant kernel
   (``quantized_ops.fake_quant``), or the table path when ``qmap`` has been
   replaced or edited in place (as codebook fitting does);
 * microscaling: one fused pass that computes the block scales, quantizes and
@@ -13,7 +16,7 @@ kernels:
 * group-wise affine: one fused pass over each block's min / max, scale, zero
   point and the affine fake-quant (``gwa_fake_quantize``).
 
-All three autograd functions pass gradients straight through to the input.
+Every autograd function passes gradients straight through to the input.
 """
 
 import logging
@@ -32,7 +35,9 @@ __all__ = [
     "FakeQuantizeFunction",
     "MXFakeQuantizeFunction",
     "GroupWiseAffineFakeQuantFunction",
+    "ObservedFakeQuantizeFunction",
     "FusedAmaxObsFakeQuantize",
+    "_DerivedObserverOrFakeQuantize",
     "get_quantization_map",
 ]
 
@@ -98,6 +103,21 @@ class MXFakeQuantizeFunction(torch.autograd.Function):
         return (grad_output,) + (None,) * 9
 
 
+class ObservedFakeQuantizeFunction(torch.autograd.Function):
+    """The observer step of a per-tensor / per-channel FusedAmaxObsFakeQuantize
+    followed by FakeQuantizeFunction (fake_quantize.py:418-426), fused into
+    one pass over the input on the device; straight-through gradient."""
+
+    @staticmethod
+    def forward(ctx, input, fake_quant_enabled, module, fmt=None):
+        y = module._observe_fake_quant(input, fake_quant_enabled, fmt)
+        return input if y is None else y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        return (grad_output,) + (None,) * 3
+
+
 class GroupWiseAffineFakeQuantFunction(torch.autograd.Function):
     """Group-wise affine fake-quant (fake_quantize.py:162-216): per block of
     block_size along the axis, scale and zero point from the block min / max,
@@ -121,7 +141,34 @@ class GroupWiseAffineFakeQuantFunction(torch.autograd.Function):
         return (grad_output,) + (None,) * 8
 
 
-class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
+class _BufferFlags:
+    """The enable flags of a FakeQuantizeBase read as the reference reads them
+    on every forward (fake_quantize.py:373, :112, :138, :422).  Their values
+    are cached and re-read only when a buffer changes: its version counter
+    moves with the enable_ / disable_ methods, load_state_dict and in-place
+    writes such as lcq.py's fake_quant_enabled.zero_() / .copy_(), and a moved
+    buffer is a new tensor.  So a forward reads the device only after a
+    change."""
+
+    def _flag(self, name):
+        cache = self.__dict__.setdefault("_flag_cache", {})
+        buf = getattr(self, name)
+        key = (id(buf), buf.data_ptr(), buf.device, buf._version)
+        hit = cache.get(name)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        v = int(buf[0].item())
+        cache[name] = (key, v)
+        return v
+
+    def _observer_on(self):
+        return self._flag("observer_enabled") == 1
+
+    def _fake_quant_on(self):
+        return self._flag("fake_quant_enabled") != 0
+
+
+class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
     """Fake-quantize with an amax-history observer (fake_quantize.py:219-463)."""
 
     def __init__(self, dtype: str, qscheme: Optional[QScheme] = None, quant_min=None, quant_max=None,
@@ -143,7 +190,6 @@ class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
         self.outlier_pct = outlier_pct
         assert outlier_pct is None or outlier_threshold is None, (
             "Only one of outlier_pct and outlier_threshold can be set.")
-        self.max_outlier_pct = 0.0
         self._fmt = parse_format(dtype)
         self.is_codebook_quantization = self._fmt.is_levels
         self._scale_fmt = parse_format(scale_dtype) if scale_dtype is not None else None
@@ -157,8 +203,8 @@ class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
         if record_histogram:
             self.register_buffer("histogram", torch.zeros(254, **fk), persistent=False)
         self.observer_enabled[0] = self.qscheme is not None
-        self._observe = self.qscheme is not None
-        self._fq_on = True
+        self._max_outlier_host = 0.0
+        self._outlier_frac = None
         self.is_per_channel = self.qscheme == QScheme.PER_CHANNEL_SYMMETRIC
         if outlier_pct is not None:
             self.outlier_ema_decay = kwargs.get("outlier_ema_decay", 0.9)
@@ -208,47 +254,74 @@ class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
         """The format's closed form applies while qmap is the table it built."""
         return self._qmap_sig == (self.qmap.data_ptr(), self.qmap._version)
 
-    # -- flags without device syncs -----------------------------------------
-    def enable_fake_quant(self, enabled: bool = True):
-        super().enable_fake_quant(enabled)
-        self._fq_on = bool(enabled)
-        return self
+    # max_outlier_pct: the largest fraction of outliers seen so far
+    # (fake_quantize.py:389-391).  The device keeps the (count, numel) pair of
+    # the largest fraction, compared exactly in int64, and the host divides
+    # only when the value is read (convert reads it), so the forward does not
+    # synchronise and the value is Python's count / numel, as in the reference.
+    @property
+    def max_outlier_pct(self):
+        if self._outlier_frac is not None:
+            c, n = self._outlier_frac.tolist()
+            return max(self._max_outlier_host, c / n)
+        return self._max_outlier_host
 
-    def disable_fake_quant(self):
-        return self.enable_fake_quant(False)
+    @max_outlier_pct.setter
+    def max_outlier_pct(self, value):
+        self._max_outlier_host = float(value)
+        self._outlier_frac = None
 
-    def enable_observer(self, enabled: bool = True):
-        super().enable_observer(enabled)
-        self._observe = bool(enabled)
-        return self
-
-    def disable_observer(self):
-        return self.enable_observer(False)
+    def _fold_outlier_count(self, skip):
+        cnt = skip.sum()
+        cur = torch.stack([cnt, torch.full_like(cnt, skip.numel())])
+        if self._outlier_frac is None:
+            self._outlier_frac = cur
+        else:
+            best = self._outlier_frac
+            self._outlier_frac = torch.where(cur[0] * best[1] > best[0] * cur[1], cur, best)
 
     # -- observer -----------------------------------------------------------
+    def _channel_geometry(self, x):
+        """(channels, inner, keepdim shape of the amax) of the observed amax:
+        one value per tensor, or per index of ch_axis (fake_quantize.py:318-324)."""
+        if not self.is_per_channel:
+            return 1, 1, ()
+        ch_axis = self.ch_axis % x.ndim
+        inner = 1
+        for d in x.shape[ch_axis + 1:]:
+            inner *= d
+        shape = tuple(x.shape[ch_axis] if i == ch_axis else 1 for i in range(x.ndim))
+        return x.shape[ch_axis], inner, shape
+
     @torch.no_grad()
-    def _update_amax_scale(self, x: torch.Tensor) -> None:
-        """Fold x's amax into the history and recompute scale (:308-341): the
-        scale uses the history maximum from before this step's amax."""
-        if self.is_per_channel:
-            ch_axis = self.ch_axis % x.ndim
-            dim = tuple(i for i in range(x.ndim) if i != ch_axis)
-            amax_cur = torch.amax(torch.abs(x), dim=dim, keepdim=True)
-        else:
-            amax_cur = torch.amax(torch.abs(x))
+    def _observe_fake_quant(self, x, fake_quant, fmt):
+        """The observer step (:308-341) and, when fake_quant, the fake-quant
+        at the new scale, in two launches that read x once: returns the
+        fake-quantized tensor, or None when fake_quant is off."""
+        C, inner, shape = self._channel_geometry(x)
         if self.amax_history.numel() == 0:
-            size = (self.amax_history_len,) + amax_cur.shape
-            self.amax_history.resize_(size).fill_(0.0)
-            self.scale.resize_(amax_cur.shape).fill_(1.0)
-        amax = torch.amax(self.amax_history, dim=0)
-        self.amax_history.copy_(torch.roll(self.amax_history, -1, 0))
-        self.amax_history[0] = amax_cur
-        sf = amax / self.quant_max
-        sf = torch.where(amax > 0.0, sf, self.scale)
-        sf = torch.where(torch.isfinite(amax), sf, self.scale)
-        if self.force_scale_power_of_two:
-            sf = torch.pow(2, torch.ceil(torch.log2(sf)))
-        self.scale.copy_(sf)
+            self.amax_history.resize_((self.amax_history_len,) + shape).fill_(0.0)
+            self.scale.resize_(shape).fill_(1.0)
+        if (self.amax_history.device != x.device or self.amax_history.dtype != torch.float32
+                or not self.amax_history.is_contiguous() or not self.scale.is_contiguous()
+                or self.scale.dtype != torch.float32 or self.scale.device != x.device):
+            raise RuntimeError("FusedAmaxObsFakeQuantize: amax_history / scale must be contiguous float32 on the "
+                               "input's device")
+        if self.amax_history.numel() != self.amax_history.shape[0] * C or self.scale.numel() != C:
+            raise RuntimeError(f"FusedAmaxObsFakeQuantize: observed {C} channel(s), but amax_history is "
+                               f"{tuple(self.amax_history.shape)} and scale {tuple(self.scale.shape)}")
+        xc = x.contiguous()
+        y = torch.empty_like(xc) if fake_quant else None
+        if fmt is not None:
+            desc, keep = fmt.desc(xc.device), None
+        else:
+            desc, keep = qops._table_desc(self.qmap.to(xc.device), xc.device)
+        _lib.call("vqx_amax_observe_fake_quant", _lib.ptr(xc), _lib.dtype_tag(xc.dtype), xc.numel(), C, inner,
+                  _lib.ctypes.byref(desc), _lib.ptr(self.amax_history), self.amax_history.shape[0],
+                  _lib.ptr(self.scale), _lib.ctypes.c_float(self.quant_max),
+                  1 if self.force_scale_power_of_two else 0, _lib.ptr(y), _lib.stream_of(xc))
+        del keep
+        return y
 
     @torch.jit.export
     def calculate_qparams(self):
@@ -270,7 +343,7 @@ class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
             exp = torch.floor(torch.log2(torch.abs(x.detach().float())))
             self.histogram += torch.histc(exp, 254, min=-126, max=127)
 
-        if self.outlier_pct is not None and self._observe:
+        if self.outlier_pct is not None and self._observer_on():
             flat = x.abs().flatten()
             k = max(1, math.ceil(self.outlier_pct * flat.numel()))
             threshold = torch.topk(flat, k, largest=True, sorted=False).values.min()
@@ -286,21 +359,22 @@ class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
             skip = x.abs() >= self.outlier_threshold
             orig_x = x
             x = x.masked_fill(skip, 0.0)
-            self.max_outlier_pct = max(skip.sum().item() / x.numel(), self.max_outlier_pct)
+            self._fold_outlier_count(skip)
 
         fmt = self._fmt if self._closed_form() else None
+        fq_on = self._fake_quant_on()
         if self.qscheme == QScheme.MICROSCALING:
-            x = MXFakeQuantizeFunction.apply(x, self._fq_on, self.scale, self.qmap, self.ch_axis,
+            x = MXFakeQuantizeFunction.apply(x, fq_on, self.scale, self.qmap, self.ch_axis,
                                              self.block_size, self.quant_max,
                                              self.force_scale_power_of_two, self.scale_qmap, fmt)
         elif self.qscheme == QScheme.GROUP_WISE_AFFINE:
-            x = GroupWiseAffineFakeQuantFunction.apply(x, self._fq_on, self.scale, self.zero_point, self.ch_axis,
+            x = GroupWiseAffineFakeQuantFunction.apply(x, fq_on, self.scale, self.zero_point, self.ch_axis,
                                                        self.block_size, self.quant_min, self.quant_max,
                                                        self.scale_qmap)
+        elif self._observer_on():
+            x = ObservedFakeQuantizeFunction.apply(x, fq_on, self, fmt)
         else:
-            if self._observe:
-                self._update_amax_scale(x)
-            x = FakeQuantizeFunction.apply(x, self._fq_on, self.qmap, self.scale, fmt)
+            x = FakeQuantizeFunction.apply(x, fq_on, self.qmap, self.scale, fmt)
 
         if skip is not None:
             x = torch.where(skip, orig_x, x)
@@ -318,3 +392,35 @@ class FusedAmaxObsFakeQuantize(FakeQuantizeBase):
                 missing_keys.append(key)
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
                                       unexpected_keys, error_msgs)
+
+
+class _DerivedObserverOrFakeQuantize(_BufferFlags, FakeQuantizeBase):
+    """A fake-quantizer whose scale is derived from other observers
+    (fake_quantize.py:466-495), e.g. a bias quantized at input scale x weight
+    scale: derive_qparams_fn(obs_or_fqs) gives the scale on every forward,
+    and the tensor goes through FakeQuantizeFunction at that scale (int24 and
+    other integer formats up to 31 bits in closed form).  It observes
+    nothing."""
+
+    def __init__(self, dtype: str, obs_or_fqs, derive_qparams_fn):
+        super().__init__()
+        self.obs_or_fqs = obs_or_fqs
+        self.derive_qparams_fn = derive_qparams_fn
+        self.dtype = dtype
+        self._fmt = parse_format(dtype)
+        self.register_buffer("qmap", torch.empty(0, dtype=torch.bfloat16), persistent=False)
+        self.observer_enabled[0] = 0
+        self.qscheme = obs_or_fqs[1].qscheme
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        _lib.require_device(x, "_DerivedObserverOrFakeQuantize")
+        devices = {p.device for p in self.buffers()}
+        if len(devices) != 1 or next(iter(devices)) != x.device:
+            self.to(x.device)
+        if self.qmap.numel() == 0:
+            q = get_quantization_map(self.dtype, x.device)
+            self.qmap = (q[1][q[0]] if isinstance(q, tuple) else q).to(x.device)
+        return FakeQuantizeFunction.apply(x, self._fake_quant_on(), self.qmap, self.calculate_qparams(), self._fmt)
+
+    def calculate_qparams(self):
+        return self.derive_qparams_fn(self.obs_or_fqs)
