@@ -311,3 +311,28 @@ def test_int_table_wide_formats_match_the_reference_expression():
     for n in (12, 16, 24, 31):
         assert same(F.int_table(n), torch.clamp(torch.round(vals), -(2 ** (n - 1)), 2 ** (n - 1) - 1)), n
         assert same(F.int_table(n, signed=False), torch.clamp(torch.round(vals), 0, 2**n - 1)), n
+
+
+def test_bf16_quotients_stay_clear_of_bf16_midpoints():
+    # The absmax kernels compute x / s for bf16 x and s as x * rcp(s), whose
+    # error (v_rcp_f32's 1 ulp plus the product's rounding) stays below 2^-22
+    # relative; that rounds like the reference's fp32 division to bf16 only
+    # because an exact quotient of two 8-bit significands is never within
+    # 2^-17 (relative) of a bf16 rounding midpoint.  Exhaustive over the
+    # significands (1..255 covers the subnormals' shorter ones).
+    from fractions import Fraction
+
+    worst = Fraction(1)
+    for X in range(1, 256):
+        for S in range(1, 256):
+            r = Fraction(X, S)
+            e = math.floor(math.log2(X) - math.log2(S))
+            m = r / Fraction(2) ** e
+            while m >= 2:
+                m /= 2
+            while m < 1:
+                m *= 2
+            k = math.floor((m - 1) * 128)  # the bf16 value below m is 1 + k / 128
+            for mid in (1 + Fraction(2 * k + 1, 256), 1 + Fraction(2 * k - 1, 256)):
+                worst = min(worst, abs(m - mid) / m)
+    assert worst > Fraction(1, 2**17), float(worst)

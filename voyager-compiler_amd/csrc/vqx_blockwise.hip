@@ -239,8 +239,8 @@ __global__ __launch_bounds__(256) void mx_group_kernel(const T* __restrict__ x, 
     if ((threadIdx.x & (LPB - 1)) == 0) {
       int64_t blk = g / LPB;
       if (out.scale) BT<T>::put(static_cast<T*>(out.scale) + blk, BT<T>::round_bits(s));
-      if (out.scale_f32) out.scale_f32[blk] = s;
-      if (out.scale_e8m0) out.scale_e8m0[blk] = (uint8_t)e8m0_of(s);
+      if (out.scale_f32) __builtin_nontemporal_store(s, out.scale_f32 + blk);
+      if (out.scale_e8m0) __builtin_nontemporal_store((uint8_t)e8m0_of(s), out.scale_e8m0 + blk);
     }
   }
 }
@@ -497,8 +497,6 @@ __device__ __forceinline__ uint32_t div_bf16_fast(float x, float s, float r) {
   return f2bf(u2f(qb));
 }
 
-// fp32 q within a few ulp of a bf16 rounding midpoint (see div_bf16_fast)
-__device__ __forceinline__ bool near_midpoint(float q) { return (f2u(q) & 0xFFFFu) - 0x7FFCu <= 8u; }
 
 typedef __attribute__((address_space(3))) const uint32_t lds_cu32;
 typedef __attribute__((address_space(3))) const uint8_t lds_cu8;
@@ -515,6 +513,29 @@ __device__ __forceinline__ float block_scale_pow2_lds(uint32_t amax, int shift, 
   float sc = e > 127 ? __builtin_huge_valf() : (e >= -133 ? exp2i(e) : 1.0f);
   sc = amax == 0x7F80u ? __builtin_huge_valf() : sc;
   return amax > 0x7F80u ? 1.0f : sc;
+}
+
+// Wave layout of the table kernels.  A wave streams 1024-element chunks,
+// lane L taking group L of the chunk (elements 16 L .. 16 L + 15), with each
+// load instruction covering one contiguous 1 KiB: load a brings the first
+// half of the chunk and load b the second, lanes 0-31 taking the even
+// 16-byte slots of a half (elements 16 L .. 16 L + 7 of it) and lanes 32-63
+// the odd ones (16 (L - 32) + 8 .. + 15).  One v_permlane32_swap per dword
+// then gives lane L < 32 its group as (a, a of lane L + 32) and lane L >= 32
+// as (b of lane L - 32, b).  (Loading each lane's own 32 contiguous bytes
+// instead leaves every load instruction half-filling its cache lines, which
+// costs about a fifth of the read rate at these sizes.)  The swap is its own
+// inverse, so it also turns a lane's 16 outputs back into two contiguous
+// 1 KiB stores at the same slots.
+__device__ __forceinline__ uint32_t half_slot(int lane) { return lane < 32 ? 2 * lane : 2 * (lane - 32) + 1; }
+
+__device__ __forceinline__ void half_swap(u32x4& a, u32x4& b) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(a[i], b[i], false, false);
+    a[i] = r[0];
+    b[i] = r[1];
+  }
 }
 
 // WANT: bit 0 = reference quantize() values, bit 1 = fake-quant values.
@@ -534,14 +555,20 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
   static_assert(!CT || (WANT == 0 && (CB == 4 || CB == 8)), "code tables serve packed 4- or 8-bit codes only");
   extern __shared__ uint32_t lds_lut[];
   __shared__ uint8_t thr8[256];
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  // the first group's loads are in flight while the tables fill LDS
+  const int lane = threadIdx.x & 63;
+  // whole 1024-element chunks, one per wave and trip (wave-uniform indices),
+  // in the swapped layout; the groups past the last whole chunk after them,
+  // one per thread, in the plain layout
+  const int64_t nchunks = ngroups / 64;
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x / 64);
+  int64_t c = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)));
+  const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+  const uint32_t slot = half_slot(lane);
+  // the first chunk's loads are in flight while the tables fill LDS
   u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0};
-  if (g < ngroups) {
-    const u32x4* q = reinterpret_cast<const u32x4*>(x + g * 16);
-    n0 = ld_nt(q);
-    n1 = ld_nt(q + 1);
+  if (c < nchunks) {
+    n0 = ld_nt(xv + c * 128 + slot);
+    n1 = ld_nt(xv + c * 128 + 64 + slot);
   }
   if constexpr (!ABSMAX)
     for (int i = threadIdx.x; i < 256; i += blockDim.x) thr8[i] = (uint8_t)log2_step_threshold(i);
@@ -562,21 +589,21 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
   // absmax: a power-of-two quant_max divides exactly as a multiply
   const bool qmax_pow2 = (f2u(sp.quant_max) & 0x807FFFFFu) == 0 && ((f2u(sp.quant_max) >> 23) - 1u) < 253u;
   const float qmax_rcp = u2f((254u - (f2u(sp.quant_max) >> 23)) << 23);
-  for (; g < ngroups; g += stride) {
-    uint32_t w[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
-    if (g + stride < ngroups) {  // prefetch the next group
-      const u32x4* q = reinterpret_cast<const u32x4*>(x + (g + stride) * 16);
-      n0 = ld_nt(q);
-      n1 = ld_nt(q + 1);
-    }
+
+  // One group of 16 consecutive elements (w, as bf16 pairs), group index gl.
+  // SW: a whole chunk in the swapped layout (every lane of the wave active).
+  auto group = [&](auto sw, const uint32_t(&w)[8], int64_t gl) {
+    constexpr bool SW = decltype(sw)::value;
     u16x2 m2 = {0, 0};  // magnitude maxima of the low and high halves
 #pragma unroll
     for (int j = 0; j < 8; ++j) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, w[j] & 0x7FFF7FFFu));
-    uint32_t amax = block_max<LPB>((uint32_t)(m2.x > m2.y ? m2.x : m2.y));
+    const uint32_t amax = block_max<LPB>((uint32_t)(m2.x > m2.y ? m2.x : m2.y));
     float s;
     if constexpr (ABSMAX) {
       if (qmax_pow2 && !sp.scale_qmap) {
-        const float sc = bf2f(f2bf(u2f(amax << 16) * qmax_rcp));
+        // the hardware RNE; a NaN or Inf amax gives NaN / Inf either way,
+        // and NaN then takes scale 1 below as with the software rounding
+        const float sc = u2f(pack_bf16x2(u2f(amax << 16) * qmax_rcp, 0.0f) << 16);
         s = sc > 0.0f ? sc : 1.0f;
       } else {
         s = block_scale_bf16<true>(amax, sp);
@@ -621,20 +648,16 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
           addr[j] = (xb > nthr ? nb : pb) + ES * (f2u(qc) >> 16);  // qc is a bf16 value
         }
       } else {
+        // x and s are bf16 values (8-bit significands), so x / s is at least
+        // 2^-17 (relative) away from every bf16 rounding midpoint, while
+        // x * rcp(s) is within 2^-22 of x / s (v_rcp_f32: 1 ulp, then the
+        // product's rounding): its bf16 rounding is that of the reference's
+        // fp32 division, with no check needed
         float q[16];
-        uint32_t near = 0xFFFFFFFFu;  // min over the group of (low 16 bits of q) - 0x7FFC
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
           q[j] = u2f(xb) * rcp;
-          near = umin32(near, (f2u(q[j]) & 0xFFFFu) - 0x7FFCu);
-        }
-        if (near <= 8u) {  // rare: redo the near-midpoint quotients by IEEE division
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
-            if (near_midpoint(q[j])) q[j] = u2f(xb) / s;
-          }
         }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -652,8 +675,9 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
       }
     } else {
       // scale 1 (NaN block), Inf, subnormal or extreme: exact division and
-      // the full table
-#pragma unroll 1
+      // the full table (unrolled: a rolled loop would index w and ent
+      // dynamically and pin their registers for the whole kernel)
+#pragma unroll
       for (int j = 0; j < 16; ++j) {
         uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
         uint32_t e = full[f2bf(u2f(xb) / s)];
@@ -670,32 +694,63 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
         // pow2 scales on the fast path multiply exactly
         fv[j] = (ABSMAX || !fast) ? f2bf(u2f(v << 16) * s) : (f2u(u2f(v << 16) * s) >> 16);
       }
-      if constexpr (WANT & 1) BT<uint16_t>::store16(static_cast<uint16_t*>(out.qvals) + g * 16, qv);
-      if constexpr (WANT & 2) BT<uint16_t>::store16(static_cast<uint16_t*>(out.fq) + g * 16, fv);
+      auto store = [&](uint16_t* base, const uint32_t(&b)[16]) {
+        if constexpr (SW) {
+          u32x4 a0 = {b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+          u32x4 a1 = {b[8] | (b[9] << 16), b[10] | (b[11] << 16), b[12] | (b[13] << 16), b[14] | (b[15] << 16)};
+          half_swap(a0, a1);
+          u32x4* p = reinterpret_cast<u32x4*>(base + (gl - lane) * 16);
+          st_nt(p + slot, a0);
+          st_nt(p + 64 + slot, a1);
+        } else {
+          BT<uint16_t>::store16(base + gl * 16, b);
+        }
+      };
+      if constexpr (WANT & 1) store(static_cast<uint16_t*>(out.qvals), qv);
+      if constexpr (WANT & 2) store(static_cast<uint16_t*>(out.fq), fv);
     }
     if constexpr (CT && CB == 4) {
       uint32_t b[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) b[k] = ent[2 * k] | ent[2 * k + 1];
       u32x2 cw = {pack_low_bytes(b[0], b[1], b[2], b[3]), pack_low_bytes(b[4], b[5], b[6], b[7])};
-      st_nt(reinterpret_cast<u32x2*>(static_cast<uint8_t*>(out.codes) + g * 8), cw);
+      st_nt(reinterpret_cast<u32x2*>(static_cast<uint8_t*>(out.codes) + gl * 8), cw);
     } else if constexpr (CT) {
       u32x4 cw = {pack_low_bytes(ent[0], ent[1], ent[2], ent[3]), pack_low_bytes(ent[4], ent[5], ent[6], ent[7]),
                   pack_low_bytes(ent[8], ent[9], ent[10], ent[11]),
                   pack_low_bytes(ent[12], ent[13], ent[14], ent[15])};
-      st_nt(reinterpret_cast<u32x4*>(static_cast<uint8_t*>(out.codes) + g * 16), cw);
+      st_nt(reinterpret_cast<u32x4*>(static_cast<uint8_t*>(out.codes) + gl * 16), cw);
     } else if constexpr (CB > 0) {
       uint32_t code[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) code[j] = ent[j] >> 16;
-      store_group_codes<CB>(static_cast<uint8_t*>(out.codes), g, code);
+      store_group_codes<CB>(static_cast<uint8_t*>(out.codes), gl, code);
     }
-    if ((threadIdx.x & (LPB - 1)) == 0) {
-      int64_t blk = g / LPB;
-      if (out.scale) BT<uint16_t>::put(static_cast<uint16_t*>(out.scale) + blk, f2bf(s));
-      if (out.scale_f32) out.scale_f32[blk] = s;
-      if (out.scale_e8m0) out.scale_e8m0[blk] = (uint8_t)e8m0_of(s);
+    if ((gl & (LPB - 1)) == 0) {
+      int64_t blk = gl / LPB;
+      // non-temporal like the codes: a plain store of these scattered
+      // scale words costs about a tenth of the kernel's time at C2's size
+      if (out.scale) __builtin_nontemporal_store((uint16_t)f2bf(s), static_cast<uint16_t*>(out.scale) + blk);
+      if (out.scale_f32) __builtin_nontemporal_store(s, out.scale_f32 + blk);
+      if (out.scale_e8m0) __builtin_nontemporal_store((uint8_t)e8m0_of(s), out.scale_e8m0 + blk);
     }
+  };
+
+  for (; c < nchunks; c += nwaves) {
+    u32x4 a = n0, b = n1;
+    if (c + nwaves < nchunks) {  // prefetch the next chunk
+      n0 = ld_nt(xv + (c + nwaves) * 128 + slot);
+      n1 = ld_nt(xv + (c + nwaves) * 128 + 64 + slot);
+    }
+    half_swap(a, b);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    group(std::true_type{}, w, c * 64 + lane);
+  }
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t g = nchunks * 64 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
+    const u32x4 a = ld_nt(xv + 2 * g), b = ld_nt(xv + 2 * g + 1);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    group(std::false_type{}, w, g);
   }
 }
 
