@@ -382,6 +382,28 @@ def setup_c5_skinny(vqx, torch, L, M):
         bound="hbm", dtype="bf16", keep=(A, codes, sc, lv, out), cpu=cpu_c5(torch, Ac, N))
 
 
+def setup_c5_dense_library(vqx, torch, L, N=11008, M=2048):
+    """Comparison point, not this build's code: C5's product with an already
+    dense bf16 weight through torch.nn.functional.linear (hipBLASLt), i.e. the
+    GEMM half of the reference's own linear_mx (decode, then F.linear), with
+    the decode not counted."""
+    g = torch.Generator().manual_seed(4)
+    K = 4096
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).cuda()
+    F = torch.nn.functional
+
+    def launch():
+        F.linear(A, W)
+        return 0
+
+    return launch, dict(
+        name=f"comparison: dense bf16 A [{M},4096] x W [{N},4096]^T through torch F.linear (hipBLASLt), the GEMM "
+             f"the reference's linear_mx runs after its decode (decode not counted)",
+        elements=M * N, flops=2 * M * N * K, bytes=M * K * 2 + N * K * 2 + M * N * 2, bound="mfma", dtype="bf16",
+        keep=(A, W))
+
+
 def setup_l1(vqx, torch, L):
     """Learned-codebook calibration statistics of a 4096x4096 fp32 weight:
     unit_scale in blocks of 64 (quant_max 7) fused with the 4001-bin fp64
@@ -678,6 +700,8 @@ def _cpu_model():
 # share a kernel name with a default config in a rocprof run of all of them
 ON_REQUEST = {
     "c5_m256_whole_tiles": lambda v, t, L: setup_c5(v, t, L, whole_tiles=True, M=256),
+    "c5_dense_library": lambda v, t, L: setup_c5_dense_library(v, t, L),
+    "c5_dense_library_n8192": lambda v, t, L: setup_c5_dense_library(v, t, L, N=8192),
 }
 
 DOMINANT = {

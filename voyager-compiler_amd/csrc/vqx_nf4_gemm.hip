@@ -547,6 +547,33 @@ __global__ void nf4_zero_counters(int* __restrict__ cnt, int n) {
 // ---------------------------------------------------------------------------
 constexpr int kSkinnyWaves = 4;
 
+// scaled_levels for two 16-lane rows that share one scale (rows 2 j and
+// 2 j + 1 of the wave): the even row scales levels 0-7, the odd row levels
+// 8-15 (lh, the row's own eight) and v_permlane16_swap gives both rows all
+// sixteen.  The same bytes as scaled_levels, for half its products and
+// conversions plus 4 swaps.
+__device__ __forceinline__ LevelBytes row_pair_scaled_levels(const float (&lh)[8], float s) {
+  const uint32_t p0 = pack_bf16x2(lh[0] * s, lh[1] * s), p1 = pack_bf16x2(lh[2] * s, lh[3] * s);
+  const uint32_t p2 = pack_bf16x2(lh[4] * s, lh[5] * s), p3 = pack_bf16x2(lh[6] * s, lh[7] * s);
+  const uint32_t ha = __builtin_amdgcn_perm(p1, p0, 0x07050301u), hb = __builtin_amdgcn_perm(p3, p2, 0x07050301u);
+  const uint32_t la = __builtin_amdgcn_perm(p1, p0, 0x06040200u), lb = __builtin_amdgcn_perm(p3, p2, 0x06040200u);
+  // r[0]: the even row's value, r[1]: the odd row's, in every lane
+  const auto xha = __builtin_amdgcn_permlane16_swap(ha, ha, false, false);
+  const auto xhb = __builtin_amdgcn_permlane16_swap(hb, hb, false, false);
+  const auto xla = __builtin_amdgcn_permlane16_swap(la, la, false, false);
+  const auto xlb = __builtin_amdgcn_permlane16_swap(lb, lb, false, false);
+  LevelBytes t;
+  t.h0 = xha[0];
+  t.h1 = xhb[0];
+  t.h2 = xha[1];
+  t.h3 = xhb[1];
+  t.l0 = xla[0];
+  t.l1 = xlb[0];
+  t.l2 = xla[1];
+  t.l3 = xlb[1];
+  return t;
+}
+
 __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uint16_t* __restrict__ A,
                                                                         const uint8_t* __restrict__ codes,
                                                                         const float* __restrict__ scale,
@@ -564,19 +591,21 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uin
   const int kb = K / 64;
   const int steps = (K + 127) / 128;
   const int s0 = steps * wave / kSkinnyWaves, s1 = steps * (wave + 1) / kSkinnyWaves;
-  float lvf[16];  // the levels as fp32 (uniform)
+  float lh[8];  // the row's eight levels as fp32: 0-7 in even 16-lane rows, 8-15 in odd
 #pragma unroll
-  for (int c = 0; c < 16; ++c) lvf[c] = u2f((uint32_t)levels[c] << 16);
+  for (int c = 0; c < 8; ++c) lh[c] = u2f((uint32_t)levels[c + 8 * (g & 1)] << 16);
   const uint8_t* wrow = codes + (size_t)nn * (K / 2);
   const float* srow = scale + (size_t)nn * kb;
   const uint16_t* arow = A + (size_t)mm * K;
   f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int st = s0; st < s1; ++st) {
-    // K % 64 == 0, so a 32-k group is either wholly inside K or wholly past
-    // it (the last step of an odd number of 64-blocks); past it: A = 0 and
-    // the loads are clamped to the last group
+  // One 128-k step.  CHECK: the step may reach past K (K % 64 == 0, so a
+  // 32-k group is either wholly inside K or wholly past it: the last step of
+  // an odd number of 64-blocks); past it A = 0 and the loads are clamped to
+  // the last group.  Only that step is checked.
+  auto step = [&](int st, auto check) {
+    constexpr bool kCheck = decltype(check)::value;
     const int k = st * 128 + g * 32;
-    const bool kok = k < K;
+    const bool kok = !kCheck || k < K;
     const int kk = kok ? k : K - 32;
     const u32x4 w = *reinterpret_cast<const u32x4*>(wrow + kk / 2);
     const float sc = srow[kk / 64];
@@ -584,10 +613,11 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uin
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       a[c] = *reinterpret_cast<const u32x4*>(arow + kk + 8 * c);
-      if (!kok) a[c] = u32x4{0u, 0u, 0u, 0u};
+      if (kCheck && !kok) a[c] = u32x4{0u, 0u, 0u, 0u};
     }
-    // the lane's 32 codes share one scale block: scale the 16 levels once
-    const LevelBytes tb = scaled_levels(lvf, sc);
+    // the lane's 32 codes share one scale block with those of the other row
+    // of its row pair (k 64-aligned): scale the 16 levels once per pair
+    const LevelBytes tb = row_pair_scaled_levels(lh, sc);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       uint32_t o[4];
@@ -596,7 +626,11 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uin
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[c]), __builtin_bit_cast(bf16x8, b),
                                                     acc, 0, 0, 0);
     }
-  }
+  };
+  const int whole = K / 128;  // steps wholly inside K
+  const int s_end = s1 < whole ? s1 : whole;
+  for (int st = s0; st < s_end; ++st) step(st, std::false_type{});
+  for (int st = s_end > s0 ? s_end : s0; st < s1; ++st) step(st, std::true_type{});
   // lane holds rows 4 (l / 16) .. + 3 of column l % 16
 #pragma unroll
   for (int j = 0; j < 4; ++j) part[wave][4 * g + j][r] = acc[j];
