@@ -55,10 +55,19 @@ def parse():
 # torch-CPU op sequence (the oracle) on a bounded sample of the config and
 # returns (seconds for the whole config, what the sample was)
 # ---------------------------------------------------------------------------
+CPU_WARMUP, CPU_RUNS = 2, 5
+
+
 def _timed(f):
-    t0 = time.perf_counter()
-    f()
-    return time.perf_counter() - t0
+    """Median seconds of CPU_RUNS runs of f after CPU_WARMUP untimed ones."""
+    for _ in range(CPU_WARMUP):
+        f()
+    ts = []
+    for _ in range(CPU_RUNS):
+        t0 = time.perf_counter()
+        f()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
 
 
 def cpu_c1(torch, xc):
@@ -116,7 +125,6 @@ def cpu_c5(torch, Ac, N):
         scale = (torch.rand(N, K // 64, generator=g) * 0.05).to(torch.bfloat16)
         nf = R.table_tensor(F.nf_levels(4))
         rows = min(M, 256)
-        R.linear_mx(Ac[:1], codes, None, scale, 64, nf)  # warm-up
         full = _timed(lambda: R.linear_mx(Ac[:rows], codes, None, scale, 64, nf))
         if rows == M:
             return full, "full M: linear_mx (weight_code[w] * expand(scale), then F.linear in bf16)"
@@ -451,9 +459,8 @@ def setup_g1(vqx, torch, L):
         from oracle import reference_ops as R
 
         q = R.table_tensor(F.quantization_table("int4"))
-        t0 = time.perf_counter()
-        R.gptq_compensate_weight(wc, Hc.clone(), T, q, 7.0, 64, 0.01)
-        return time.perf_counter() - t0, "one run of the oracle's compensate_weight on the full 4096x4096 weight"
+        return _timed(lambda: R.gptq_compensate_weight(wc, Hc.clone(), T, q, 7.0, 64, 0.01)), \
+            "the oracle's compensate_weight on the full 4096x4096 weight"
 
     return launch, dict(
         name="G1 GPTQ compensate_weight: fp32 4096x4096 weight N(0,0.02) seed 11 onto int4 blocks of 64 "
@@ -629,7 +636,8 @@ def cpu_baseline_c2(torch, x):
         s = R.calculate_mx_qparam(xs, [-1], 64, 1.0, False)
         return R.quantize(xs, s, None, [-1], 64, idx_q)
 
-    run()
+    for _ in range(2):  # warm-up
+        run()
     ts = []
     t_start = time.perf_counter()
     while time.perf_counter() - t_start < 10.0 or len(ts) < 3:
@@ -639,7 +647,7 @@ def cpu_baseline_c2(torch, x):
     med = statistics.median(ts)
     return {"value": xs.numel() / med, "unit": "elements/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"full C2 tensor (45,088,768 bf16 elements), 1 warm-up + {len(ts)} timed runs "
+            "sample": f"full C2 tensor (45,088,768 bf16 elements), 2 warm-ups + {len(ts)} timed runs "
                       f"(~10 s), median {med:.3f} s; torch-CPU restatement of calculate_mx_qparam + quantize "
                       f"with the NF4 index table",
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
@@ -656,7 +664,8 @@ def cpu_oracle_time(torch, k, info, kernel_ms):
     if "cpu" in info:
         dt, sample = info["cpu"]()
         return {"seconds": dt, "cores": torch.get_num_threads(), "kind": "port",
-                "gpu_speedup": dt / (kernel_ms * 1e-3), "elements_per_s": info["elements"] / dt, "sample": sample}
+                "gpu_speedup": dt / (kernel_ms * 1e-3), "elements_per_s": info["elements"] / dt, "sample": sample,
+                "timing": f"each timed piece: {CPU_WARMUP} warm-up runs, then the median of {CPU_RUNS}"}
     if k == "l1_histogram":
         x = info["cpu_input"]
 
@@ -678,11 +687,10 @@ def cpu_oracle_time(torch, k, info, kernel_ms):
 
             def fn():
                 return R.quantize_mx_outlier(x, qmap, [-1], 32, 448.0, True, threshold=t, max_pct=pct)
-    t0 = time.perf_counter()
-    fn()
-    dt = time.perf_counter() - t0
+    dt = _timed(fn)
     return {"seconds": dt, "cores": torch.get_num_threads(), "kind": "port", "gpu_speedup": dt / (kernel_ms * 1e-3),
-            "elements_per_s": info["elements"] / dt, "sample": "one run on the config's full input"}
+            "elements_per_s": info["elements"] / dt, "sample": "the config's full input",
+            "timing": f"{CPU_WARMUP} warm-up runs, then the median of {CPU_RUNS}"}
 
 
 def _cpu_model():
@@ -745,7 +753,8 @@ def measured_traffic(key):
 
 def hbm_ceiling(steps, warmup):
     """HBM bandwidth by traffic mix with 1 GiB working sets, which the 256 MiB
-    MALL cannot hold: write only (torch fill_), 1:1 (torch copy_), and two
+    MALL cannot hold: read only (torch amax and sum reductions), write only
+    (torch fill_), 1:1 (torch copy_), and two
     passes of this library's MX kernel over a bf16 16384x32768 input: E8M0
     scales only (read-mostly: 2 B read, 1/32 B written per element) and the
     C3 e4m3 quantize (2:1 read:write).  One JSON line."""
@@ -766,9 +775,33 @@ def hbm_ceiling(steps, warmup):
         print(f"[bench] hbm ceiling {name}: {ms * 1e3:.1f} us, {res[name]['GBps']:.0f} GB/s", file=sys.stderr,
               flush=True)
 
+    run("read_1GiB (torch amax)", lambda: torch.amax(a), 4 * n)
+    run("read_1GiB (torch sum)", lambda: a.sum(), 4 * n)
     run("write_1GiB (torch fill_)", lambda: b.fill_(1.0), 4 * n)
     run("copy_1GiB_to_1GiB (torch copy_)", lambda: b.copy_(a), 8 * n)
     del a, b
+    torch.cuda.empty_cache()
+    # the probe library's streaming kernel at fixed read:write mixes, each
+    # stream 512 MiB (16-byte non-temporal accesses, 1 KiB per wave
+    # instruction), with a one-shot grid (a workgroup per 256 units) and with a
+    # persistent grid of 2048 workgroups
+    import ctypes
+
+    probe = ctypes.CDLL(os.path.join(ROOT, "voyager-compiler_amd", "libvqx_probe.so"))
+    fn = probe.vqx_probe_hbm_mix
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                   ctypes.c_int, ctypes.c_void_p]
+    units = 1 << 25
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    big = torch.empty(4 * units * 16, dtype=torch.uint8, device="cuda").random_()
+    out = torch.empty(4 * units * 16, dtype=torch.uint8, device="cuda")
+    sink = torch.empty(max(units // 256, 2048) * 256, dtype=torch.int32, device="cuda")
+    for r, w in ((1, 0), (0, 1), (1, 1), (2, 1), (4, 1), (1, 2), (1, 4)):
+        for grid, how in ((units // 256, "one-shot grid"), (2048, "persistent grid")):
+            args = (big.data_ptr(), out.data_ptr(), units, r, w, sink.data_ptr(), grid, st)
+            run(f"probe read:write {r}:{w} ({how})", lambda: fn(*args), (r + w) * units * 16)
+    del big, out, sink
     torch.cuda.empty_cache()
     vqx = __graft_entry__.load_package()
     L = vqx._lib
