@@ -518,7 +518,7 @@ __global__ __launch_bounds__(256) void csr_decode_kernel(CsrDecode d) {
 template <int DT, int V>
 __global__ __launch_bounds__(256) void spmm_csr_kernel(SpmmArgs a) {
   using S = typename FT<DT>::S;
-  constexpr int U = 4;
+  constexpr int U = 8;
   const int lane = threadIdx.x & 63;
   const int64_t nch = (a.N + 64 * V - 1) / (64 * V);
   const int64_t items = a.nb * a.rows * nch;
@@ -543,33 +543,42 @@ __global__ __launch_bounds__(256) void spmm_csr_kernel(SpmmArgs a) {
       float acc[V];
 #pragma unroll
       for (int j = 0; j < V; ++j) acc[j] = 0.f;
-      int64_t p = p0;
-      for (; p + U <= p1; p += U) {
-        Group<S, V> grp[U];
-        float av[U];
-        bool ok[U];
+      // The row's entries 64 at a time: lane j loads entry p + j's column and
+      // value once, and the B loads of a group of U entries take them from
+      // the lanes as scalars, so they issue back to back without waiting on
+      // index loads.  The FMAs run in entry order, as before.
+      for (int64_t p = p0; p < p1; p += 64) {
+        const int cnt = (int)(p1 - p < 64 ? p1 - p : 64);
+        const int32_t kl = lane < cnt ? idx[p + lane] : -1;
+        const float al = lane < cnt ? load_f(a.data, a.data_dtype, dbase + p + lane) : 0.f;
+        int q = 0;
+        for (; q + U <= cnt; q += U) {
+          Group<S, V> grp[U];
+          float av[U];
+          bool ok[U];
 #pragma unroll
-        for (int q = 0; q < U; ++q) {
-          const int64_t k = idx[p + q];
-          ok[q] = (uint64_t)k < (uint64_t)a.K;
-          av[q] = load_f(a.data, a.data_dtype, dbase + p + q);
-          grp[q].load(Bb + (ok[q] ? k : 0) * a.N);
+          for (int u = 0; u < U; ++u) {
+            const int k = __builtin_amdgcn_readlane(kl, q + u);
+            ok[u] = (uint32_t)k < (uint64_t)a.K;
+            av[u] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, al), q + u));
+            grp[u].load(Bb + (ok[u] ? (int64_t)k : 0) * a.N);
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int j = 0; j < V; ++j)
+              if (ok[u]) acc[j] = fmaf(av[u], FT<DT>::val(grp[u].get(j)), acc[j]);
         }
-#pragma unroll
-        for (int q = 0; q < U; ++q)
+        for (; q < cnt; ++q) {
+          const int k = __builtin_amdgcn_readlane(kl, q);
+          const bool ok = (uint32_t)k < (uint64_t)a.K;
+          const float av = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, al), q));
+          Group<S, V> grp;
+          grp.load(Bb + (ok ? (int64_t)k : 0) * a.N);
 #pragma unroll
           for (int j = 0; j < V; ++j)
-            if (ok[q]) acc[j] = fmaf(av[q], FT<DT>::val(grp[q].get(j)), acc[j]);
-      }
-      for (; p < p1; ++p) {
-        const int64_t k = idx[p];
-        const bool ok = (uint64_t)k < (uint64_t)a.K;
-        const float av = load_f(a.data, a.data_dtype, dbase + p);
-        Group<S, V> grp;
-        grp.load(Bb + (ok ? k : 0) * a.N);
-#pragma unroll
-        for (int j = 0; j < V; ++j)
-          if (ok) acc[j] = fmaf(av, FT<DT>::val(grp.get(j)), acc[j]);
+            if (ok) acc[j] = fmaf(av, FT<DT>::val(grp.get(j)), acc[j]);
+        }
       }
       if (nok) {
         uint32_t o[V];
