@@ -85,13 +85,16 @@ def test_convert_weight_is_the_nf4_index_table():
 
 @pytest.mark.gpu
 def test_linear_mx_fused_c5_shape(vqx):
-    """The full C5 shape: A bf16 [2048, 4096] x W [11008, 4096] in convert
-    format, fused, against the oracle's linear_mx."""
-    print("linear_mx fused M=2048 N=11008 K=4096", flush=True)
+    """The drop-in check at the full C5 shape: a bf16 weight [11008, 4096]
+    quantized to NF4 blocks of 64 as convert_pt2e writes it (index weight,
+    weight_code, weight_scale; quantize_pt2e.py:456-508), then the
+    reference's own op, torch.ops.quantized_ops.linear_mx, on A bf16
+    [2048, 4096] through the fused kernel, against the oracle's linear_mx."""
+    print("linear_mx fused M=2048 N=11008 K=4096 (convert-format weight)", flush=True)
     M, N, K = 2048, 11008, 4096
     g = torch.Generator().manual_seed(4)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16)
-    idx, scale, code = random_convert_format(N, K, 4)
+    idx, scale, code = convert_format(N, K, 4)
     with fused_only():
         out = Q.linear_mx(A.cuda(), idx.cuda(), None, weight_scale=scale.cuda(), weight_code=code.cuda(), block_size=64)
     assert out.dtype == torch.bfloat16 and out.shape == (M, N)
