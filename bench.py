@@ -500,8 +500,14 @@ def setup_o1(vqx, torch, L, mx=False):
     R, C = x.shape
     n = x.numel()
     bufs, fargs, max_nnz = _outlier_csr(torch, L, x)
-    filt = L.load().vqx_filter_outlier
-    filt(*fargs)
+    # the one-pass entry points: x read once, the outliers staged in a
+    # workspace and placed by a second, small launch
+    wsz = L.ctypes.c_int64(0)
+    L.call("vqx_outlier_workspace_size", L.BF16, 1, R, C, max_nnz, L.ctypes.byref(wsz))
+    ws = torch.empty(max(wsz.value, 1), dtype=torch.uint8, device="cuda")
+    filt = L.load().vqx_filter_outlier_ws
+    fargs = fargs[:-1] + (L.ptr(ws), wsz.value, fargs[-1])
+    L.call("vqx_filter_outlier_ws", *fargs)
     torch.cuda.synchronize()
     nnz = int(bufs["ptr"][-1])
     csr_bytes = 6 * max_nnz + 4 * (R + 1)
@@ -511,20 +517,21 @@ def setup_o1(vqx, torch, L, mx=False):
         return (lambda: filt(*fargs)), dict(
             name=f"O1 filter_outlier, bf16 4096x11008 N(0,1) with 0.5% x32 seed 5, |x| > {OUTLIER_THRESHOLD}, "
                  f"capacity 1% -> CSR ({nnz} outliers) + inliers",
-            bytes=4 * n + csr_bytes, **common)
+            bytes=4 * n + csr_bytes, keep=(ws,), **common)
     # the one-pass form: the split writes the quantized inliers and their
     # block scales instead of the inliers
     table = vqx.get_quantization_map("fp8_e4m3", "cuda")
     sc = torch.empty(R, C // 32, dtype=torch.bfloat16, device="cuda")
     qv = torch.empty_like(x)
-    fused = L.load().vqx_quantize_mx_outlier
+    fused = L.load().vqx_quantize_mx_outlier_ws
     margs = (L.ptr(x), 1, R, C, L.ctypes.c_float(OUTLIER_THRESHOLD), max_nnz, 0, 32, 0, 8, L.ctypes.c_float(448.0),
              None, L.ptr(table), L.ptr(bufs["data"]), L.ptr(bufs["idx"]), L.ptr(bufs["ptr"]), L.ptr(sc), L.ptr(qv),
-             L.stream_of(x))
+             L.ptr(ws), wsz.value, L.stream_of(x))
+    L.call("vqx_quantize_mx_outlier_ws", *margs)
     return (lambda: fused(*margs)), dict(
         name=f"O2 quantize_mx_outlier: O1's CSR and, in the same split pass, MX block-32 fp8_e4m3 power-of-two "
              f"scales and quantized values of the inliers -> CSR + bf16 scales + bf16 quantized inliers",
-        bytes=4 * n + n // 32 * 2 + csr_bytes, keep=(table, sc, qv), **common)
+        bytes=4 * n + n // 32 * 2 + csr_bytes, keep=(table, sc, qv, ws), **common)
 
 
 def setup_o3(vqx, torch, L):
@@ -730,8 +737,8 @@ DOMINANT = {
     "c5_m1": "nf4_skinny_kernel",
     "c5_m16": "nf4_skinny_kernel",
     "f3_gwa": "gwa_fq_rows_kernel<unsigned short, 8>",
-    "o1_filter": "outlier_split_kernel<1, 8>",
-    "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8, true, 4>",
+    "o1_filter": "outlier_split_kernel<1, 8, false, 1, true>",
+    "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8, true, 4, true>",
     "o3_spmm": "spmm_csr_kernel<1, 8>",
     "l1_histogram": "lcq_hist_kernel<0, true, false>",
     "g1_gptq": "gptq_block_kernel",

@@ -355,6 +355,34 @@ int vqx_quantize_mx_outlier(const void* x, int64_t batches, int64_t rows, int64_
                             vqx_stream_t stream);
 
 /*
+ * One-pass forms of vqx_filter_outlier and vqx_quantize_mx_outlier (same
+ * arguments, same outputs bit for bit), which read x once: the first launch
+ * writes the inliers (or the quantized inliers and their scales), each row's
+ * outlier count, and the row's first outliers to staging slots in
+ * `workspace`; the second places them behind the row pointers, reading again
+ * only the rows whose outliers did not fit their slots, and pads the unused
+ * entries.  Same reference interfaces as the two entry points above
+ * (src/vc/ops/quantized.py:532-630, :633-712).
+ * vqx_outlier_workspace_size gives the bytes for the default slots per row
+ * (0 when batches * rows == 0; workspace may then be NULL).  Any workspace of
+ * at least the 256-byte-aligned 4 * batches * rows bytes of the counts works:
+ * the rest sets the slots per row (fewer slots, more rows read again).
+ * workspace: 256-byte aligned device memory, contents ignored; calls that
+ * share one workspace must be ordered (one stream).
+ */
+int vqx_outlier_workspace_size(int32_t x_dtype, int64_t batches, int64_t rows, int64_t cols, int64_t max_nnz,
+                               int64_t* bytes);
+int vqx_filter_outlier_ws(const void* x, int32_t x_dtype, int64_t batches, int64_t rows, int64_t cols,
+                          float threshold, int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices,
+                          int32_t* indptr, void* inlier, void* workspace, int64_t workspace_bytes,
+                          vqx_stream_t stream);
+int vqx_quantize_mx_outlier_ws(const void* x, int64_t batches, int64_t rows, int64_t cols, float threshold,
+                               int64_t max_nnz, int32_t indptr_offset, int64_t block_size, int32_t scale_mode,
+                               int32_t shift, float quant_max, const uint16_t* scale_qmap, const uint16_t* qmap,
+                               void* data, int32_t* indices, int32_t* indptr, void* scale, void* values,
+                               void* workspace, int64_t workspace_bytes, vqx_stream_t stream);
+
+/*
  * quantized_ops::slice_csr_tensor (src/vc/ops/quantized.py:715-777) of one CSR
  * matrix: data [nnz] (F32, BF16 or F16), indices [nnz] int32, indptr [rows + 1]
  * int32 starting at 0; entries past indptr[rows] are padding (index -1).

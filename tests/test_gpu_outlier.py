@@ -7,6 +7,7 @@ capacity, negative / infinite / NaN thresholds, the threshold rounded to the
 input dtype, NaN / Inf / signed zeros, odd widths (the element-wise path),
 batch dims, row pointers offset into a longer array."""
 
+import ctypes
 import math
 
 import pytest
@@ -278,3 +279,106 @@ def test_quantize_mx_outlier_fused_equals_two_pass_at_bench_size(vqx):
     s, v = Q.quantize_mx(inl, qm, [-1], 32, 448.0, True)
     for a, b in zip(fused, (d, i, p, s, v)):
         assert same(a, b)
+
+
+# ---------------------------------------------------------------------------
+# one-pass entry points (staged outliers) against the two-pass ones, through
+# the C ABI: default staging, none (every row with outliers read again) and
+# three slots per row (some rows staged, some read again)
+# ---------------------------------------------------------------------------
+def _csr_buffers(x, max_nnz):
+    nb = math.prod(x.shape[:-2])
+    R = x.shape[-2]
+    return (torch.full((nb, max_nnz), 7, dtype=x.dtype, device=x.device),
+            torch.full((nb, max_nnz), 7, dtype=torch.int32, device=x.device),
+            torch.full((nb, R + 1), 7, dtype=torch.int32, device=x.device))
+
+
+def _workspace(vqx, x, max_nnz, slots):
+    L = vqx._lib
+    nb, (R, C) = math.prod(x.shape[:-2]), x.shape[-2:]
+    if slots is None:
+        n = ctypes.c_int64(0)
+        L.call("vqx_outlier_workspace_size", L.dtype_tag(x.dtype), nb, R, C, max_nnz, ctypes.byref(n))
+        size = n.value
+    else:
+        size = (nb * R * 4 + 255) // 256 * 256 + nb * R * slots * (4 + x.element_size())
+    return torch.empty(max(size, 1), dtype=torch.uint8, device=x.device), size
+
+
+def _filter(vqx, x, thr, max_nnz, offset, slots="two-pass"):
+    L = vqx._lib
+    nb, (R, C) = math.prod(x.shape[:-2]), x.shape[-2:]
+    data, idx, ptr = _csr_buffers(x, max_nnz)
+    inl = torch.full_like(x, 3.0)
+    args = (L.ptr(x), L.dtype_tag(x.dtype), nb, R, C, thr, max_nnz, offset, L.ptr(data), L.ptr(idx), L.ptr(ptr),
+            L.ptr(inl))
+    if slots == "two-pass":
+        L.call("vqx_filter_outlier", *args, L.stream_of(x))
+    else:
+        ws, size = _workspace(vqx, x, max_nnz, slots)
+        L.call("vqx_filter_outlier_ws", *args, L.ptr(ws), size, L.stream_of(x))
+    return data, idx, ptr, inl
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(3, 40, 72), (64, 256), (2, 7, 1001), (300, 96), (1, 5)])
+@pytest.mark.parametrize("slots", [None, 0, 3])
+def test_filter_outlier_one_pass_equals_two_pass(vqx, dtype, shape, slots):
+    x = with_specials(rand_outliers(shape, dtype, seed=sum(shape) + 1, frac=0.05)).cuda()
+    per = math.prod(shape[-2:])
+    for pct, offset in [(0.01, 0), (0.5, 7), (0.0, 0), (1.0, -(1 << 31))]:
+        max_nnz = int(per * pct)
+        print(f"one-pass filter {dtype} {shape} slots={slots} max_nnz={max_nnz} offset={offset}", flush=True)
+        want = _filter(vqx, x, 3.0, max_nnz, offset)
+        got = _filter(vqx, x, 3.0, max_nnz, offset, slots)
+        check_all(got, want, CSR)
+
+
+@pytest.mark.gpu
+def test_filter_outlier_one_pass_dense_rows_and_many_rows(vqx):
+    # rows all outliers (more than the largest default staging), and more
+    # than 16384 rows per batch (256-row chunks in the second launch)
+    x = rand_outliers((2, 40, 3000), torch.bfloat16, seed=4)
+    x[0, 5] = 100.0
+    x[1, 39, 1000:] = -100.0
+    x = x.cuda()
+    for pct in (0.5, 0.02):
+        max_nnz = int(40 * 3000 * pct)
+        check_all(_filter(vqx, x, 3.0, max_nnz, 0, None), _filter(vqx, x, 3.0, max_nnz, 0), CSR)
+    y = rand_outliers((2, 17000, 64), torch.bfloat16, seed=6, frac=0.01).cuda()
+    for slots in (None, 1):
+        check_all(_filter(vqx, y, 3.0, int(17000 * 64 * 0.01), 5, slots), _filter(vqx, y, 3.0, int(17000 * 64 * 0.01), 5),
+                  CSR)
+
+
+def _qmx(vqx, x, qm, bs, pow2, sq, thr, max_nnz, offset, slots="two-pass"):
+    L = vqx._lib
+    nb, (R, C) = math.prod(x.shape[:-2]), x.shape[-2:]
+    data, idx, ptr = _csr_buffers(x, max_nnz)
+    scale = torch.full((*x.shape[:-1], C // bs), 3.0, dtype=x.dtype, device=x.device)
+    values = torch.full_like(x, 3.0)
+    args = (L.ptr(x), nb, R, C, thr, max_nnz, offset, bs, 0 if pow2 else 1, 8 if pow2 else 0, 448.0, L.ptr(sq),
+            L.ptr(qm), L.ptr(data), L.ptr(idx), L.ptr(ptr), L.ptr(scale), L.ptr(values))
+    if slots == "two-pass":
+        L.call("vqx_quantize_mx_outlier", *args, L.stream_of(x))
+    else:
+        ws, size = _workspace(vqx, x, max_nnz, slots)
+        L.call("vqx_quantize_mx_outlier_ws", *args, L.ptr(ws), size, L.stream_of(x))
+    return data, idx, ptr, scale, values
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bs", [8, 32, 64])
+@pytest.mark.parametrize("slots", [None, 0, 2])
+@pytest.mark.parametrize("fmt", ["fp8_e4m3", "fp4_e2m1", "int8"])
+def test_quantize_mx_outlier_one_pass_equals_two_pass(vqx, bs, slots, fmt):
+    x = with_specials(rand_outliers((3, 24, 384), torch.bfloat16, seed=21 + bs, frac=0.05)).cuda()
+    qm = vqx.ops.quantized._table_bf16(vqx.get_quantization_map(fmt, "cuda"))
+    for pow2, pct, offset in [(True, 0.02, 0), (False, 0.5, 11), (True, 0.0, 3)]:
+        max_nnz = int(24 * 384 * pct)
+        print(f"one-pass quantize_mx_outlier {fmt} bs={bs} slots={slots} pow2={pow2} max_nnz={max_nnz}", flush=True)
+        want = _qmx(vqx, x, qm, bs, pow2, None, 4.0, max_nnz, offset)
+        got = _qmx(vqx, x, qm, bs, pow2, None, 4.0, max_nnz, offset, slots)
+        check_all(got, want, ("data", "indices", "indptr", "scale", "values"))

@@ -86,6 +86,11 @@ _SIGNATURES = {
     "vqx_nf4_linear_noalloc": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
     "vqx_nf4_pack_weight": ([_P, _I32, _P, _I32, _I64, _I64, _I32, _I32, _P, _P, _P, _P], ctypes.c_int),
     "vqx_filter_outlier": ([_P, _I32, _I64, _I64, _I64, _F, _I64, _I32, _P, _P, _P, _P, _P], ctypes.c_int),
+    "vqx_outlier_workspace_size": ([_I32, _I64, _I64, _I64, _I64, ctypes.POINTER(_I64)], ctypes.c_int),
+    "vqx_filter_outlier_ws": ([_P, _I32, _I64, _I64, _I64, _F, _I64, _I32, _P, _P, _P, _P, _P, _I64, _P],
+                              ctypes.c_int),
+    "vqx_quantize_mx_outlier_ws": ([_P, _I64, _I64, _I64, ctypes.c_float, _I64, _I32, _I64, _I32, _I32,
+                                    ctypes.c_float, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P], ctypes.c_int),
     "vqx_slice_csr": ([_P, _I32, _P, _P, _I64, _I64, _I32, _I64, _I64, _I64, _P, _P, _P, _P], ctypes.c_int),
     "vqx_csr_decode_weight": ([_P, _I32, _I64, _I64, _I64, _I32, _P, _I32, _I64, _P, _I32, _I64, _I64, _I64,
                                _I64, _I64, _P, _I32, _P], ctypes.c_int),

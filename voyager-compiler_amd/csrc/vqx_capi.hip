@@ -311,6 +311,34 @@ int vqx_quantize_mx_outlier(const void* x, int64_t batches, int64_t rows, int64_
                                    data, indices, indptr, scale, values, (hipStream_t)stream);
 }
 
+int vqx_outlier_workspace_size(int32_t x_dtype, int64_t batches, int64_t rows, int64_t cols, int64_t max_nnz,
+                               int64_t* bytes) {
+  g_err[0] = 0;
+  return outlier_workspace_size(x_dtype, batches, rows, cols, max_nnz, bytes);
+}
+
+int vqx_filter_outlier_ws(const void* x, int32_t x_dtype, int64_t batches, int64_t rows, int64_t cols,
+                          float threshold, int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices,
+                          int32_t* indptr, void* inlier, void* workspace, int64_t workspace_bytes,
+                          vqx_stream_t stream) {
+  g_err[0] = 0;
+  return filter_outlier_ws(x, x_dtype, batches, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr,
+                           inlier, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int vqx_quantize_mx_outlier_ws(const void* x, int64_t batches, int64_t rows, int64_t cols, float threshold,
+                               int64_t max_nnz, int32_t indptr_offset, int64_t block_size, int32_t scale_mode,
+                               int32_t shift, float quant_max, const uint16_t* scale_qmap, const uint16_t* qmap,
+                               void* data, int32_t* indices, int32_t* indptr, void* scale, void* values,
+                               void* workspace, int64_t workspace_bytes, vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (scale_mode != 0 && scale_mode != 1) return set_error(kErrInvalid, "quantize_mx_outlier: scale_mode 0 or 1");
+  ScaleParams sp{scale_mode, shift, quant_max, scale_mode == 1 ? scale_qmap : nullptr};
+  return quantize_mx_outlier_fused_ws(x, batches, rows, cols, threshold, max_nnz, indptr_offset, block_size, sp, qmap,
+                                      data, indices, indptr, scale, values, workspace, workspace_bytes,
+                                      (hipStream_t)stream);
+}
+
 int vqx_slice_csr(const void* data, int32_t dtype, const int32_t* indices, const int32_t* indptr, int64_t nnz,
                   int64_t rows, int32_t dim, int64_t start, int64_t end, int64_t max_nnz, void* data_out,
                   int32_t* indices_out, int32_t* indptr_out, vqx_stream_t stream) {

@@ -139,6 +139,15 @@ int quantize_mx_outlier_fused(const void* x, int64_t nb, int64_t rows, int64_t c
                               int64_t max_nnz, int32_t indptr_offset, int64_t block_size, const ScaleParams& sp,
                               const uint16_t* qmap, void* data, int32_t* indices, int32_t* indptr, void* scale,
                               void* values, hipStream_t st);
+int64_t outlier_stage_slots(int64_t rows, int64_t cols, int64_t max_nnz);
+int outlier_workspace_size(int dtype, int64_t nb, int64_t rows, int64_t cols, int64_t max_nnz, int64_t* bytes);
+int filter_outlier_ws(const void* x, int dtype, int64_t nb, int64_t rows, int64_t cols, float threshold,
+                      int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices, int32_t* indptr,
+                      void* inlier, void* workspace, int64_t workspace_bytes, hipStream_t st);
+int quantize_mx_outlier_fused_ws(const void* x, int64_t nb, int64_t rows, int64_t cols, float threshold,
+                                 int64_t max_nnz, int32_t indptr_offset, int64_t block_size, const ScaleParams& sp,
+                                 const uint16_t* qmap, void* data, int32_t* indices, int32_t* indptr, void* scale,
+                                 void* values, void* workspace, int64_t workspace_bytes, hipStream_t st);
 int csr_slice(const void* data, int dtype, const int32_t* indices, const int32_t* indptr, int64_t nnz_in,
               int64_t rows, int dim, int64_t start, int64_t end, int64_t max_nnz, void* data_out,
               int32_t* indices_out, int32_t* indptr_out, hipStream_t st);

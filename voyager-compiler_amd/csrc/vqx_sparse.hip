@@ -17,6 +17,16 @@
 // come from wave ballots (lane-major, so column order is kept).  Entries past
 // the capacity are dropped, which keeps the first max_nnz in row-major order.
 //
+// The one-pass form (the _ws entry points) reads x once, in two launches:
+//   1. outlier_split_kernel<.., STAGE>  as 3. above, but each row's outliers
+//                            go to the row's own staging slots in a caller's
+//                            workspace (the first `slots` of them) and its
+//                            count to counts[row];
+//   2. outlier_finalize_kernel  one workgroup per chunk of rows: row pointers
+//                            from the counts, the staged entries copied to
+//                            their slots, rows that overflowed their staging
+//                            read again from x, and the padding.
+//
 // The column slice of a CSR matrix reuses the same count -> scan -> scatter
 // shape over the stored entries; the row slice is one gather launch.
 //
@@ -118,6 +128,12 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
 }
 
 __device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
@@ -232,38 +248,61 @@ struct MxFuse {
   uint16_t* scale;       // [rows, cols / (V * LPB)] bf16
 };
 
-template <int DT, int V, bool MXQ = false, int LPB = 1>
+// The one-pass form (STAGE) has no row pointers yet: each row's outliers go
+// to the row's own staging slots (the first `slots` of them, in column
+// order) and its count to counts[row]; outlier_finalize_kernel then places
+// them.
+struct Stage {
+  int32_t* counts;  // [nb * rows]
+  int32_t* col;     // [nb * rows][slots]
+  void* val;        // [nb * rows][slots], x's storage type
+  int64_t slots;
+};
+
+template <int DT, int V, bool MXQ = false, int LPB = 1, bool STAGE = false>
 __global__ __launch_bounds__(256) void outlier_split_kernel(const typename FT<DT>::S* __restrict__ x,
                                                             int64_t nb, int64_t rows, int64_t cols,
                                                             float t, const int32_t* __restrict__ indptr,
                                                             int64_t max_nnz, typename FT<DT>::S* __restrict__ inlier,
                                                             typename FT<DT>::S* __restrict__ data,
-                                                            int32_t* __restrict__ indices, MxFuse mf = {}) {
+                                                            int32_t* __restrict__ indices, MxFuse mf = {},
+                                                            Stage sg = {}) {
   static_assert(!MXQ || (DT == kBF16 && V == 8), "the fused MX quantization takes bf16 groups of 8");
   using S = typename FT<DT>::S;
   constexpr int U = 4;
   constexpr uint32_t CAP = 1024, FLUSH = CAP - 64 * V;  // a group adds at most 64 * V
-  __shared__ uint32_t s_val[4][CAP];
+  __shared__ S s_val[4][CAP];
   __shared__ uint32_t s_col[4][CAP];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  uint32_t* bval = s_val[wv];
+  S* bval = s_val[wv];
   uint32_t* bcol = s_col[wv];
   const int64_t nw = (int64_t)gridDim.x * 4;
   const int64_t nrows = nb * rows;
   for (int64_t g = (int64_t)blockIdx.x * 4 + wv; g < nrows; g += nw) {
     const int64_t b = g / rows, r = g - b * rows;
-    const int32_t* ptr = indptr + b * (rows + 1);
-    int64_t pos = (int64_t)(uint32_t)((uint32_t)ptr[r] - (uint32_t)ptr[0]);
+    int64_t pos, lim;
+    S* drow;
+    int32_t* crow;
+    if constexpr (STAGE) {
+      pos = 0;
+      lim = sg.slots;
+      drow = (S*)sg.val + g * sg.slots;
+      crow = sg.col + g * sg.slots;
+    } else {
+      const int32_t* ptr = indptr + b * (rows + 1);
+      pos = (int64_t)(uint32_t)((uint32_t)ptr[r] - (uint32_t)ptr[0]);
+      lim = max_nnz;
+      drow = data + b * max_nnz;
+      crow = indices + b * max_nnz;
+    }
     const S* row = x + g * cols;
     S* irow = inlier + g * cols;
-    S* drow = data + b * max_nnz;
-    int32_t* crow = indices + b * max_nnz;
     uint32_t nbuf = 0;
     auto flush = [&]() {
       wave_lds_sync();
       for (uint32_t i = lane; i < nbuf; i += 64) {
         const int64_t p = pos + i;
-        if (p < max_nnz) {
+        if (p < lim) {
           drow[p] = (S)bval[i];
           crow[p] = (int32_t)bcol[i];
         }
@@ -331,7 +370,7 @@ __global__ __launch_bounds__(256) void outlier_split_kernel(const typename FT<DT
 #pragma unroll
           for (int j = 0; j < V; ++j) {
             if (f[j]) {
-              bval[q] = grp[u].get(j);
+              bval[q] = (S)grp[u].get(j);
               bcol[q] = c + j;
               ++q;
             }
@@ -342,8 +381,157 @@ __global__ __launch_bounds__(256) void outlier_split_kernel(const typename FT<DT
       }
     }
     if (nbuf != 0) flush();
+    if constexpr (STAGE) {
+      if (lane == 0) sg.counts[g] = (int32_t)pos;
+    }
   }
-  pad_tail(indptr, rows, nb, max_nnz, data, indices);
+  if constexpr (!STAGE) pad_tail(indptr, rows, nb, max_nnz, data, indices);
+}
+
+// The one-pass form's second launch, one workgroup per (batch, chunk of 16
+// to 256 rows): the chunk's row pointers (the batch's counts before the
+// chunk summed, then a scan over the chunk's own), its rows' staged
+// outliers copied to their slots, and its share of the batch's unused slots
+// padded with 0 / -1.  The chunk's entries fill one contiguous run of slots,
+// so each thread takes slots of that run (a binary search over the chunk's
+// row starts names the row) and all the copies are independent.  A row with
+// more outliers than staging slots reads its row of x again and places all
+// of them, in column order, directly.  The pointers clamp to max_nnz and add
+// the offset as csr_scan_kernel does, and every entry lands where the
+// two-pass form puts it.  Each workgroup reads the batch's whole count array
+// (L2-resident: 4 bytes per row).
+template <int DT, int V>
+__global__ __launch_bounds__(256) void outlier_finalize_kernel(const typename FT<DT>::S* __restrict__ x,
+                                                               int64_t rows, int64_t cols, float t, Stage sg,
+                                                               int64_t chunk, int64_t nchunk, int64_t max_nnz,
+                                                               int32_t offset, typename FT<DT>::S* __restrict__ data,
+                                                               int32_t* __restrict__ indices,
+                                                               int32_t* __restrict__ indptr) {
+  using S = typename FT<DT>::S;
+  constexpr int U = 16;
+  __shared__ int64_t red[2][4];
+  __shared__ int64_t wtot[4];
+  __shared__ int64_t first[256];  // slot of each chunk row's first outlier, before clamping
+  __shared__ int32_t ncnt[256];   // each chunk row's count
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t b = blockIdx.x / nchunk, c = blockIdx.x - b * nchunk;
+  const int64_t r0 = c * chunk, r1 = min64(r0 + chunk, rows), nr = r1 - r0;
+  const int32_t* cnt = sg.counts + b * rows;
+  // every load unconditional (indices clamped into the array, values
+  // masked), so that all of a thread's loads are in flight together
+  const int64_t r = r0 + tid;
+  int32_t v = rows > 0 ? cnt[min64(r, rows - 1)] : 0;
+  v = tid < nr ? v : 0;
+  int64_t pre = 0, tot = 0;
+  const int last = (int)rows - 1;  // rows < 2^31
+  for (int q = tid; q <= last; q += 256 * U) {
+    int32_t w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) w[u] = cnt[min(q + 256 * u, last)];
+    // all U loads issue before the first use
+    __builtin_amdgcn_sched_barrier(0);
+    int64_t st = 0, sp = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = q + 256 * u;
+      st += i <= last ? w[u] : 0;
+      sp += i < r0 ? w[u] : 0;
+    }
+    tot += st;
+    pre += sp;
+  }
+  pre = wave_sum64(pre);
+  tot = wave_sum64(tot);
+  if (lane == 0) red[0][wv] = pre, red[1][wv] = tot;
+  const int64_t incl = wave_incl_scan(v, lane);
+  if (lane == 63) wtot[wv] = incl;
+  __syncthreads();
+  pre = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+  tot = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  int64_t before = pre;
+  for (int w = 0; w < wv; ++w) before += wtot[w];
+  first[tid] = before + incl - v;
+  ncnt[tid] = v;
+  if (tid < nr) {
+    const int64_t e = before + incl;
+    indptr[b * (rows + 1) + r + 1] = (int32_t)((uint32_t)(e < max_nnz ? e : max_nnz) + (uint32_t)offset);
+  }
+  if (c == 0 && tid == 0) indptr[b * (rows + 1)] = offset;
+  __syncthreads();
+  S* drow = data + b * max_nnz;
+  int32_t* crow = indices + b * max_nnz;
+  {
+    const int64_t lo = tot < max_nnz ? tot : max_nnz, span = max_nnz - lo;
+    const int64_t a1 = lo + span * (c + 1) / nchunk;
+    for (int64_t j = lo + span * c / nchunk + tid; j < a1; j += 256) {
+      drow[j] = (S)0;
+      crow[j] = -1;
+    }
+  }
+  const int64_t run0 = first[0];
+  const int64_t run1 = min64(pre + (wtot[0] + wtot[1] + wtot[2] + wtot[3]), max_nnz);
+  constexpr int P = 4;  // slots per thread in flight
+  for (int64_t p0 = run0 + tid; sg.slots > 0 && p0 < run1; p0 += 256 * P) {
+    S dv[P];
+    int32_t cv[P];
+    bool take[P];
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      const int64_t p = p0 + 256 * u;
+      // the chunk row whose run holds slot p: the last i < nr with first[i] <= p
+      int lo = 0, hi = (int)nr - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (first[mid] <= p) lo = mid;
+        else hi = mid - 1;
+      }
+      take[u] = p < run1 && ncnt[lo] <= sg.slots;
+      // a slot not taken reads staging entry 0 (slots > 0 here)
+      const int64_t k = take[u] ? (b * rows + r0 + lo) * sg.slots + (p - first[lo]) : 0;
+      dv[u] = ((const S*)sg.val)[k];
+      cv[u] = sg.col[k];
+    }
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      if (take[u]) {
+        drow[p0 + 256 * u] = dv[u];
+        crow[p0 + 256 * u] = cv[u];
+      }
+    }
+  }
+  for (int64_t i = wv; i < nr; i += 4) {
+    const int64_t p0 = first[i], n = ncnt[i];
+    if (n <= sg.slots || p0 >= max_nnz) continue;
+    const S* row = x + (b * rows + r0 + i) * cols;
+    int64_t pos = p0;
+    for (int64_t c0 = 0; c0 < cols && pos < max_nnz; c0 += 64 * V) {
+      const int64_t cc = c0 + (int64_t)lane * V;
+      const bool ok = cc < cols;
+      Group<S, V> grp;
+      grp.load(row + (ok ? cc : cols - V));
+      bool f[V];
+      uint32_t below = 0, n_grp = 0;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        f[j] = ok && is_outlier(FT<DT>::val(grp.get(j)), t);
+        const uint64_t m = __ballot(f[j]);
+        below += lanes_below(m);
+        n_grp += (uint32_t)__popcll(m);
+      }
+      int64_t q = pos + below;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        if (f[j]) {
+          if (q < max_nnz) {
+            drow[q] = (S)grp.get(j);
+            crow[q] = (int32_t)(cc + j);
+          }
+          ++q;
+        }
+      }
+      pos += n_grp;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -638,6 +826,75 @@ void launch_split_mx(const uint16_t* x, int64_t nb, int64_t rows, int64_t cols, 
                      dim3(256), 0, st, x, nb, rows, cols, t, indptr, max_nnz, values, data, indices, mf);
 }
 
+// One-pass workspace: counts [nrows] int32 (256-byte aligned block), then the
+// staging columns [nrows][slots] int32 and values [nrows][slots] (x's
+// storage type).  The slots per row follow from the bytes given.
+size_t stage_counts_bytes(int64_t nrows) { return ((size_t)nrows * 4 + 255) & ~(size_t)255; }
+
+int stage_from_workspace(void* ws, int64_t ws_bytes, int64_t nrows, int64_t cols, int es, Stage* sg,
+                         const char* what) {
+  *sg = Stage{};
+  if (nrows == 0) return kOk;
+  const size_t cb = stage_counts_bytes(nrows);
+  if (!ws || ws_bytes < 0 || (size_t)ws_bytes < cb)
+    return set_error(kErrInvalid, "%s: workspace of %lld bytes, at least %zu needed", what, (long long)ws_bytes, cb);
+  if (((uintptr_t)ws & 255) != 0) return set_error(kErrInvalid, "%s: workspace must be 256-byte aligned", what);
+  int64_t slots = (int64_t)(((size_t)ws_bytes - cb) / ((size_t)nrows * (size_t)(4 + es)));
+  if (slots > cols) slots = cols;
+  sg->counts = (int32_t*)ws;
+  sg->col = (int32_t*)((char*)ws + cb);
+  sg->val = (char*)ws + cb + (size_t)nrows * (size_t)slots * 4;
+  sg->slots = slots;
+  return kOk;
+}
+
+template <int DT>
+int launch_finalize(const void* x, bool wide, int64_t nb, int64_t rows, int64_t cols, float t, const Stage& sg,
+                    int64_t max_nnz, int32_t offset, void* data, int32_t* indices, int32_t* indptr, hipStream_t st) {
+  using S = typename FT<DT>::S;
+  constexpr int V = FT<DT>::kVec;
+  // about 256 workgroups per batch: chunks of 16 to 256 rows
+  const int64_t chunk = std::min<int64_t>(256, std::max<int64_t>(16, (rows + 255) / 256));
+  const int64_t nchunk = rows > 0 ? (rows + chunk - 1) / chunk : 1;
+  if (nb * nchunk > INT32_MAX) return set_error(kErrInvalid, "filter_outlier: too many row chunks");
+  const dim3 grid((unsigned)(nb * nchunk));
+  if (wide)
+    hipLaunchKernelGGL((outlier_finalize_kernel<DT, V>), grid, dim3(256), 0, st, (const S*)x, rows, cols, t, sg,
+                       chunk, nchunk, max_nnz, offset, (S*)data, indices, indptr);
+  else
+    hipLaunchKernelGGL((outlier_finalize_kernel<DT, 1>), grid, dim3(256), 0, st, (const S*)x, rows, cols, t, sg,
+                       chunk, nchunk, max_nnz, offset, (S*)data, indices, indptr);
+  return kOk;
+}
+
+template <int DT>
+int launch_filter_ws(const void* x, int64_t nb, int64_t rows, int64_t cols, float t, int64_t max_nnz, int32_t offset,
+                     void* data, int32_t* indices, int32_t* indptr, void* inlier, const Stage& sg, hipStream_t st) {
+  using S = typename FT<DT>::S;
+  constexpr int V = FT<DT>::kVec;
+  const int64_t nrows = nb * rows;
+  const bool wide = cols % V == 0 && aligned(x, 16) && aligned(inlier, 16);
+  if (nrows > 0) {
+    const unsigned grid = grid_for(nrows, 4, 16);
+    if (wide)
+      hipLaunchKernelGGL((outlier_split_kernel<DT, V, false, 1, true>), dim3(grid), dim3(256), 0, st, (const S*)x,
+                         nb, rows, cols, t, nullptr, max_nnz, (S*)inlier, nullptr, nullptr, MxFuse{}, sg);
+    else
+      hipLaunchKernelGGL((outlier_split_kernel<DT, 1, false, 1, true>), dim3(grid), dim3(256), 0, st, (const S*)x,
+                         nb, rows, cols, t, nullptr, max_nnz, (S*)inlier, nullptr, nullptr, MxFuse{}, sg);
+  }
+  const int rc = launch_finalize<DT>(x, wide, nb, rows, cols, t, sg, max_nnz, offset, data, indices, indptr, st);
+  if (rc != kOk) return rc;
+  return check_launch("filter_outlier");
+}
+
+template <int LPB>
+void launch_split_mx_stage(const uint16_t* x, int64_t nb, int64_t rows, int64_t cols, float t, uint16_t* values,
+                           const MxFuse& mf, const Stage& sg, hipStream_t st) {
+  hipLaunchKernelGGL((outlier_split_kernel<kBF16, 8, true, LPB, true>), dim3(grid_for(nb * rows, 4, 16)),
+                     dim3(256), 0, st, x, nb, rows, cols, t, nullptr, (int64_t)0, values, nullptr, nullptr, mf, sg);
+}
+
 template <int DT>
 int launch_spmm(const SpmmArgs& a, hipStream_t st) {
   constexpr int V = FT<DT>::kVec;
@@ -703,6 +960,91 @@ int quantize_mx_outlier_fused(const void* x, int64_t nb, int64_t rows, int64_t c
     case 32: launch_split_mx<4>(xs, nb, rows, cols, threshold, indptr, max_nnz, v, d, indices, mf, st); break;
     default: launch_split_mx<8>(xs, nb, rows, cols, threshold, indptr, max_nnz, v, d, indices, mf, st); break;
   }
+  return check_launch("quantize_mx_outlier");
+}
+
+int64_t outlier_stage_slots(int64_t rows, int64_t cols, int64_t max_nnz) {
+  if (max_nnz <= 0 || rows <= 0 || cols <= 0) return 0;
+  const int64_t per = (max_nnz + rows - 1) / rows;
+  int64_t s = (2 * per + 63) / 64 * 64;
+  s = s < 64 ? 64 : (s > 1024 ? 1024 : s);
+  return s < cols ? s : cols;
+}
+
+int outlier_workspace_size(int dtype, int64_t nb, int64_t rows, int64_t cols, int64_t max_nnz, int64_t* bytes) {
+  if (!bytes) return set_error(kErrInvalid, "outlier_workspace_size: null result pointer");
+  if (nb < 0 || rows < 0 || cols < 0 || max_nnz < 0)
+    return set_error(kErrInvalid, "outlier_workspace_size: negative size");
+  int es;
+  switch (dtype) {
+    case kF32: es = 4; break;
+    case kBF16:
+    case kF16: es = 2; break;
+    default: return set_error(kErrInvalid, "outlier_workspace_size: dtype %d not supported (fp32, bf16, fp16)", dtype);
+  }
+  const int64_t nrows = nb * rows;
+  *bytes = nrows == 0 ? 0
+                      : (int64_t)(stage_counts_bytes(nrows) +
+                                  (size_t)nrows * (size_t)outlier_stage_slots(rows, cols, max_nnz) * (size_t)(4 + es));
+  return kOk;
+}
+
+int filter_outlier_ws(const void* x, int dtype, int64_t nb, int64_t rows, int64_t cols, float threshold,
+                      int64_t max_nnz, int32_t indptr_offset, void* data, int32_t* indices, int32_t* indptr,
+                      void* inlier, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+  if (nb < 0 || rows < 0 || cols < 0 || max_nnz < 0) return set_error(kErrInvalid, "filter_outlier: negative size");
+  if (nb == 0) return kOk;
+  if (!indptr || (max_nnz > 0 && (!data || !indices)) || (rows * cols > 0 && (!x || !inlier)))
+    return set_error(kErrInvalid, "filter_outlier: null buffer");
+  if (max_nnz > INT32_MAX || rows >= INT32_MAX || cols > INT32_MAX)
+    return set_error(kErrInvalid, "filter_outlier: sizes beyond int32 indices");
+  const int es = dtype == kF32 ? 4 : 2;
+  if (dtype != kF32 && dtype != kBF16 && dtype != kF16)
+    return set_error(kErrInvalid, "filter_outlier: dtype %d not supported (fp32, bf16, fp16)", dtype);
+  Stage sg;
+  if (stage_from_workspace(workspace, workspace_bytes, nb * rows, cols, es, &sg, "filter_outlier") != kOk)
+    return kErrInvalid;
+  switch (dtype) {
+    case kF32: return launch_filter_ws<kF32>(x, nb, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr, inlier, sg, st);
+    case kBF16: return launch_filter_ws<kBF16>(x, nb, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr, inlier, sg, st);
+    default: return launch_filter_ws<kF16>(x, nb, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr, inlier, sg, st);
+  }
+}
+
+int quantize_mx_outlier_fused_ws(const void* x, int64_t nb, int64_t rows, int64_t cols, float threshold,
+                                 int64_t max_nnz, int32_t indptr_offset, int64_t block_size, const ScaleParams& sp,
+                                 const uint16_t* qmap, void* data, int32_t* indices, int32_t* indptr, void* scale,
+                                 void* values, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+  if (nb < 0 || rows < 0 || cols < 0 || max_nnz < 0)
+    return set_error(kErrInvalid, "quantize_mx_outlier: negative size");
+  if (block_size != 8 && block_size != 16 && block_size != 32 && block_size != 64)
+    return set_error(kErrUnsupported, "quantize_mx_outlier: fused form takes blocks of 8, 16, 32 or 64");
+  if (cols % block_size) return set_error(kErrUnsupported, "quantize_mx_outlier: cols must be whole blocks");
+  if (nb == 0) return kOk;
+  if (!indptr || !qmap || (max_nnz > 0 && (!data || !indices)) ||
+      (rows * cols > 0 && (!x || !values || !scale)))
+    return set_error(kErrInvalid, "quantize_mx_outlier: null buffer");
+  if (max_nnz > INT32_MAX || rows >= INT32_MAX || cols > INT32_MAX)
+    return set_error(kErrInvalid, "quantize_mx_outlier: sizes beyond int32 indices");
+  if (!aligned(x, 16) || !aligned(values, 16))
+    return set_error(kErrInvalid, "quantize_mx_outlier: input and values must be 16-byte aligned");
+  Stage sg;
+  if (stage_from_workspace(workspace, workspace_bytes, nb * rows, cols, 2, &sg, "quantize_mx_outlier") != kOk)
+    return kErrInvalid;
+  const uint16_t* xs = (const uint16_t*)x;
+  if (nb * rows > 0) {
+    MxFuse mf{sp, qmap, (uint16_t*)scale};
+    uint16_t* v = (uint16_t*)values;
+    switch (block_size) {
+      case 8: launch_split_mx_stage<1>(xs, nb, rows, cols, threshold, v, mf, sg, st); break;
+      case 16: launch_split_mx_stage<2>(xs, nb, rows, cols, threshold, v, mf, sg, st); break;
+      case 32: launch_split_mx_stage<4>(xs, nb, rows, cols, threshold, v, mf, sg, st); break;
+      default: launch_split_mx_stage<8>(xs, nb, rows, cols, threshold, v, mf, sg, st); break;
+    }
+  }
+  const int rc = launch_finalize<kBF16>(x, true, nb, rows, cols, threshold, sg, max_nnz, indptr_offset, data, indices,
+                                        indptr, st);
+  if (rc != kOk) return rc;
   return check_launch("quantize_mx_outlier");
 }
 

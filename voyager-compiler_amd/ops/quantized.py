@@ -726,9 +726,18 @@ def _outlier_csr(input, threshold, max_pct, indptr_offset):
     indices = torch.empty((*batch_shape, max_nnz), dtype=torch.int32, device=dev)
     indptr = torch.empty((*batch_shape, R + 1), dtype=torch.int32, device=dev)
     inlier = torch.empty_like(x)
-    _lib.call("vqx_filter_outlier", _lib.ptr(x), tag, nb, R, C, t, max_nnz, int(indptr_offset), _lib.ptr(data),
-              _lib.ptr(indices), _lib.ptr(indptr), _lib.ptr(inlier), _lib.stream_of(x))
+    ws = _outlier_workspace(tag, nb, R, C, max_nnz, dev)
+    _lib.call("vqx_filter_outlier_ws", _lib.ptr(x), tag, nb, R, C, t, max_nnz, int(indptr_offset), _lib.ptr(data),
+              _lib.ptr(indices), _lib.ptr(indptr), _lib.ptr(inlier), _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
     return data, indices, indptr, inlier
+
+
+def _outlier_workspace(tag, nb, R, C, max_nnz, dev):
+    """Staging memory of the one-pass outlier split: each row's count and its
+    first outliers (the library sizes it; the caching allocator keeps it)."""
+    n = ctypes.c_int64(0)
+    _lib.call("vqx_outlier_workspace_size", tag, nb, R, C, max_nnz, ctypes.byref(n))
+    return torch.empty(max(n.value, 1), dtype=torch.uint8, device=dev)
 
 
 @_impl("filter_outlier")
@@ -780,9 +789,10 @@ def _quantize_mx_outlier_fused(input, qmap, block_size, quant_max, force_pow2, s
     table = _table_bf16(qmap.to(dev))
     sq = _table_bf16(scale_qmap.to(dev)) if (scale_qmap is not None and not force_pow2) else None
     shift = math.floor(math.log2(quant_max)) if force_pow2 else 0
-    _lib.call("vqx_quantize_mx_outlier", _lib.ptr(x), nb, R, C, t, max_nnz, int(indptr_offset), block_size,
-              0 if force_pow2 else 1, shift, float(quant_max), _lib.ptr(sq), _lib.ptr(table), _lib.ptr(data),
-              _lib.ptr(indices), _lib.ptr(indptr), _lib.ptr(scale), _lib.ptr(values), _lib.stream_of(x))
+    ws = _outlier_workspace(_lib.dtype_tag(x.dtype), nb, R, C, max_nnz, dev)
+    _lib.call("vqx_quantize_mx_outlier_ws", _lib.ptr(x), nb, R, C, t, max_nnz, int(indptr_offset), block_size,
+              0 if force_pow2 else 1, shift, float(quant_max), _lib.ptr(sq), _lib.ptr(table), _lib.ptr(data), _lib.ptr(indices), _lib.ptr(indptr), _lib.ptr(scale), _lib.ptr(values), _lib.ptr(ws),
+              ws.numel(), _lib.stream_of(x))
     return data, indices, indptr, scale, values
 
 
