@@ -67,6 +67,36 @@ def test_gwa_special_values_and_scale_qmap(vqx, dt):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("bs", [8, 64])
+def test_gwa_quotients_near_and_below_the_normal_range(vqx, bs):
+    # bf16 blocks whose quotients x / scale fall among the bf16 subnormals
+    # (where rounding midpoints can be hit exactly), whose scale is itself
+    # subnormal or infinite, and blocks of mixed magnitudes from 2^-140 to
+    # 2^100, against the oracle's IEEE divisions
+    from importlib import import_module
+
+    qops = import_module(vqx.__name__ + ".ops.quantized")
+    g = torch.Generator().manual_seed(17)
+    sub = 2.0 ** -133
+    rows = [
+        torch.cat([torch.tensor([1.0]), torch.arange(1, 64) * sub]),              # subnormal quotients
+        torch.cat([torch.tensor([3.0 * 2 ** -126]), torch.arange(1, 64) * sub]),  # ties near 2^-126
+        torch.randint(-100, 100, (64,), generator=g) * sub,                      # subnormal scale
+        torch.tensor([3e38, -3e38] * 32),                                          # range overflows
+        torch.tensor([1.5 * 2 ** -120] + [float(k) * 2 ** -130 for k in range(63)]),
+    ]
+    for _ in range(27):
+        e = torch.randint(-140, 100, (64,), generator=g).float()
+        sgn = torch.where(torch.rand(64, generator=g) < 0.5, -1.0, 1.0)
+        rows.append(sgn * torch.exp2(e) * (1 + torch.rand(64, generator=g)))
+    x = torch.stack(rows).to(torch.bfloat16)
+    sf, zp, y = qops.gwa_fake_quantize(x.cuda(), -1, bs, 0, 3)
+    rsf, rzp, ry = R.group_wise_affine_fake_quant(x, -1, bs, 0, 3)
+    assert same(sf, rsf) and same(zp, rzp), "scale / zero point"
+    assert same(y, ry), f"{int((y.cpu().float() != ry.float()).sum())} outputs differ"
+
+
+@pytest.mark.gpu
 def test_gwa_fakequantize_module(vqx):
     """FusedAmaxObsFakeQuantize with qscheme group_wise_affine (uint2 KV-cache
     style, fake_quantize.py:409-420): output and the scale / zero_point buffers."""

@@ -364,11 +364,27 @@ __global__ __launch_bounds__(256) void gwa_fq_kernel(const T* __restrict__ x, in
 // order adds is which of +0 and -0 a min or max keeps, and neither sf
 // (max - min, then 1 where not > 0) nor zp (-min / sf + qmin) nor y changes
 // with it.
+// v from the lane that DPP control CTRL names (within rows of 16 lanes)
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+
 template <typename T, int G>
 __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ x, int64_t nchunks, float qmin,
                                                           float qmax, const uint16_t* __restrict__ scale_qmap,
                                                           T* scale_out, T* zp_out, T* __restrict__ y) {
   const float qrange = qmax - qmin;
+  // qrange as a bf16 value (at most 8 significant bits) and its reciprocal
+  const bool qr_exact = (f2u(qrange) & 0xFFFFu) == 0 && ((f2u(qrange) >> 23) & 0xFFu) - 1u < 252u;
+  const float qr_rcp = __builtin_amdgcn_rcpf(qrange);
+  // 0 < |q| < 2^-125: a quotient among the subnormals, or within one binade
+  // of them (a margin for the rounding of the fast quotient)
+  auto tiny = [](float q) { return (f2u(q) & 0x7FFFFFFFu) - 1u < 0x00FFFFFFu; };
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   // every lane runs the same number of iterations (nchunks is a multiple of
   // G and the stride of 256), so the shuffles see whole groups
@@ -390,23 +406,44 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
     }
     float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
     int nan = 0;
+    // fminf / fmaxf (v_min / v_max) skip NaN operands; the NaN flag stands in
+    // for them, and which zero a min or max keeps changes nothing (see above)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       nan |= v[i] != v[i];
-      mn = v[i] < mn ? v[i] : mn;
-      mx = v[i] > mx ? v[i] : mx;
+      mn = __builtin_fminf(mn, v[i]);
+      mx = __builtin_fmaxf(mx, v[i]);
     }
-#pragma unroll
-    for (int m = 1; m < G; m <<= 1) {
-      const float omn = __shfl_xor(mn, m, 64), omx = __shfl_xor(mx, m, 64);
-      nan |= __shfl_xor(nan, m, 64);
-      mn = omn < mn ? omn : mn;
-      mx = omx > mx ? omx : mx;
-    }
+    // over the block's G lanes with DPP: XOR 1 and XOR 2 within quads, then
+    // the half-row mirror, which pairs the two quads of 8 lanes
+    auto combine = [&](float omn, float omx, int onan) {
+      nan |= onan;
+      mn = __builtin_fminf(mn, omn);
+      mx = __builtin_fmaxf(mx, omx);
+    };
+    if constexpr (G >= 2) combine(dpp_f<0xB1>(mn), dpp_f<0xB1>(mx), dpp_i<0xB1>(nan));
+    if constexpr (G >= 4) combine(dpp_f<0x4E>(mn), dpp_f<0x4E>(mx), dpp_i<0x4E>(nan));
+    if constexpr (G >= 8) combine(dpp_f<0x141>(mn), dpp_f<0x141>(mx), dpp_i<0x141>(nan));
     if (nan) mn = mx = __builtin_nanf("");
-    float sf = round_to<T>(round_to<T>(mx - mn) / qrange);
-    sf = sf > 0.0f ? sf : 1.0f;
-    float zp = round_to<T>(round_to<T>(-mn / sf) + qmin);
+    float sf, zp;
+    if constexpr (sizeof(T) == 2) {
+      // both quotients have bf16 operands (qrange a bf16 integer), so a
+      // reciprocal multiply rounds like the IEEE division (as for x / sf
+      // below), with the same fallback
+      const float d = round_to<T>(mx - mn);
+      float q1 = d * qr_rcp;
+      if (!qr_exact || tiny(q1)) q1 = d / qrange;
+      sf = round_to<T>(q1);
+      sf = sf > 0.0f ? sf : 1.0f;
+      const uint32_t se = (f2u(sf) >> 23) & 0xFFu;
+      float q2 = -mn * __builtin_amdgcn_rcpf(sf);
+      if (se - 1u >= 252u || tiny(q2)) q2 = -mn / sf;
+      zp = round_to<T>(round_to<T>(q2) + qmin);
+    } else {
+      sf = round_to<T>(round_to<T>(mx - mn) / qrange);
+      sf = sf > 0.0f ? sf : 1.0f;
+      zp = round_to<T>(round_to<T>(-mn / sf) + qmin);
+    }
     if (scale_qmap) {
       sf = round_to<T>(bf2f(scale_qmap[f2bf(sf)]));
       zp = round_to<T>(bf2f(scale_qmap[f2bf(zp)]));
@@ -416,12 +453,85 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
       if (scale_out) BT<T>::put(scale_out + c / G, BT<T>::round_bits(sf));
       if (zp_out) BT<T>::put(zp_out + c / G, BT<T>::round_bits(zp));
     }
-    float o[8];
+    // x / sf, rounded to the element type.  bf16: x and sf are both bf16
+    // values, so x * rcp(sf) rounds to bf16 exactly as the IEEE quotient does
+    // (an exact quotient of two 8-bit significands lies at least 2^-16.86
+    // relative from every bf16 rounding midpoint, hazard H7, far beyond the
+    // few fp32 ulps of v_rcp_f32 and the product), except where the quotient
+    // falls below the normal range (bf16 subnormal midpoints can be hit
+    // exactly) or 1 / sf is not a normal float; those elements take the
+    // IEEE division.
+    float qd[8];
+    bool slow = true;
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t se = (f2u(sf) >> 23) & 0xFFu;
+      const float rs = __builtin_amdgcn_rcpf(sf);
+      slow = se - 1u >= 252u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float q = __builtin_rintf(round_to<T>(round_to<T>(v[i] / sf) + zp));
-      q = q < qmin ? qmin : (q > qmax ? qmax : q);  // NaN stays NaN
-      o[i] = round_to<T>(q - zp) * sf;
+      for (int i = 0; i < 8; ++i) {
+        qd[i] = v[i] * rs;
+        slow |= tiny(qd[i]);
+      }
+    }
+    if (slow) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qd[i] = v[i] / sf;
+    }
+    float o[8];
+    // bf16 and only finite values in all of the wave's blocks: then sf, zp
+    // and every intermediate are finite (|x / sf| stays below about 3 * 2^8,
+    // the block's range being at least one bf16 step of its values), so the
+    // clamp is one v_med3 and the stores go through v_cvt_pk_bf16_f32
+    const bool finite = __builtin_isfinite(mn) && __builtin_isfinite(mx);
+    const bool fast = sizeof(T) == 2 && __builtin_amdgcn_ballot_w64(!finite) == 0;
+    if (fast) {
+      u32x4 w;
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        uint32_t p = pack_bf16x2(qd[i], qd[i + 1]);
+        float a = u2f(p << 16) + zp, b = u2f(p & 0xFFFF0000u) + zp;
+        p = pack_bf16x2(a, b);
+        a = __builtin_amdgcn_fmed3f(__builtin_rintf(u2f(p << 16)), qmin, qmax) - zp;
+        b = __builtin_amdgcn_fmed3f(__builtin_rintf(u2f(p & 0xFFFF0000u)), qmin, qmax) - zp;
+        p = pack_bf16x2(a, b);
+        w[i / 2] = pack_bf16x2(u2f(p << 16) * sf, u2f(p & 0xFFFF0000u) * sf);
+      }
+      if constexpr (sizeof(T) == 2) *reinterpret_cast<u32x4*>(y + c * 8) = w;
+      continue;
+    }
+    if constexpr (sizeof(T) == 2) {
+      // the intermediate bf16 roundings two at a time (v_cvt_pk_bf16_f32:
+      // RNE as f2bf for every non-NaN value; a NaN stays a NaN, and the
+      // final store gives it f2bf's pattern)
+      auto rnd2 = [](float& a, float& b) {
+        const uint32_t p = pack_bf16x2(a, b);
+        a = u2f(p << 16);
+        b = u2f(p & 0xFFFF0000u);
+      };
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        float a = qd[i], b = qd[i + 1];
+        rnd2(a, b);
+        a += zp;
+        b += zp;
+        rnd2(a, b);
+        a = __builtin_rintf(a);
+        b = __builtin_rintf(b);
+        a = a < qmin ? qmin : (a > qmax ? qmax : a);  // NaN stays NaN
+        b = b < qmin ? qmin : (b > qmax ? qmax : b);
+        a -= zp;
+        b -= zp;
+        rnd2(a, b);
+        o[i] = a * sf;
+        o[i + 1] = b * sf;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float q = __builtin_rintf(round_to<T>(round_to<T>(qd[i]) + zp));
+        q = q < qmin ? qmin : (q > qmax ? qmax : q);  // NaN stays NaN
+        o[i] = round_to<T>(q - zp) * sf;
+      }
     }
     if constexpr (sizeof(T) == 2) {
       u32x4 w;
