@@ -1074,10 +1074,18 @@ __device__ __forceinline__ void decode_chunks(const uint8_t* __restrict__ codes,
     }
     const float s = load_scale(scale, scale_kind, e / bs);
     if constexpr (E == 8) {
-      uint32_t o[8];
+      u32x4 v;
+      if (__builtin_isfinite(s)) {
+        // finite products: v_cvt_pk_bf16_f32 rounds them as f2bf does
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(tab[c[j]]) * s);
-      u32x4 v = {o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+        for (int j = 0; j < 4; ++j)
+          v[j] = pack_bf16x2(bf2f(tab[c[2 * j]]) * s, bf2f(tab[c[2 * j + 1]]) * s);
+      } else {
+        uint32_t o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(tab[c[j]]) * s);
+        v = u32x4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+      }
       st_nt(reinterpret_cast<u32x4*>(out + e), v);
     } else {
       f32x4 v = {bf2f(tab[c[0]]) * s, bf2f(tab[c[1]]) * s, bf2f(tab[c[2]]) * s, bf2f(tab[c[3]]) * s};
