@@ -350,7 +350,17 @@ __global__ __launch_bounds__(256) void outlier_split_kernel(const typename FT<DT
           const uint32_t sb = f2u(sc), se = (sb >> 23) & 0xFFu;
           const bool p2 = (sb & 0x807FFFFFu) == 0 && se - 1u < 253u;
           uint32_t qv[V];
-          if (__builtin_amdgcn_ballot_w64(!p2) == 0) {
+          if (__builtin_amdgcn_ballot_w64(!p2 || am > 0x7F80u) == 0) {
+            // no NaN inlier in the wave: v_cvt_pk_bf16_f32 rounds the
+            // quotients two at a time, as f2bf does for every non-NaN value
+            const float rc = u2f((254u - se) << 23);
+#pragma unroll
+            for (int j = 0; j < V; j += 2) {
+              const uint32_t h = pack_bf16x2(bf2f(keep[j]) * rc, bf2f(keep[j + 1]) * rc);
+              qv[j] = mf.qmap[h & 0xFFFFu];
+              qv[j + 1] = mf.qmap[h >> 16];
+            }
+          } else if (__builtin_amdgcn_ballot_w64(!p2) == 0) {
             const float rc = u2f((254u - se) << 23);
 #pragma unroll
             for (int j = 0; j < V; ++j) qv[j] = mf.qmap[f2bf(bf2f(keep[j]) * rc)];
