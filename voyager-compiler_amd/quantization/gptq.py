@@ -206,7 +206,7 @@ def compensate_with_factor(weight, hinv, salience, fake_quant, shrink=False):
                           float(fake_quant.quant_max), _lib.ptr(sq), _lib.ptr(hinv), hinv.shape[1], _lib.ptr(qmap),
                           _lib.ptr(out), _lib.ptr(d), deltas.stride(0), _lib.stream_of(work))
                 if hi < stop:
-                    work[:, hi:stop].sub_(d @ hinv[lo:hi, hi:stop])
+                    work[:, hi:stop].addmm_(d, hinv[lo:hi, hi:stop], alpha=-1.0)
         if stop < C:
             work[:, stop:].addmm_(deltas, hinv[outer:stop, stop:], alpha=-1.0)
     return out
