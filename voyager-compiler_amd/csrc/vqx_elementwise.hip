@@ -186,8 +186,14 @@ typedef __attribute__((address_space(3))) const uint32_t lds_cu32;
 // threshold for the sign, and one LDS read giving value and code together.
 // Other groups, and every group under a non-unit scale, take the exact
 // per-element route (IEEE division, full table beyond S).
+// 1024 threads: sixteen waves share one copy of the table, which a 27 KB
+// posit8 table would otherwise limit to six workgroups of four waves per CU,
+// and each workgroup's fill serves four times the waves (C1 28.4 us with 256
+// threads, 27.0-27.5 with 512, 26.2-26.5 with 1024)
+constexpr int kFqLutThreads = 1024;
+
 template <typename T, int CB>
-__global__ __launch_bounds__(256) void fq_lut_kernel(const T* __restrict__ x, T* __restrict__ y,
+__global__ __launch_bounds__(kFqLutThreads) void fq_lut_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                      void* __restrict__ codes, int64_t n,
                                                      const float* __restrict__ scale, bool mul, LutView lv) {
   extern __shared__ uint32_t lds_lut[];
@@ -376,12 +382,12 @@ static int launch_fq_lut(const T* x, T* y, void* codes, int code_bytes, int64_t 
   size_t lds = sizeof(uint32_t) * 2 * lv.len;
   if (code_bytes == 0) {
     auto k = fq_lut_kernel<T, 0>;
-    unsigned grid = persistent_grid((const void*)k, 256, lds, n / 8 + 1);
-    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, st, x, y, codes, n, scale, mul, lv);
+    unsigned grid = persistent_grid((const void*)k, kFqLutThreads, lds, n / 8 + 1);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kFqLutThreads), lds, st, x, y, codes, n, scale, mul, lv);
   } else {
     auto k = fq_lut_kernel<T, 1>;
-    unsigned grid = persistent_grid((const void*)k, 256, lds, n / 8 + 1);
-    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, st, x, y, codes, n, scale, mul, lv);
+    unsigned grid = persistent_grid((const void*)k, kFqLutThreads, lds, n / 8 + 1);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kFqLutThreads), lds, st, x, y, codes, n, scale, mul, lv);
   }
   return check_launch("fake_quant(lut)");
 }
