@@ -659,8 +659,14 @@ __device__ __forceinline__ void half_swap(u32x4& a, u32x4& b) {
 // clamping after it, the bounds being bf16 values), one compare against a
 // uniform threshold picking the sign's table base, and one LDS read at that
 // base plus the clamped quotient's bf16 bits, scaled to the entry size.
+// 1024 threads: sixteen waves share one copy of the tables and each
+// workgroup's fill serves them all (C2 20.1-20.4 us with 256 threads,
+// 19.8-19.9 with 1024; C3 e4m3 36.7 -> 35.4, e2m1 31.0 -> 30.2, fake-quant
+// 51.2 -> 49.4; e3m2 unchanged)
+constexpr int kMxLutThreads = 1024;
+
 template <int CB, int LPB, bool ABSMAX, int WANT, bool CT>
-__global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict__ x, int64_t ngroups,
+__global__ __launch_bounds__(kMxLutThreads) void mx_lut_kernel(const uint16_t* __restrict__ x, int64_t ngroups,
                                                      ScaleParams sp, LutView lv, MxOut out) {
   static_assert(!CT || (WANT == 0 && (CB == 4 || CB == 8)), "code tables serve packed 4- or 8-bit codes only");
   extern __shared__ uint32_t lds_lut[];
@@ -867,17 +873,17 @@ __global__ __launch_bounds__(256) void mx_lut_kernel(const uint16_t* __restrict_
 template <int CB, int LPB, bool ABSMAX, int WANT>
 static int launch_lut_k(const uint16_t* x, int64_t ngroups, const ScaleParams& sp, const LutView& lv,
                         const MxOut& out, hipStream_t st) {
-  const int bs = 256;
+  const int bs = kMxLutThreads;
   // codes-only outputs use the code tables where they fit
   constexpr bool kCodes = WANT == 0 && (CB == 4 || CB == 8);
   if (kCodes && (CB == 8 || (int64_t)lv.len * 2 <= kCodeCopy2)) {
     auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT, kCodes>;
     size_t lds = CB == 4 ? kCodeCopy2 + (size_t)lv.len * 2 : (size_t)lv.len * 2;
     unsigned grid = persistent_grid((const void*)k, bs, lds, ngroups);
-    // byte codes stream fastest from 4 workgroups per CU (C3 e4m3 36.3-36.6
-    // us against 37.3-37.6 at full occupancy; every other form of this
-    // kernel is fastest at full occupancy, 5-7 per CU measured too)
-    if (CB == 8 && grid > (unsigned)num_cus() * 4u) grid = (unsigned)num_cus() * 4u;
+    // byte codes stream fastest from 16 waves per CU (C3 e4m3 35.4 us
+    // against 36.7 at full occupancy; every other form of this kernel is
+    // fastest at full occupancy)
+    if (CB == 8 && grid > (unsigned)num_cus()) grid = (unsigned)num_cus();
     hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out);
   } else {
     auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT, false>;
