@@ -369,11 +369,12 @@ def setup_c5_linear_mx(vqx, torch, L, M=2048):
         bound="mfma", dtype="bf16", cpu=cpu_c5(torch, Ac, N), keep=(A, idx, scale, code))
 
 
-def setup_c5_skinny(vqx, torch, L, M):
+def setup_c5_skinny(vqx, torch, L, M, N=11008):
     """C5's weight with a decode-time batch of M rows (the skinny kernel,
-    bound by the 4-bit weight's bytes)."""
+    bound by the 4-bit weight's bytes); N = 4096 is a 7B attention
+    projection."""
     g = torch.Generator().manual_seed(4)
-    N, K = 11008, 4096
+    K = 4096
     Ac = torch.randn(M, K, generator=g).to(torch.bfloat16)
     A = Ac.cuda()
     W = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).cuda()
@@ -385,7 +386,7 @@ def setup_c5_skinny(vqx, torch, L, M):
     fn = L.load().vqx_nf4_linear
     args = (L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), M, N, K, L.stream_of(A))
     return (lambda: fn(*args)), dict(
-        name=f"C5 skinny NF4-dequant linear: A bf16 [{M},4096] x W NF4 block-64 [11008,4096]^T -> bf16",
+        name=f"C5 skinny NF4-dequant linear: A bf16 [{M},4096] x W NF4 block-64 [{N},4096]^T -> bf16",
         elements=M * N, bytes=N * K // 2 + N * K // 64 * 4 + M * K * 2 + M * N * 2, flops=2 * M * N * K,
         bound="hbm", dtype="bf16", keep=(A, codes, sc, lv, out), cpu=cpu_c5(torch, Ac, N))
 
@@ -574,6 +575,7 @@ CONFIGS = {
     "c5_m256": lambda v, t, L: setup_c5(v, t, L, M=256),
     "c5_m1": lambda v, t, L: setup_c5_skinny(v, t, L, 1),
     "c5_m16": lambda v, t, L: setup_c5_skinny(v, t, L, 16),
+    "c5_m1_n4096": lambda v, t, L: setup_c5_skinny(v, t, L, 1, N=4096),
     "f3_gwa": lambda v, t, L: setup_f3(v, t, L),
     "o1_filter": lambda v, t, L: setup_o1(v, t, L),
     "o2_quantize_mx_outlier": lambda v, t, L: setup_o1(v, t, L, mx=True),
@@ -736,6 +738,7 @@ DOMINANT = {
     "c5_m256_whole_tiles": "nf4_gemm_kernel",
     "c5_m1": "nf4_skinny_kernel",
     "c5_m16": "nf4_skinny_kernel",
+    "c5_m1_n4096": "nf4_skinny_kernel",
     "f3_gwa": "gwa_fq_rows_kernel<unsigned short, 8>",
     "o1_filter": "outlier_split_kernel<1, 8, false, 1, true>",
     "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8, true, 4, true>",

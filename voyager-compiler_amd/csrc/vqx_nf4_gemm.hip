@@ -545,7 +545,10 @@ __global__ void nf4_zero_counters(int* __restrict__ cnt, int n) {
 // are idle most of the time: the decode's VALU and the weight's bytes bound
 // the kernel.
 // ---------------------------------------------------------------------------
-constexpr int kSkinnyWaves = 4;
+// Waves per workgroup (each a 1/W share of K): 4, or 8 / 16 when N is too
+// small for 16-column workgroups of 4 waves to give every CU about eight
+// waves (N = 4096 at M = 1: 256 workgroups).
+constexpr int kSkinnyWavesMin = 4, kSkinnyWavesMax = 16;
 
 // scaled_levels for two 16-lane rows that share one scale (rows 2 j and
 // 2 j + 1 of the wave): the even row scales levels 0-7, the odd row levels
@@ -574,14 +577,15 @@ __device__ __forceinline__ LevelBytes row_pair_scaled_levels(const float (&lh)[8
   return t;
 }
 
-__global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uint16_t* __restrict__ A,
+template <int W>
+__global__ __launch_bounds__(64 * W) void nf4_skinny_kernel(const uint16_t* __restrict__ A,
                                                                         const uint8_t* __restrict__ codes,
                                                                         const float* __restrict__ scale,
                                                                         const uint16_t* __restrict__ levels,
                                                                         const uint16_t* __restrict__ bias,
                                                                         uint16_t* __restrict__ out, int M, int N,
                                                                         int K) {
-  __shared__ float part[kSkinnyWaves][16][16];  // [wave][row m][column]
+  __shared__ float part[W][16][16];  // [wave][row m][column]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
@@ -590,7 +594,7 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uin
   const int mm = r < M ? r : M - 1;
   const int kb = K / 64;
   const int steps = (K + 127) / 128;
-  const int s0 = steps * wave / kSkinnyWaves, s1 = steps * (wave + 1) / kSkinnyWaves;
+  const int s0 = steps * wave / W, s1 = steps * (wave + 1) / W;
   float lh[8];  // the row's eight levels as fp32: 0-7 in even 16-lane rows, 8-15 in odd
 #pragma unroll
   for (int c = 0; c < 8; ++c) lh[c] = u2f((uint32_t)levels[c + 8 * (g & 1)] << 16);
@@ -639,7 +643,7 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void nf4_skinny_kernel(const uin
     const int t = threadIdx.x, m = t >> 4, c = t & 15;
     float v = part[0][m][c];
 #pragma unroll
-    for (int w = 1; w < kSkinnyWaves; ++w) v += part[w][m][c];
+    for (int w = 1; w < W; ++w) v += part[w][m][c];
     const int n = n0 + c;
     if (m < M && n < N) {
       const float b = bias ? u2f((uint32_t)bias[n] << 16) : 0.0f;
@@ -844,8 +848,19 @@ int nf4_gemm(const uint16_t* A, const uint8_t* codes, const float* scale, const 
   if (!aligned(A, 16) || !aligned(codes, 16) || !aligned(out, 8) || (bias && !aligned(bias, 8)))
     return set_error(kErrInvalid, "nf4_gemm: A and codes must be 16-byte aligned, out and bias 8-byte aligned");
   if (M <= 16) {
-    hipLaunchKernelGGL(nf4_skinny_kernel, dim3((unsigned)((N + 15) / 16)), dim3(64 * kSkinnyWaves), 0, st, A, codes, scale,
-                       levels, bias, out, (int)M, (int)N, (int)K);
+    const unsigned tiles = (unsigned)((N + 15) / 16);
+    // about eight waves per CU, at most one wave per 128-k step
+    int w = kSkinnyWavesMin;
+    while (w < kSkinnyWavesMax && (int64_t)tiles * w < (int64_t)num_cus() * 8 && 2 * w <= (K + 127) / 128) w *= 2;
+    if (w == 16)
+      hipLaunchKernelGGL(nf4_skinny_kernel<16>, dim3(tiles), dim3(64 * 16), 0, st, A, codes, scale, levels, bias, out,
+                         (int)M, (int)N, (int)K);
+    else if (w == 8)
+      hipLaunchKernelGGL(nf4_skinny_kernel<8>, dim3(tiles), dim3(64 * 8), 0, st, A, codes, scale, levels, bias, out,
+                         (int)M, (int)N, (int)K);
+    else
+      hipLaunchKernelGGL(nf4_skinny_kernel<4>, dim3(tiles), dim3(64 * 4), 0, st, A, codes, scale, levels, bias, out,
+                         (int)M, (int)N, (int)K);
     return check_launch("nf4_skinny");
   }
   if (N % kBN)
