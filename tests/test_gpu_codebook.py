@@ -95,6 +95,21 @@ def test_codebook_sizes_and_shapes(vqx, K, rows, cols):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("K,rows,cols", [(16, 5, 4112), (100, 5, 4112), (256, 5, 4112), (256, 700, 3088),
+                                         (16, 4500, 2064)])
+def test_codebook_rows_shared_by_waves(vqx, K, rows, cols):
+    """Rows split over 2 or 4 waves (each taking every 2nd or 4th chunk and
+    building its own tree), the tail past the last whole chunk, and more
+    split rows than resident waves (each wave then takes several rows)."""
+    g = torch.Generator().manual_seed(77 + K + rows)
+    cb = random_codebooks(rows, K, g)
+    x = torch.randn(rows, cols, generator=g) * 1.5
+    x[:, -3:] = cb[:, :3]
+    codes = Q.codebook_encode(x.cuda(), cb.cuda())
+    assert torch.equal(codes.cpu().long(), R.codebook_encode_rows(x, cb))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("K", [2, 16, 256])
 def test_codebook_subnormals_and_signed_zeros(vqx, K):
     """Codebooks whose entries straddle zero at subnormal magnitudes, and

@@ -152,24 +152,31 @@ __device__ __forceinline__ void load_chunk(const T* xr, int64_t base, int lane, 
   }
 }
 
-// Per-channel encode.  Each wave works through its own rows (row gw, gw + nw,
-// ... for global wave gw of nw) with no workgroup barriers; the items it
-// streams are the 1024-element chunks of those rows in order, in two register
-// buffers used in turn: the next item's load is issued before the current one
-// is encoded, also across a row boundary, so loads stay in flight while a
-// row's search tree is built.  Rows and chunks are wave-uniform (the wave
-// index goes through readfirstlane), so the loop's branches are scalar.  The tree (see tree_slot) holds the row's K - 1
-// decision thresholds, padded with "no threshold" to 2^LOGP - 1, in the
+// Per-channel encode.  Each row is shared by `split` waves (1, 2 or 4: waves
+// gw and gw' with gw / split = gw' / split take the row's chunks s, s + split,
+// ... for s = gw % split), and each wave works through its own rows (row
+// gw / split, then + nw / split, ... for global wave gw of nw) with no
+// workgroup barriers; the items it streams are its 1024-element chunks of
+// those rows in order, in two register buffers used in turn: the next item's
+// load is issued before the current one is encoded, also across a row
+// boundary, so loads stay in flight while a row's search tree is built (each
+// wave builds its own copy).  Rows and chunks are wave-uniform (the wave index
+// goes through readfirstlane), so the loop's branches are scalar.  The tree
+// (see tree_slot) holds the row's K - 1 decision thresholds, padded with "no threshold" to 2^LOGP - 1, in the
 // wave's 1 KiB LDS slice.  The search walks LDS byte addresses A = B + 4n
 // (B: the slice, 1 KiB aligned): a step is A -> 2A - B + 4c, the root level
 // compares against a register copy, and the last step yields
-// A / 2 + c = B / 2 + 256 + code, whose low byte is the code.  fp32 inputs
+// A / 2 + c = B / 2 + 256 + code, whose low byte is the code.  A lane searches
+// G of its values at once, level by level, so G independent LDS reads are in
+// flight per wave at each level (G = 16 for the deep trees of 32 entries and
+// more, whose waves are few and long; G = 4 for the shallow ones, held to 64
+// registers so that 8 waves fit on each SIMD).  fp32 inputs
 // are rounded to bf16 two at a time (v_cvt_pk_bf16_f32: round to nearest
 // even, NaN kept, subnormals kept under the kernel's f32 denormal mode).
 template <typename T, int LOGP>
-__global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LOGP <= 4 ? 8 : 1))) void cb_encode_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
                                                         const float* __restrict__ cb, int K,
-                                                        uint8_t* __restrict__ codes) {
+                                                        uint8_t* __restrict__ codes, int split) {
   constexpr uint32_t kRoot = 1u << (8 - LOGP);
   __shared__ __attribute__((aligned(1024))) float s_tw[4][256];  // slot n of wave w at s_tw[w][n]
   __shared__ float s_cbw[4][kCbMaxK];
@@ -197,16 +204,45 @@ __global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x,
       return (A >> 1) + (lds_f32(A) <= f ? 1u : 0u);
     }
   };
+  // search for G values at once, level by level
+  constexpr int G = LOGP <= 4 ? 4 : 16;
+  auto searchG = [&](const float (&f)[G], uint32_t (&out)[G]) {
+    if constexpr (LOGP == 0) {
+#pragma unroll
+      for (int k = 0; k < G; ++k) out[k] = 0u;
+    } else if constexpr (LOGP == 1) {
+#pragma unroll
+      for (int k = 0; k < G; ++k) out[k] = root <= f[k] ? 1u : 0u;
+    } else {
+      uint32_t A[G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) A[k] = root <= f[k] ? kRight : kLeft;
+#pragma unroll
+      for (int l = 1; l < LOGP - 1; ++l) {
+        float t[G];
+#pragma unroll
+        for (int k = 0; k < G; ++k) t[k] = lds_f32(A[k]);
+#pragma unroll
+        for (int k = 0; k < G; ++k) A[k] = (A[k] << 1) + (t[k] <= f[k] ? kStep1 : kStep0);
+      }
+      float t[G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) t[k] = lds_f32(A[k]);
+#pragma unroll
+      for (int k = 0; k < G; ++k) out[k] = (A[k] >> 1) + (t[k] <= f[k] ? 1u : 0u);
+    }
+  };
   auto load_cb = [&](int64_t r, float (&c)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) c[j] = (r < rows && lane + 64 * j < K) ? cb[r * K + lane + 64 * j] : 0.0f;
   };
+  const int64_t nwr = nw / split, s = gw % split;
   float cbn[4];
-  load_cb(gw, cbn);
-  int64_t r = gw, c = 0;  // current item: chunk c of row r
+  load_cb(gw / split, cbn);
+  int64_t r = gw / split, c = s;  // current item: chunk c of row r
   // one item: encode chunk (r, c) from cur after loading the next item into nxt
   auto step = [&](const float (&cur)[16], float (&nxt)[16]) {
-    if (c == 0) {  // new row: its tree from the prefetched codebook
+    if (c == s) {  // new row: its tree from the prefetched codebook
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (lane + 64 * j < K) s_cb[lane + 64 * j] = cbn[j];
@@ -216,38 +252,46 @@ __global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x,
       for (int j = lane; j < (1 << LOGP) - 1; j += 64)
         s_t[tree_slot(j)] = threshold_value(j < K - 1 ? code_threshold(s_cb, K, j, gap, ok) : 0x10000u);
       tree = __builtin_amdgcn_ballot_w64(!ok) == 0;
-      load_cb(r + nw, cbn);
+      load_cb(r + nwr, cbn);
       wave_lds_sync();
       if constexpr (LOGP > 0) root = s_t[kRoot];
     }
-    const bool last = c + 1 >= nchunk;
-    const int64_t rn = last ? r + nw : r, cn = last ? 0 : c + 1;
+    const bool last = c + split >= nchunk;
+    const int64_t rn = last ? r + nwr : r, cn = last ? s : c + split;
     if (nchunk > 0) {
       if (rn < rows) load_chunk(x + rn * cols, cn * kCbChunk, lane, nxt);  // wave-uniform branch
       uint8_t* cr = codes + r * cols + c * kCbChunk;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float f[4];
-        if constexpr (std::is_same<T, float>::value) {
+      for (int h = 0; h < 16; h += G) {
+        float f[G];
 #pragma unroll
-          for (int k = 0; k < 4; k += 2) {
-            const uint32_t p = pack_bf16x2(cur[4 * q + k], cur[4 * q + k + 1]);
+        for (int k = 0; k < G; k += 2) {
+          if constexpr (std::is_same<T, float>::value) {
+            const uint32_t p = pack_bf16x2(cur[h + k], cur[h + k + 1]);
             f[k] = u2f(p << 16);
             f[k + 1] = u2f(p & 0xFFFF0000u);
+          } else {
+            f[k] = cur[h + k];  // bf16 values already
+            f[k + 1] = cur[h + k + 1];
           }
+        }
+        uint32_t code[G];
+        if (tree) {
+          searchG(f, code);
         } else {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) f[k] = cur[4 * q + k];  // bf16 values already
+          for (int k = 0; k < G; ++k) code[k] = nearest_sorted(s_cb, K, f[k]);
         }
-        const uint32_t w = tree ? pack_low_bytes(search(f[0]), search(f[1]), search(f[2]), search(f[3]))
-                                : pack_low_bytes(nearest_sorted(s_cb, K, f[0]), nearest_sorted(s_cb, K, f[1]),
-                                                 nearest_sorted(s_cb, K, f[2]), nearest_sorted(s_cb, K, f[3]));
-        __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(cr + q * 256 + lane * 4));
+#pragma unroll
+        for (int q = 0; q < G / 4; ++q) {
+          const uint32_t w = pack_low_bytes(code[4 * q], code[4 * q + 1], code[4 * q + 2], code[4 * q + 3]);
+          __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(cr + (h / 4 + q) * 256 + lane * 4));
+        }
       }
     }
     if (last) {  // row done: its tail
       const T* xr = x + r * cols;
-      for (int64_t i = full + lane; i < cols; i += 64) {
+      for (int64_t i = full + lane + (s == 0 ? 0 : cols); i < cols; i += 64) {
         float xv = std::is_same<T, float>::value ? u2f(pack_bf16x2((float)xr[i], 0.0f) << 16)
                                                  : u2f((uint32_t)((const uint16_t*)xr)[i] << 16);
         codes[r * cols + i] = (uint8_t)(tree ? search(xv) : nearest_sorted(s_cb, K, xv));
@@ -258,7 +302,7 @@ __global__ __launch_bounds__(256) void cb_encode_kernel(const T* __restrict__ x,
     c = cn;
   };
   float va[16], vb[16];
-  if (r < rows && nchunk > 0) load_chunk(x + r * cols, 0, lane, va);
+  if (r < rows && nchunk > 0) load_chunk(x + r * cols, c * kCbChunk, lane, va);
   while (r < rows) {
     step(va, vb);
     if (r >= rows) break;
@@ -340,16 +384,22 @@ __global__ __launch_bounds__(256) void cb_decode_kernel(const uint8_t* __restric
   }
 }
 
-// one wave per row, as many as fit on the device at once
+// split waves per row (1, 2 or 4: whichever leaves the fewest rows' worth of
+// chunks to the busiest wave), as many waves as fit on the device at once
 template <typename T>
 static void launch_encode(int logp, hipStream_t st, const T* x, int64_t rows, int64_t cols, const float* cb,
                           int K, uint8_t* codes) {
+  const int64_t nchunk = cols / kCbChunk;
 #define VQX_CB_CASE(L)                                                                                    \
-  case L:                                                                                                 \
-    hipLaunchKernelGGL((cb_encode_kernel<T, L>),                                                          \
-                       dim3(persistent_grid((const void*)cb_encode_kernel<T, L>, 256, 0, rows * 64)), dim3(256), \
-                       0, st, x, rows, cols, cb, K, codes);                                               \
-    break;
+  case L: {                                                                                               \
+    unsigned grid = persistent_grid((const void*)cb_encode_kernel<T, L>, 256, 0, rows * 64 * 4);          \
+    int split = 1;                                                                                        \
+    for (int sp = 2; sp <= 4 && sp <= nchunk; sp *= 2) /* fewest rows-worth per wave */                  \
+      if ((rows * sp + grid * 4 - 1) / (grid * 4) * split < (rows * split + grid * 4 - 1) / (grid * 4) * sp) split = sp; \
+    grid = (unsigned)std::min<int64_t>(grid, (rows * split + 3) / 4);                                     \
+    hipLaunchKernelGGL((cb_encode_kernel<T, L>), dim3(grid), dim3(256), 0, st, x, rows, cols, cb, K, codes, \
+                       split);                                                                            \
+  } break;
   switch (logp) {
     VQX_CB_CASE(0) VQX_CB_CASE(1) VQX_CB_CASE(2) VQX_CB_CASE(3) VQX_CB_CASE(4)
     VQX_CB_CASE(5) VQX_CB_CASE(6) VQX_CB_CASE(7) default: VQX_CB_CASE(8)
