@@ -310,14 +310,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(LOGP <= 4 ?
   }
 }
 
-// Per-channel decode, organised like the encode: each wave streams the
-// 1024-element chunks of its own rows through two register buffers, the next
-// chunk's codes loaded before the current one is written out, the row's table
-// (bf16 of each entry) in the wave's LDS slice.
+// Per-channel decode, organised like the encode: rows shared by `split` waves
+// in the same way, each wave streaming its 1024-element chunks of its rows
+// through two register buffers, the next chunk's codes loaded before the
+// current one is written out, the row's table (bf16 of each entry) in the
+// wave's LDS slice.
 template <typename T>
 __global__ __launch_bounds__(256) void cb_decode_kernel(const uint8_t* __restrict__ codes, int64_t rows,
                                                         int64_t cols, const float* __restrict__ cb, int K,
-                                                        T* __restrict__ out) {
+                                                        T* __restrict__ out, int split) {
   __shared__ float s_cbw[4][kCbMaxK];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -333,19 +334,20 @@ __global__ __launch_bounds__(256) void cb_decode_kernel(const uint8_t* __restric
 #pragma unroll
     for (int q = 0; q < 4; ++q) d[q] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p + q * 256 + lane * 4));
   };
+  const int64_t nwr = nw / split, s = gw % split;
   float cbn[4];
-  load_cb(gw, cbn);
-  int64_t r = gw, c = 0;
+  load_cb(gw / split, cbn);
+  int64_t r = gw / split, c = s;
   auto step = [&](const uint32_t(&cur)[4], uint32_t(&nxt)[4]) {
-    if (c == 0) {
+    if (c == s) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (lane + 64 * j < K) s_cb[lane + 64 * j] = bf2f(f2bf(cbn[j]));
-      load_cb(r + nw, cbn);
+      load_cb(r + nwr, cbn);
       wave_lds_sync();
     }
-    const bool last = c + 1 >= nchunk;
-    const int64_t rn = last ? r + nw : r, cn = last ? 0 : c + 1;
+    const bool last = c + split >= nchunk;
+    const int64_t rn = last ? r + nwr : r, cn = last ? s : c + split;
     if (nchunk > 0) {
       if (rn < rows) load(codes + rn * cols + cn * kCbChunk, nxt);  // wave-uniform branch
       T* orow = out + r * cols + c * kCbChunk;
@@ -365,7 +367,7 @@ __global__ __launch_bounds__(256) void cb_decode_kernel(const uint8_t* __restric
     if (last) {
       const uint8_t* cr = codes + r * cols;
       T* orow = out + r * cols;
-      for (int64_t i = full + lane; i < cols; i += 64) {
+      for (int64_t i = full + lane + (s == 0 ? 0 : cols); i < cols; i += 64) {
         float v = value(cr[i]);
         if constexpr (std::is_same<T, float>::value) orow[i] = v;
         else ((uint16_t*)orow)[i] = (uint16_t)(f2u(v) >> 16);
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(256) void cb_decode_kernel(const uint8_t* __restric
     c = cn;
   };
   uint32_t wa[4], wb[4];
-  if (r < rows && nchunk > 0) load(codes + r * cols, wa);
+  if (r < rows && nchunk > 0) load(codes + r * cols + c * kCbChunk, wa);
   while (r < rows) {
     step(wa, wb);
     if (r >= rows) break;
@@ -384,8 +386,20 @@ __global__ __launch_bounds__(256) void cb_decode_kernel(const uint8_t* __restric
   }
 }
 
-// split waves per row (1, 2 or 4: whichever leaves the fewest rows' worth of
-// chunks to the busiest wave), as many waves as fit on the device at once
+// Waves per row for the codebook kernels: 1, 2 or 4 (at most the row's whole
+// chunks), whichever leaves the fewest rows' worth of chunks to the busiest
+// of the grid's waves (grid: the resident workgroups of 4 waves); the grid is
+// then trimmed to the waves that have work.
+static int row_split(unsigned& grid, int64_t rows, int64_t nchunk) {
+  const int64_t nw = (int64_t)grid * 4;
+  int split = 1;
+  for (int sp = 2; sp <= 4 && sp <= nchunk; sp *= 2)
+    if ((rows * sp + nw - 1) / nw * split < (rows * split + nw - 1) / nw * sp) split = sp;
+  grid = (unsigned)std::min<int64_t>(grid, (rows * split + 3) / 4);
+  return split;
+}
+
+// row_split waves per row, as many waves as fit on the device at once
 template <typename T>
 static void launch_encode(int logp, hipStream_t st, const T* x, int64_t rows, int64_t cols, const float* cb,
                           int K, uint8_t* codes) {
@@ -393,10 +407,7 @@ static void launch_encode(int logp, hipStream_t st, const T* x, int64_t rows, in
 #define VQX_CB_CASE(L)                                                                                    \
   case L: {                                                                                               \
     unsigned grid = persistent_grid((const void*)cb_encode_kernel<T, L>, 256, 0, rows * 64 * 4);          \
-    int split = 1;                                                                                        \
-    for (int sp = 2; sp <= 4 && sp <= nchunk; sp *= 2) /* fewest rows-worth per wave */                  \
-      if ((rows * sp + grid * 4 - 1) / (grid * 4) * split < (rows * split + grid * 4 - 1) / (grid * 4) * sp) split = sp; \
-    grid = (unsigned)std::min<int64_t>(grid, (rows * split + 3) / 4);                                     \
+    const int split = row_split(grid, rows, nchunk);                                                      \
     hipLaunchKernelGGL((cb_encode_kernel<T, L>), dim3(grid), dim3(256), 0, st, x, rows, cols, cb, K, codes, \
                        split);                                                                            \
   } break;
@@ -432,15 +443,18 @@ int codebook_decode(const uint8_t* codes, int64_t rows, int64_t cols, const floa
   if (rows == 0 || cols == 0) return kOk;
   if (!aligned(out, 16) || !aligned(codes, 16) || (cols % 16) != 0)
     return set_error(kErrInvalid, "codebook decode needs 16-byte aligned rows (cols %% 16 == 0)");
-  const int64_t work = rows * 64;  // one wave per row
-  if (dtype == kF32)
-    hipLaunchKernelGGL((cb_decode_kernel<float>), dim3(persistent_grid((const void*)cb_decode_kernel<float>, 256, 0, work)),
-                       dim3(256), 0, st, codes, rows, cols, cb, K, (float*)out);
-  else if (dtype == kBF16)
-    hipLaunchKernelGGL((cb_decode_kernel<uint16_t>),
-                       dim3(persistent_grid((const void*)cb_decode_kernel<uint16_t>, 256, 0, work)), dim3(256), 0, st,
-                       codes, rows, cols, cb, K, (uint16_t*)out);
-  else
+  const int64_t work = rows * 64 * 4, nchunk = cols / kCbChunk;  // up to four waves per row
+  if (dtype == kF32) {
+    unsigned grid = persistent_grid((const void*)cb_decode_kernel<float>, 256, 0, work);
+    const int split = row_split(grid, rows, nchunk);
+    hipLaunchKernelGGL((cb_decode_kernel<float>), dim3(grid), dim3(256), 0, st, codes, rows, cols, cb, K,
+                       (float*)out, split);
+  } else if (dtype == kBF16) {
+    unsigned grid = persistent_grid((const void*)cb_decode_kernel<uint16_t>, 256, 0, work);
+    const int split = row_split(grid, rows, nchunk);
+    hipLaunchKernelGGL((cb_decode_kernel<uint16_t>), dim3(grid), dim3(256), 0, st, codes, rows, cols, cb, K,
+                       (uint16_t*)out, split);
+  } else
     return set_error(kErrInvalid, "codebook output dtype %d not supported", dtype);
   return check_launch("codebook_decode");
 }
