@@ -180,7 +180,7 @@ def setup_c1(vqx, torch, L):
     return (lambda: fn(*args)), dict(
         name="C1 posit8_1 fake-quant + uint8 codes, fp32 4096x4096 N(0,1) seed 0",
         elements=n, bytes=9 * n, bound="hbm", dtype="f32->u8", cpu=cpu_c1(torch, xc),
-        check=dict(x=xc, out=y, codes=codes))
+        check=dict(x=xc, out=y, codes=codes), keep=(x,))
 
 
 def c2_input(torch, rows=4096, cols=11008, seed=1):
@@ -211,7 +211,7 @@ def setup_c2(vqx, torch, L, decode=False):
             name="C2 NF4 block-64 absmax encode, bf16 4096x11008 N(0,0.02)+0.1% outliers seed 1 "
                  "-> packed 4-bit codes + fp32 scales",
             elements=n, bytes=algo, bound="hbm", dtype="bf16->u4", cpu_input=xc,
-            check=dict(x=xc, codes=codes, scale=scale))
+            check=dict(x=xc, codes=codes, scale=scale), keep=(x,))
     enc(*eargs)
     out = torch.empty_like(x)
     dtab = fmt.tables(x.device)["decode"]
@@ -220,7 +220,7 @@ def setup_c2(vqx, torch, L, decode=False):
     return (lambda: dec(*dargs)), dict(
         name="C2 NF4 block-64 decode: packed codes + fp32 scales -> bf16 4096x11008",
         elements=n, bytes=algo, bound="hbm", dtype="u4->bf16", cpu=cpu_c2_decode(torch, xc),
-        check=dict(x=xc, codes=codes, scale=scale, out=out))
+        check=dict(x=xc, codes=codes, scale=scale, out=out), keep=(x, dtab))
 
 
 def c3_input(torch, rows=8192, cols=8192, seed=2):
@@ -293,7 +293,7 @@ def setup_c4(vqx, torch, L, K, decode=False):
         return (lambda: enc(*eargs)), dict(
             name=f"C4 per-channel codebook encode K={K}, fp32 4096x4096 N(0,1) seed 3 -> uint8 indices",
             elements=n, bytes=algo, bound="hbm", dtype="f32->u8", cpu=cpu_c4(torch, xc, cbc, False),
-            check=dict(x=xc, codebooks=cbc, codes=codes))
+            check=dict(x=xc, codebooks=cbc, codes=codes), keep=(x, cb))
     enc(*eargs)
     out = torch.empty_like(x)
     dec = L.load().vqx_codebook_decode
@@ -301,7 +301,7 @@ def setup_c4(vqx, torch, L, K, decode=False):
     return (lambda: dec(*dargs)), dict(
         name=f"C4 per-channel codebook decode K={K}: uint8 indices -> fp32 4096x4096",
         elements=n, bytes=algo, bound="hbm", dtype="u8->f32", cpu=cpu_c4(torch, xc, cbc, True),
-        check=dict(x=xc, codebooks=cbc, codes=codes, out=out))
+        check=dict(x=xc, codebooks=cbc, codes=codes, out=out), keep=(x, cb))
 
 
 def setup_c5(vqx, torch, L, whole_tiles=False, M=2048):
@@ -518,7 +518,7 @@ def setup_o1(vqx, torch, L, mx=False):
         return (lambda: filt(*fargs)), dict(
             name=f"O1 filter_outlier, bf16 4096x11008 N(0,1) with 0.5% x32 seed 5, |x| > {OUTLIER_THRESHOLD}, "
                  f"capacity 1% -> CSR ({nnz} outliers) + inliers",
-            bytes=4 * n + csr_bytes, keep=(ws,), **common)
+            bytes=4 * n + csr_bytes, keep=(ws, x, bufs), **common)
     # the one-pass form: the split writes the quantized inliers and their
     # block scales instead of the inliers
     table = vqx.get_quantization_map("fp8_e4m3", "cuda")
@@ -532,7 +532,7 @@ def setup_o1(vqx, torch, L, mx=False):
     return (lambda: fused(*margs)), dict(
         name=f"O2 quantize_mx_outlier: O1's CSR and, in the same split pass, MX block-32 fp8_e4m3 power-of-two "
              f"scales and quantized values of the inliers -> CSR + bf16 scales + bf16 quantized inliers",
-        bytes=4 * n + n // 32 * 2 + csr_bytes, keep=(table, sc, qv, ws), **common)
+        bytes=4 * n + n // 32 * 2 + csr_bytes, keep=(table, sc, qv, ws, x, bufs), **common)
 
 
 def setup_o3(vqx, torch, L):
@@ -556,7 +556,7 @@ def setup_o3(vqx, torch, L):
         name=f"O3 spmm_csr: O1's CSR [4096 x 11008] ({nnz} entries) x bf16 [11008, 4096] ('ck') -> bf16, "
              f"fp32 accumulate",
         elements=R * N, bytes=nnz * 6 + 4 * (R + 1) + K * N * 2 + R * N * 2, gathered_bytes=nnz * N * 2,
-        flops=2 * nnz * N, bound="hbm", dtype="bf16", nnz=nnz, cpu_input=cpu, keep=bufs)
+        flops=2 * nnz * N, bound="hbm", dtype="bf16", nnz=nnz, cpu_input=cpu, keep=(bufs, B, out))
 
 
 CONFIGS = {

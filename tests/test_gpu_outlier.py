@@ -166,7 +166,7 @@ def spmm_bound(data, idx, ptr, Bd, layout):
 @pytest.mark.gpu
 @pytest.mark.parametrize("bdt", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("layout", ["kc", "ck"])
-@pytest.mark.parametrize("N", [256, 40, 7])
+@pytest.mark.parametrize("N", [256, 40, 7, 4624])
 def test_spmm_plain_matches_oracle(vqx, bdt, layout, N):
     x = rand_outliers((3, 24, 96), torch.bfloat16, seed=N, frac=0.1)
     d, i, p, _ = R.filter_outlier(x, 2.0, max_pct=0.3)
@@ -176,6 +176,20 @@ def test_spmm_plain_matches_oracle(vqx, bdt, layout, N):
     want = R.spmm_csr(d, i, p, B, None, None, None, layout)
     assert got.dtype == want.dtype == bdt and got.shape == want.shape
     assert_spmm_close(got, want, spmm_bound(d, i, p, B, layout), f"{bdt} {layout} N={N}")
+
+
+@pytest.mark.gpu
+def test_spmm_more_items_than_resident_waves(vqx):
+    """Rows x column slices well beyond the resident grid: each XCD's run of
+    the slice-major item sequence is taken by its waves in several passes,
+    and the runs' ends fall inside slices."""
+    x = rand_outliers((1, 3000, 96), torch.bfloat16, seed=11, frac=0.1)
+    d, i, p, _ = R.filter_outlier(x, 2.0, max_pct=0.3)
+    g = torch.Generator().manual_seed(2)
+    B = torch.randn(96, 4104, generator=g).to(torch.bfloat16)
+    got = Q.spmm_csr(d.cuda(), i.cuda(), p.cuda(), B.cuda(), None, None, None, "ck")
+    want = R.spmm_csr(d, i, p, B, None, None, None, "ck")
+    assert_spmm_close(got, want, spmm_bound(d, i, p, B, "ck"), "3000 rows, N=4104")
 
 
 @pytest.mark.gpu

@@ -709,21 +709,31 @@ __global__ __launch_bounds__(256) void csr_decode_kernel(CsrDecode d) {
 }
 
 // out[g][n] = round(sum over the row's entries p, in order, of a_p * B[k_p][n])
-// (+ addend[g][n], rounded again, when given).  One wave per (row, chunk of
-// 64*V columns: 1 KiB of a B row), consecutive waves on consecutive chunks of
-// a row; entries are read four at a time.  Each entry reads its piece of a B
-// row from L2 / MALL: nnz * N * sizeof(B) bytes gathered in all.
+// (+ addend[g][n], rounded again, when given).  One wave per (row, slice of
+// 64*V columns: 1 KiB of a B row); entries are read eight at a time.  Each
+// entry reads its piece of a B row from L2 / MALL: nnz * N * sizeof(B) bytes
+// gathered in all, so the items are ordered for the L2s: taken slice by
+// slice (all rows of a column slice, then the next slice), the sequence is
+// cut into kXcds equal runs, and run x goes to the workgroups x, x + kXcds,
+// ..., which the dispatcher places on XCD x (workgroups go to the XCDs in
+// turn).  Each XCD then gathers from one or two B slices at a time instead of
+// from all of B (11 MB of B rows per XCD at O3 instead of 90 MB).  The grid is
+// a multiple of kXcds; where the workgroups land affects speed only.
+constexpr int kXcds = 8;
+
 template <int DT, int V>
 __global__ __launch_bounds__(256) void spmm_csr_kernel(SpmmArgs a) {
   using S = typename FT<DT>::S;
   constexpr int U = 8;
   const int lane = threadIdx.x & 63;
   const int64_t nch = (a.N + 64 * V - 1) / (64 * V);
-  const int64_t items = a.nb * a.rows * nch;
+  const int64_t nrow = a.nb * a.rows, items = nrow * nch;
   const S* B = (const S*)a.B;
-  const int64_t nw = (int64_t)gridDim.x * 4;
-  for (int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); w < items; w += nw) {
-    const int64_t g = w / nch, ch = w - g * nch;
+  const int xcd = blockIdx.x % kXcds;
+  const int64_t lo = items * xcd / kXcds, hi = items * (xcd + 1) / kXcds;
+  const int64_t nwx = (int64_t)(gridDim.x / kXcds) * 4;
+  for (int64_t w = lo + (int64_t)(blockIdx.x / kXcds) * 4 + (threadIdx.x >> 6); w < hi; w += nwx) {
+    const int64_t ch = w / nrow, g = w - ch * nrow;
     const int64_t n = ch * 64 * V + (int64_t)lane * V;
     const bool nok = n < a.N;
     const int64_t nn = nok ? n : a.N - V;
@@ -912,10 +922,19 @@ int launch_spmm(const SpmmArgs& a, hipStream_t st) {
                     (!a.addend || aligned(a.addend, 16));
   const int v = wide ? V : 1;
   const int64_t items = a.nb * a.rows * ((a.N + 64 * v - 1) / (64 * v));
+  // resident workgroups only (the slice order relies on them running
+  // together), a multiple of kXcds, no more than the items need
+  auto grid_of = [&](const void* k) {
+    const int64_t need = ((items + 3) / 4 + kXcds - 1) / kXcds * kXcds;
+    const int64_t res = (int64_t)persistent_grid(k, 256, 0, items * 64) / kXcds * kXcds;
+    return (unsigned)std::max<int64_t>(kXcds, std::min(need, res));
+  };
   if (wide)
-    hipLaunchKernelGGL((spmm_csr_kernel<DT, V>), dim3(grid_for(items, 4, 16)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((spmm_csr_kernel<DT, V>), dim3(grid_of((const void*)spmm_csr_kernel<DT, V>)), dim3(256), 0,
+                       st, a);
   else
-    hipLaunchKernelGGL((spmm_csr_kernel<DT, 1>), dim3(grid_for(items, 4, 16)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((spmm_csr_kernel<DT, 1>), dim3(grid_of((const void*)spmm_csr_kernel<DT, 1>)), dim3(256), 0,
+                       st, a);
   return check_launch("spmm_csr");
 }
 
