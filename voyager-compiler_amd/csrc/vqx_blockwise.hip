@@ -450,8 +450,14 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
     }
     if (!live) continue;
     if (c % G == 0) {
-      if (scale_out) BT<T>::put(scale_out + c / G, BT<T>::round_bits(sf));
-      if (zp_out) BT<T>::put(zp_out + c / G, BT<T>::round_bits(zp));
+      // write-once outputs: non-temporal stores (42.0-42.5 against
+      // 42.9-43.6 us at F3 with plain stores; non-temporal loads were slower)
+      auto put_nt = [](T* p, uint32_t b) {
+        if constexpr (sizeof(T) == 2) __builtin_nontemporal_store((uint16_t)b, p);
+        else __builtin_nontemporal_store(u2f(b), p);
+      };
+      if (scale_out) put_nt(scale_out + c / G, BT<T>::round_bits(sf));
+      if (zp_out) put_nt(zp_out + c / G, BT<T>::round_bits(zp));
     }
     // x / sf, rounded to the element type.  bf16: x and sf are both bf16
     // values, so x * rcp(sf) rounds to bf16 exactly as the IEEE quotient does
@@ -496,7 +502,7 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
         p = pack_bf16x2(a, b);
         w[i / 2] = pack_bf16x2(u2f(p << 16) * sf, u2f(p & 0xFFFF0000u) * sf);
       }
-      if constexpr (sizeof(T) == 2) *reinterpret_cast<u32x4*>(y + c * 8) = w;
+      if constexpr (sizeof(T) == 2) st_nt(reinterpret_cast<u32x4*>(y + c * 8), w);
       continue;
     }
     if constexpr (sizeof(T) == 2) {
@@ -538,7 +544,7 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         w[i] = (uint32_t)BT<T>::round_bits(o[2 * i]) | ((uint32_t)BT<T>::round_bits(o[2 * i + 1]) << 16);
-      *reinterpret_cast<u32x4*>(y + c * 8) = w;
+      st_nt(reinterpret_cast<u32x4*>(y + c * 8), w);
     } else {
       *reinterpret_cast<float4*>(y + c * 8) = float4{o[0], o[1], o[2], o[3]};
       *reinterpret_cast<float4*>(y + c * 8 + 4) = float4{o[4], o[5], o[6], o[7]};
