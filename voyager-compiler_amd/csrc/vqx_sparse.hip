@@ -800,7 +800,9 @@ __global__ __launch_bounds__(256) void spmm_csr_kernel(SpmmArgs a) {
 #pragma unroll
           for (int j = 0; j < V; ++j) o[j] = FT<DT>::bits(acc[j]);
         }
-        store_group<S, V>((S*)a.out + g * a.N + n, o);
+        // non-temporal: the write-once output does not displace the B
+        // slices the XCD's L2 holds (142.5-143.2 against 144.0-146.7 us)
+        store_group<S, V, true>((S*)a.out + g * a.N + n, o);
       }
     }
   }
