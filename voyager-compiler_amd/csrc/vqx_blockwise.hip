@@ -450,14 +450,10 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
     }
     if (!live) continue;
     if (c % G == 0) {
-      // write-once outputs: non-temporal stores (42.0-42.5 against
-      // 42.9-43.6 us at F3 with plain stores; non-temporal loads were slower)
-      auto put_nt = [](T* p, uint32_t b) {
-        if constexpr (sizeof(T) == 2) __builtin_nontemporal_store((uint16_t)b, p);
-        else __builtin_nontemporal_store(u2f(b), p);
-      };
-      if (scale_out) put_nt(scale_out + c / G, BT<T>::round_bits(sf));
-      if (zp_out) put_nt(zp_out + c / G, BT<T>::round_bits(zp));
+      // plain stores: these scattered 2-byte words merge in L2 (non-temporal
+      // ones took the same time and wrote 3.7 MB more at F3)
+      if (scale_out) BT<T>::put(scale_out + c / G, BT<T>::round_bits(sf));
+      if (zp_out) BT<T>::put(zp_out + c / G, BT<T>::round_bits(zp));
     }
     // x / sf, rounded to the element type.  bf16: x and sf are both bf16
     // values, so x * rcp(sf) rounds to bf16 exactly as the IEEE quotient does
@@ -502,6 +498,8 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
         p = pack_bf16x2(a, b);
         w[i / 2] = pack_bf16x2(u2f(p << 16) * sf, u2f(p & 0xFFFF0000u) * sf);
       }
+      // the output non-temporally (42.0-42.5 against 42.9-43.6 us at F3
+      // with plain stores; non-temporal loads as well were slower)
       if constexpr (sizeof(T) == 2) st_nt(reinterpret_cast<u32x4*>(y + c * 8), w);
       continue;
     }
