@@ -1060,6 +1060,8 @@ __device__ __forceinline__ float load_scale(const void* s, int kind, int64_t i) 
 // and store instruction of the wave covers one contiguous span; each chunk
 // lies inside one block (block sizes are multiples of 16).  6-bit codes and
 // any elements past the last whole 1024 take 16-element groups per thread.
+// The codes are read with plain loads (non-temporal ones made the C2 decode
+// 22.5 us against 16.9), the output is stored non-temporally.
 template <typename T, int CB>
 __device__ __forceinline__ void decode_chunks(const uint8_t* __restrict__ codes, const void* scale, int scale_kind,
                                               const uint16_t* tab, T* __restrict__ out, int64_t base, int lane,
@@ -1071,19 +1073,19 @@ __device__ __forceinline__ void decode_chunks(const uint8_t* __restrict__ codes,
     const int64_t e = base + (int64_t)q * 64 * E + (int64_t)lane * E;
     uint32_t c[E];
     if constexpr (CB == 4 && E == 8) {
-      uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(codes + e / 2));
+      uint32_t w = *reinterpret_cast<const uint32_t*>(codes + e / 2);
 #pragma unroll
       for (int j = 0; j < 8; ++j) c[j] = (w >> (4 * j)) & 0xFu;
     } else if constexpr (CB == 4) {  // E == 4
-      uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(codes + e / 2));
+      uint32_t w = *reinterpret_cast<const uint16_t*>(codes + e / 2);
 #pragma unroll
       for (int j = 0; j < 4; ++j) c[j] = (w >> (4 * j)) & 0xFu;
     } else if constexpr (E == 8) {  // CB == 8
-      u32x2 w = ld_nt(reinterpret_cast<const u32x2*>(codes + e));
+      u32x2 w = *reinterpret_cast<const u32x2*>(codes + e);
 #pragma unroll
       for (int j = 0; j < 8; ++j) c[j] = ((j < 4 ? w.x : w.y) >> (8 * (j & 3))) & 0xFFu;
     } else {  // CB == 8, E == 4
-      uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(codes + e));
+      uint32_t w = *reinterpret_cast<const uint32_t*>(codes + e);
 #pragma unroll
       for (int j = 0; j < 4; ++j) c[j] = (w >> (8 * j)) & 0xFFu;
     }
@@ -1130,7 +1132,7 @@ __global__ __launch_bounds__(256) void decode_group_kernel(const uint8_t* __rest
   for (int64_t g = g0 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
     uint32_t c[16];
     if constexpr (CB == 4) {
-      u32x2 w = ld_nt(reinterpret_cast<const u32x2*>(codes + g * 8));
+      u32x2 w = *reinterpret_cast<const u32x2*>(codes + g * 8);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         c[j] = (w.x >> (4 * j)) & 0xFu;
@@ -1138,8 +1140,7 @@ __global__ __launch_bounds__(256) void decode_group_kernel(const uint8_t* __rest
       }
     } else if constexpr (CB == 6) {
       const uint32_t* q = reinterpret_cast<const uint32_t*>(codes + g * 12);
-      uint32_t w0 = __builtin_nontemporal_load(q), w1 = __builtin_nontemporal_load(q + 1),
-               w2 = __builtin_nontemporal_load(q + 2);
+      uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
       uint64_t lo = (uint64_t)w0 | ((uint64_t)w1 << 32);
 #pragma unroll
       for (int j = 0; j < 10; ++j) c[j] = (uint32_t)(lo >> (6 * j)) & 0x3Fu;
@@ -1147,7 +1148,7 @@ __global__ __launch_bounds__(256) void decode_group_kernel(const uint8_t* __rest
 #pragma unroll
       for (int j = 11; j < 16; ++j) c[j] = (w2 >> (6 * j - 64)) & 0x3Fu;
     } else {
-      u32x4 w = ld_nt(reinterpret_cast<const u32x4*>(codes + g * 16));
+      u32x4 w = *reinterpret_cast<const u32x4*>(codes + g * 16);
       uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int j = 0; j < 16; ++j) c[j] = (ww[j >> 2] >> (8 * (j & 3))) & 0xFFu;
