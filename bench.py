@@ -792,16 +792,16 @@ def hbm_ceiling(steps, warmup):
     del a, b
     torch.cuda.empty_cache()
     # the probe library's streaming kernel at fixed read:write mixes, each
-    # stream 512 MiB (16-byte non-temporal accesses, 1 KiB per wave
-    # instruction), with a one-shot grid (a workgroup per 256 units) and with a
-    # persistent grid of 2048 workgroups
+    # stream 512 MiB (16-byte accesses, 1 KiB per wave instruction; stores
+    # non-temporal, loads non-temporal or plain), with a one-shot grid (a
+    # workgroup per 256 units) and with a persistent grid of 2048 workgroups
     import ctypes
 
     probe = ctypes.CDLL(os.path.join(ROOT, "voyager-compiler_amd", "libvqx_probe.so"))
-    fn = probe.vqx_probe_hbm_mix
+    fn = probe.vqx_probe_hbm_mix_loads
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                   ctypes.c_int, ctypes.c_void_p]
+                   ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     units = 1 << 25
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     big = torch.empty(4 * units * 16, dtype=torch.uint8, device="cuda").random_()
@@ -809,8 +809,11 @@ def hbm_ceiling(steps, warmup):
     sink = torch.empty(max(units // 256, 2048) * 256, dtype=torch.int32, device="cuda")
     for r, w in ((1, 0), (0, 1), (1, 1), (2, 1), (4, 1), (1, 2), (1, 4)):
         for grid, how in ((units // 256, "one-shot grid"), (2048, "persistent grid")):
-            args = (big.data_ptr(), out.data_ptr(), units, r, w, sink.data_ptr(), grid, st)
-            run(f"probe read:write {r}:{w} ({how})", lambda: fn(*args), (r + w) * units * 16)
+            for nt, kind in ((1, "non-temporal loads"), (0, "plain loads")):
+                if r == 0 and nt == 0:
+                    continue
+                args = (big.data_ptr(), out.data_ptr(), units, r, w, sink.data_ptr(), grid, nt, st)
+                run(f"probe read:write {r}:{w} ({how}, {kind})", lambda: fn(*args), (r + w) * units * 16)
     del big, out, sink
     torch.cuda.empty_cache()
     vqx = __graft_entry__.load_package()
