@@ -459,9 +459,13 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
     // values, so x * rcp(sf) rounds to bf16 exactly as the IEEE quotient does
     // (an exact quotient of two 8-bit significands lies at least 2^-16.86
     // relative from every bf16 rounding midpoint, hazard H7, far beyond the
-    // few fp32 ulps of v_rcp_f32 and the product), except where the quotient
-    // falls below the normal range (bf16 subnormal midpoints can be hit
-    // exactly) or 1 / sf is not a normal float; those elements take the
+    // few fp32 ulps of v_rcp_f32 and the product).  A quotient below 2^-124
+    // (where bf16 subnormal midpoints can be hit exactly) may round
+    // differently, but the output does not depend on it beyond its sign,
+    // which the product keeps: with |zp| >= 2^-116 the sum with zp rounds to
+    // zp whatever it is; otherwise the sum rounds to an integer zero, and
+    // the output is bf16((0 - zp) * sf), or the sign of that zero when zp is
+    // 0.  Only where 1 / sf is not a normal float do the elements take the
     // IEEE division.
     float qd[8];
     bool slow = true;
@@ -470,10 +474,7 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
       const float rs = __builtin_amdgcn_rcpf(sf);
       slow = se - 1u >= 252u;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        qd[i] = v[i] * rs;
-        slow |= tiny(qd[i]);
-      }
+      for (int i = 0; i < 8; ++i) qd[i] = v[i] * rs;
     }
     if (slow) {
 #pragma unroll
