@@ -150,3 +150,48 @@ def test_codebook_tied_distances_row_all_patterns(vqx):
     x = torch.stack([pats, pats])
     codes = Q.codebook_encode(x.cuda(), cb.cuda())
     assert torch.equal(codes.cpu().long(), R.codebook_encode_rows(x, cb))
+
+
+def deep_codebooks():
+    """Codebooks of the deep search trees (K = 32 .. 256): quantile rows of
+    every deep size, evenly spaced rows whose decision thresholds sit on
+    integers (range 1024), the same all <= 0, a row within one binade,
+    a row with three thresholds within 0.0004 of its range, and a row with
+    a duplicate entry (two equal thresholds)."""
+    rows = []
+    for K in (32, 64, 128, 256):
+        rows.append(c4_codebooks(2, K, seed=K)[:, :].tolist())
+    flat = [r for pair in rows for r in pair]
+    out = [torch.tensor(r) for r in flat]
+    edges = torch.arange(256, dtype=torch.float32) * 4.0
+    edges[-1] = 1024.0                                                  # thresholds 2, 6, ..., 1018, 1020
+    out.append(edges)
+    out.append(edges - 1024.0)                                          # the same, all <= 0
+    out.append(torch.linspace(-3.0, 3.0, 200))
+    out.append(torch.linspace(0.5, 0.75, 100))
+    crowded = c4_codebooks(1, 256, seed=9)[0].clone()
+    w = float(crowded[-1] - crowded[0]) / 1024
+    for i in (1, 2, 3):                                                  # crowded thresholds
+        crowded[99 + i] = crowded[99] + 0.2 * i * w
+    out.append(torch.sort(crowded).values)
+    dup = c4_codebooks(1, 128, seed=10)[0].clone()
+    dup[40] = dup[39]
+    out.append(dup)
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_codebook_deep_trees_all_patterns(vqx, dtype):
+    """Every bf16 bit pattern (NaNs, infinities, subnormals, signed zeros)
+    encoded against the deep-tree codebooks, equal to the brute-force argmin;
+    one call per codebook size."""
+    pats = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    cbs = deep_codebooks()
+    for K in sorted({len(c) for c in cbs}):
+        cb = torch.stack([c for c in cbs if len(c) == K])
+        x = pats.float().expand(cb.shape[0], -1).contiguous()
+        print(f"deep tree K={K} rows={cb.shape[0]} {dtype}", flush=True)
+        codes = Q.codebook_encode(x.to(dtype).cuda(), cb.cuda())
+        want = R.codebook_encode_rows(x, cb)
+        assert torch.equal(codes.cpu().long(), want), K
