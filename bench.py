@@ -7,10 +7,14 @@ input already resident in HBM.  The headline (``value``) is BASELINE.json
 NF4 block-64 encode of a bf16 4096x11008 weight (C2), in
 quantized elements per second over the whole timed region (K back-to-back
 launches between two synchronisations); every other config is reported in
-``configs``.  ``roofline.achieved`` divides the algorithmic bytes of a launch
-by the kernel's average launch duration, from HIP events around each launch
-on the launch stream (the kernels launch on torch's current stream, so
-torch.cuda.Event sees them); ``roofline.traffic`` is the HBM bytes per launch
+``configs``.  A bandwidth-bound config cycles its launches through several
+copies of its buffers, more than twice the 256 MiB MALL together, so every
+launch streams from HBM (the cold figure, which every fraction uses); the
+warm figure (one buffer set, input left in the MALL by the launch before) is
+reported beside it.  ``roofline.achieved`` divides the algorithmic bytes of a
+launch by the kernel's average launch duration, from HIP events around the
+launches on the launch stream (the kernels launch on torch's current stream,
+so torch.cuda.Event sees them); ``roofline.traffic`` is the HBM bytes per launch
 measured by rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/
 hbm_traffic.json).  ``cpu_baseline`` times the CPU oracle (a restatement of
 the reference's PyTorch CPU path) on this host's cores.
@@ -40,10 +44,15 @@ def parse():
     ap.add_argument("--only", default=None, help="comma list of config keys to run")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--no-warm", action="store_true",
+                    help="skip the warm-MALL timing pass (one buffer set re-launched), so that a profiler's "
+                         "average over every launch of a kernel is the cold figure the bench reports")
     ap.add_argument("--hbm-ceiling", action="store_true",
                     help="only measure what HBM sustains on this box for each traffic mix, with 1 GiB working sets "
                          "(beyond the 256 MiB MALL): torch's own copy, fill and read kernels, and the C3 e4m3 "
                          "kernel on a 1 GiB input")
+    ap.add_argument("--build-probe", action="store_true",
+                    help="only compile bench_hbm_probe.hip (the --hbm-ceiling probe) into bench_hbm_probe.so")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device-to-device copy of 512 MiB (5 times), the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -135,8 +144,26 @@ def cpu_c5(torch, Ac, N):
 
 
 # ---------------------------------------------------------------------------
-# configs: setup() -> (launch callable, info)
+# configs: setup() -> (list of launch callables, info)
+#
+# An HBM-bound config builds several sets of its input and output buffers and
+# the timed loop cycles through them, so that the sets together exceed twice
+# the 256 MiB MALL (MI355X's last-level cache) and no launch finds its input
+# still cached from the launch before: its time is the time to stream from
+# HBM.  The first set is the one the parity tests check.
 # ---------------------------------------------------------------------------
+ROTATE_BYTES = 640 << 20
+MIN_SETS = 3
+
+
+def rotate(make, set_bytes):
+    """[launch] and [buffers] of n buffer sets, make(i) -> (launch, buffers),
+    n = the sets whose bytes reach ROTATE_BYTES, at least MIN_SETS."""
+    n = max(MIN_SETS, -(-ROTATE_BYTES // max(int(set_bytes), 1)))
+    made = [make(i) for i in range(n)]
+    return [m[0] for m in made], [m[1] for m in made]
+
+
 def cpu_f3(torch, xc):
     def run():
         from oracle import reference_ops as R
@@ -151,36 +178,47 @@ def setup_f3(vqx, torch, L):
     """Group-wise affine fake-quant (uint2, blocks of 64 along the last
     axis, as for a KV cache) of C2's bf16 input."""
     xc = c2_input(torch)
-    x = xc.cuda()
-    rows, cols = x.shape
-    y = torch.empty_like(x)
-    sc = torch.empty(rows, cols // 64, dtype=x.dtype, device="cuda")
-    zp = torch.empty_like(sc)
-    args = (L.ptr(x), L.BF16, rows, cols, 1, 64, 0.0, 3.0, None, L.ptr(sc), L.ptr(zp), L.ptr(y), L.stream_of(x))
+    rows, cols = xc.shape
+    n = xc.numel()
     fn = L.load().vqx_gwa_fake_quant
-    n = x.numel()
-    return (lambda: fn(*args)), dict(
+
+    def make(i):
+        x = xc.cuda()
+        y = torch.empty_like(x)
+        sc = torch.empty(rows, cols // 64, dtype=x.dtype, device="cuda")
+        zp = torch.empty_like(sc)
+        args = (L.ptr(x), L.BF16, rows, cols, 1, 64, 0.0, 3.0, None, L.ptr(sc), L.ptr(zp), L.ptr(y),
+                L.stream_of(x))
+        return (lambda: fn(*args)), (x, y, sc, zp)
+
+    algo = 4 * n + 2 * 2 * (n // 64)
+    launches, bufs = rotate(make, algo)
+    return launches, dict(
         name="F3 group-wise affine fake-quant, uint2 (0..3), blocks of 64 along the last axis: bf16 [4096,11008] "
              "-> bf16 values + bf16 scale and zero point per block",
-        elements=n, bytes=4 * n + 2 * 2 * (n // 64), bound="hbm", dtype="bf16", keep=(x, y, sc, zp),
-        cpu=cpu_f3(torch, xc))
+        elements=n, bytes=algo, bound="hbm", dtype="bf16", keep=bufs, cpu=cpu_f3(torch, xc))
 
 
 def setup_c1(vqx, torch, L):
     torch.manual_seed(0)
     xc = torch.randn(4096, 4096, dtype=torch.float32)
-    x = xc.cuda()
-    y = torch.empty_like(x)
-    codes = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
-    desc = vqx.parse_format("posit8_1").desc(x.device)
-    st = L.stream_of(x)
-    args = (L.ptr(x), L.F32, x.numel(), L.ctypes.byref(desc), None, 1, 1, 1, L.ptr(y), L.ptr(codes), 1, st)
+    n = xc.numel()
+    desc = vqx.parse_format("posit8_1").desc(torch.device("cuda"))
     fn = L.load().vqx_fake_quant
-    n = x.numel()
-    return (lambda: fn(*args)), dict(
+
+    def make(i):
+        x = xc.cuda()
+        y = torch.empty_like(x)
+        codes = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
+        args = (L.ptr(x), L.F32, n, L.ctypes.byref(desc), None, 1, 1, 1, L.ptr(y), L.ptr(codes), 1,
+                L.stream_of(x))
+        return (lambda: fn(*args)), (x, y, codes)
+
+    launches, bufs = rotate(make, 9 * n)
+    return launches, dict(
         name="C1 posit8_1 fake-quant + uint8 codes, fp32 4096x4096 N(0,1) seed 0",
         elements=n, bytes=9 * n, bound="hbm", dtype="f32->u8", cpu=cpu_c1(torch, xc),
-        check=dict(x=xc, out=y, codes=codes), keep=(x,))
+        check=dict(x=xc, out=bufs[0][1], codes=bufs[0][2]), keep=(bufs, desc))
 
 
 def c2_input(torch, rows=4096, cols=11008, seed=1):
@@ -195,32 +233,40 @@ def c2_input(torch, rows=4096, cols=11008, seed=1):
 
 def setup_c2(vqx, torch, L, decode=False):
     xc = c2_input(torch)
-    x = xc.cuda()
-    n = x.numel()
+    n = xc.numel()
     fmt = vqx.parse_format("nf4")
-    desc = fmt.desc(x.device)
-    codes = torch.empty(n // 2, dtype=torch.uint8, device="cuda")
-    scale = torch.empty(4096, 11008 // 64, dtype=torch.float32, device="cuda")
-    st = L.stream_of(x)
+    desc = fmt.desc(torch.device("cuda"))
+    dtab = fmt.tables(torch.device("cuda"))["decode"]
     enc = L.load().vqx_mx_quantize
-    eargs = (L.ptr(x), L.BF16, 4096, 11008, 1, 64, L.ctypes.byref(desc), 1, 0, L.ctypes.c_float(1.0), None,
-             None, L.ptr(scale), None, None, None, L.ptr(codes), 0, st)
-    algo = n * 2 + n // 2 + scale.numel() * 4
+    dec = L.load().vqx_mx_decode
+    algo = n * 2 + n // 2 + n // 64 * 4
+
+    def make(i):
+        x = xc.cuda()
+        codes = torch.empty(n // 2, dtype=torch.uint8, device="cuda")
+        scale = torch.empty(4096, 11008 // 64, dtype=torch.float32, device="cuda")
+        st = L.stream_of(x)
+        eargs = (L.ptr(x), L.BF16, 4096, 11008, 1, 64, L.ctypes.byref(desc), 1, 0, L.ctypes.c_float(1.0), None,
+                 None, L.ptr(scale), None, None, None, L.ptr(codes), 0, st)
+        if not decode:
+            return (lambda: enc(*eargs)), (x, codes, scale)
+        enc(*eargs)
+        del x
+        out = torch.empty(4096, 11008, dtype=torch.bfloat16, device="cuda")
+        dargs = (L.ptr(codes), 4, L.ptr(dtab), dtab.numel(), L.ptr(scale), 0, n, 64, L.ptr(out), L.BF16, st)
+        return (lambda: dec(*dargs)), (None, codes, scale, out)
+
+    launches, bufs = rotate(make, algo)
     if not decode:
-        return (lambda: enc(*eargs)), dict(
+        return launches, dict(
             name="C2 NF4 block-64 absmax encode, bf16 4096x11008 N(0,0.02)+0.1% outliers seed 1 "
                  "-> packed 4-bit codes + fp32 scales",
             elements=n, bytes=algo, bound="hbm", dtype="bf16->u4", cpu_input=xc,
-            check=dict(x=xc, codes=codes, scale=scale), keep=(x,))
-    enc(*eargs)
-    out = torch.empty_like(x)
-    dtab = fmt.tables(x.device)["decode"]
-    dec = L.load().vqx_mx_decode
-    dargs = (L.ptr(codes), 4, L.ptr(dtab), dtab.numel(), L.ptr(scale), 0, n, 64, L.ptr(out), L.BF16, st)
-    return (lambda: dec(*dargs)), dict(
+            check=dict(x=xc, codes=bufs[0][1], scale=bufs[0][2]), keep=(bufs, desc))
+    return launches, dict(
         name="C2 NF4 block-64 decode: packed codes + fp32 scales -> bf16 4096x11008",
         elements=n, bytes=algo, bound="hbm", dtype="u4->bf16", cpu=cpu_c2_decode(torch, xc),
-        check=dict(x=xc, codes=codes, scale=scale, out=out), keep=(x, dtab))
+        check=dict(x=xc, codes=bufs[0][1], scale=bufs[0][2], out=bufs[0][3]), keep=(bufs, dtab, desc))
 
 
 def c3_input(torch, rows=8192, cols=8192, seed=2):
@@ -234,36 +280,53 @@ def c3_input(torch, rows=8192, cols=8192, seed=2):
 _C3_X = {}
 
 
-def setup_c3(vqx, torch, L, dtype, qmax, fake=False):
-    if "x" not in _C3_X:
+def _c3_inputs(torch, nsets):
+    """C3's bf16 input on the device, nsets copies (kept across the C3
+    configs, which all read it)."""
+    if "xc" not in _C3_X:
         _C3_X["xc"] = c3_input(torch)
-        _C3_X["x"] = _C3_X["xc"].cuda()
-    x = _C3_X["x"]
-    cpu = cpu_c3(torch, _C3_X["xc"], dtype, qmax, fake)
-    n = x.numel()
+        _C3_X["x"] = []
+    while len(_C3_X["x"]) < nsets:
+        _C3_X["x"].append(_C3_X["xc"].cuda())
+    return _C3_X["x"]
+
+
+def setup_c3(vqx, torch, L, dtype, qmax, fake=False):
+    n = 8192 * 8192
     fmt = vqx.parse_format(dtype)
-    desc = fmt.desc(x.device)
-    st = L.stream_of(x)
+    desc = fmt.desc(torch.device("cuda"))
     shift = math.floor(math.log2(qmax))
     fn = L.load().vqx_mx_quantize
-    if fake:
-        y = torch.empty_like(x)
-        sc = torch.empty(8192, 256, dtype=torch.bfloat16, device="cuda")
-        args = (L.ptr(x), L.BF16, 8192, 8192, 1, 32, L.ctypes.byref(desc), 0, shift, L.ctypes.c_float(qmax),
-                None, L.ptr(sc), None, None, None, L.ptr(y), None, 1, st)
-        return (lambda: fn(*args)), dict(
-            name=f"C3 MX block-32 {dtype} fake-quant (bf16 values + bf16 scales), bf16 8192x8192 Laplace seed 2",
-            elements=n, bytes=n * 4 + sc.numel() * 2, bound="hbm", dtype="bf16", cpu=cpu,
-            check=dict(x=_C3_X["xc"], out=y, scale=sc))
     cb = fmt.code_bits
-    codes = torch.empty(n * cb // 8, dtype=torch.uint8, device="cuda")
-    e8 = torch.empty(8192, 256, dtype=torch.uint8, device="cuda")
-    args = (L.ptr(x), L.BF16, 8192, 8192, 1, 32, L.ctypes.byref(desc), 0, shift, L.ctypes.c_float(qmax),
-            None, None, None, L.ptr(e8), None, None, L.ptr(codes), 0, st)
-    return (lambda: fn(*args)), dict(
+    algo = n * 4 + n // 32 * 2 if fake else n * 2 + n * cb // 8 + n // 32
+    xs = _c3_inputs(torch, max(MIN_SETS, -(-ROTATE_BYTES // algo)))
+    cpu = cpu_c3(torch, _C3_X["xc"], dtype, qmax, fake)
+
+    def make(i):
+        x = xs[i]
+        st = L.stream_of(x)
+        if fake:
+            y = torch.empty_like(x)
+            sc = torch.empty(8192, 256, dtype=torch.bfloat16, device="cuda")
+            args = (L.ptr(x), L.BF16, 8192, 8192, 1, 32, L.ctypes.byref(desc), 0, shift, L.ctypes.c_float(qmax),
+                    None, L.ptr(sc), None, None, None, L.ptr(y), None, 1, st)
+            return (lambda: fn(*args)), (y, sc)
+        codes = torch.empty(n * cb // 8, dtype=torch.uint8, device="cuda")
+        e8 = torch.empty(8192, 256, dtype=torch.uint8, device="cuda")
+        args = (L.ptr(x), L.BF16, 8192, 8192, 1, 32, L.ctypes.byref(desc), 0, shift, L.ctypes.c_float(qmax),
+                None, None, None, L.ptr(e8), None, None, L.ptr(codes), 0, st)
+        return (lambda: fn(*args)), (codes, e8)
+
+    launches, bufs = rotate(make, algo)
+    if fake:
+        return launches, dict(
+            name=f"C3 MX block-32 {dtype} fake-quant (bf16 values + bf16 scales), bf16 8192x8192 Laplace seed 2",
+            elements=n, bytes=algo, bound="hbm", dtype="bf16", cpu=cpu,
+            check=dict(x=_C3_X["xc"], out=bufs[0][0], scale=bufs[0][1]), keep=(bufs, desc))
+    return launches, dict(
         name=f"C3 MX block-32 {dtype} + E8M0 scales, bf16 8192x8192 Laplace x 10^U(-1,1) seed 2 -> packed codes",
-        elements=n, bytes=n * 2 + n * cb // 8 + e8.numel(), bound="hbm", dtype=f"bf16->{dtype}", cpu=cpu,
-        check=dict(x=_C3_X["xc"], codes=codes, scale=e8))
+        elements=n, bytes=algo, bound="hbm", dtype=f"bf16->{dtype}", cpu=cpu,
+        check=dict(x=_C3_X["xc"], codes=bufs[0][0], scale=bufs[0][1]), keep=(bufs, desc))
 
 
 def c4_codebooks(torch, rows, K, seed=3):
@@ -280,28 +343,36 @@ def c4_codebooks(torch, rows, K, seed=3):
 def setup_c4(vqx, torch, L, K, decode=False):
     g = torch.Generator().manual_seed(3)
     xc = torch.randn(4096, 4096, generator=g)
-    x = xc.cuda()
     cbc = c4_codebooks(torch, 4096, K)
-    cb = cbc.cuda()
-    codes = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
-    st = L.stream_of(x)
-    n = x.numel()
-    algo = 5 * n + cb.numel() * 4
+    n = xc.numel()
+    algo = 5 * n + cbc.numel() * 4
     enc = L.load().vqx_codebook_encode
-    eargs = (L.ptr(x), L.F32, 4096, 4096, L.ptr(cb), K, L.ptr(codes), st)
+    dec = L.load().vqx_codebook_decode
+
+    def make(i):
+        x = xc.cuda()
+        cb = cbc.cuda()
+        codes = torch.empty(x.shape, dtype=torch.uint8, device="cuda")
+        st = L.stream_of(x)
+        eargs = (L.ptr(x), L.F32, 4096, 4096, L.ptr(cb), K, L.ptr(codes), st)
+        if not decode:
+            return (lambda: enc(*eargs)), (x, cb, codes)
+        enc(*eargs)
+        del x
+        out = torch.empty(4096, 4096, dtype=torch.float32, device="cuda")
+        dargs = (L.ptr(codes), 4096, 4096, L.ptr(cb), K, L.ptr(out), L.F32, st)
+        return (lambda: dec(*dargs)), (None, cb, codes, out)
+
+    launches, bufs = rotate(make, algo)
     if not decode:
-        return (lambda: enc(*eargs)), dict(
+        return launches, dict(
             name=f"C4 per-channel codebook encode K={K}, fp32 4096x4096 N(0,1) seed 3 -> uint8 indices",
             elements=n, bytes=algo, bound="hbm", dtype="f32->u8", cpu=cpu_c4(torch, xc, cbc, False),
-            check=dict(x=xc, codebooks=cbc, codes=codes), keep=(x, cb))
-    enc(*eargs)
-    out = torch.empty_like(x)
-    dec = L.load().vqx_codebook_decode
-    dargs = (L.ptr(codes), 4096, 4096, L.ptr(cb), K, L.ptr(out), L.F32, st)
-    return (lambda: dec(*dargs)), dict(
+            check=dict(x=xc, codebooks=cbc, codes=bufs[0][2]), keep=bufs)
+    return launches, dict(
         name=f"C4 per-channel codebook decode K={K}: uint8 indices -> fp32 4096x4096",
         elements=n, bytes=algo, bound="hbm", dtype="u8->f32", cpu=cpu_c4(torch, xc, cbc, True),
-        check=dict(x=xc, codebooks=cbc, codes=codes, out=out), keep=(x, cb))
+        check=dict(x=xc, codebooks=cbc, codes=bufs[0][2], out=bufs[0][3]), keep=bufs)
 
 
 def setup_c5(vqx, torch, L, whole_tiles=False, M=2048):
@@ -332,7 +403,7 @@ def setup_c5(vqx, torch, L, whole_tiles=False, M=2048):
         else:
             how, launches = "whole 256x128 tiles (the last round is too full for a K split to pay)", 1
         keep = (A, codes, sc, lv, out, ws)
-    return (lambda: fn(*args)), dict(
+    return [lambda: fn(*args)], dict(
         name=f"C5 NF4-dequant linear: A bf16 [{M},4096] x W NF4 block-64 [11008,4096]^T -> bf16, fp32 accumulate; "
              + how,
         elements=M * N, flops=2 * M * N * K, bytes=M * K * 2 + N * K // 2 + N * K // 64 * 4 + M * N * 2,
@@ -361,7 +432,7 @@ def setup_c5_linear_mx(vqx, torch, L, M=2048):
         return 0
 
     launch()  # packs the weight once
-    return launch, dict(
+    return [launch], dict(
         name=f"C5 via quantized_ops::linear_mx on convert-format operands: A bf16 [{M},4096], weight = bf16 NF4 "
              f"indices [11008,4096] + weight_code (16 bf16 levels) + bf16 weight_scale [11008,64], block 64 -> bf16; "
              f"the fused dequant MFMA kernel (weight packed once, cached)",
@@ -385,7 +456,7 @@ def setup_c5_skinny(vqx, torch, L, M, N=11008):
     out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
     fn = L.load().vqx_nf4_linear
     args = (L.ptr(A), L.ptr(codes), L.ptr(sc), L.ptr(lv), None, L.ptr(out), M, N, K, L.stream_of(A))
-    return (lambda: fn(*args)), dict(
+    return [lambda: fn(*args)], dict(
         name=f"C5 skinny NF4-dequant linear: A bf16 [{M},4096] x W NF4 block-64 [{N},4096]^T -> bf16",
         elements=M * N, bytes=N * K // 2 + N * K // 64 * 4 + M * K * 2 + M * N * 2, flops=2 * M * N * K,
         bound="hbm", dtype="bf16", keep=(A, codes, sc, lv, out), cpu=cpu_c5(torch, Ac, N))
@@ -406,7 +477,7 @@ def setup_c5_dense_library(vqx, torch, L, N=11008, M=2048):
         F.linear(A, W)
         return 0
 
-    return launch, dict(
+    return [launch], dict(
         name=f"comparison: dense bf16 A [{M},4096] x W [{N},4096]^T through torch F.linear (hipBLASLt), the GEMM "
              f"the reference's linear_mx runs after its decode (decode not counted)",
         elements=M * N, flops=2 * M * N * K, bytes=M * K * 2 + N * K * 2 + M * N * 2, bound="mfma", dtype="bf16",
@@ -419,17 +490,25 @@ def setup_l1(vqx, torch, L):
     histogram of Histogram.add, unit weights."""
     g = torch.Generator().manual_seed(9)
     xc = torch.randn(4096, 4096, generator=g)
-    x = xc.cuda()
+    n = xc.numel()
     h = vqx.quantization.Histogram(-7.0, 7.0, 4001)
-    edges = h._prepare(x.device)
+    edges = h._prepare(torch.device("cuda"))
     fn = L.load().vqx_lcq_histogram
-    args = (L.ptr(x), L.F32, x.numel(), 64, L.ctypes.c_float(7.0), None, 1, L.ptr(edges), 4001, L.ptr(h.weight),
-            L.ptr(h.total), L.ptr(h.square), L.stream_of(x))
-    return (lambda: fn(*args)), dict(
+
+    def make(i):
+        # every set adds into the one histogram (its 96 KB of bins stay
+        # cached either way); the inputs rotate
+        x = xc.cuda()
+        args = (L.ptr(x), L.F32, n, 64, L.ctypes.c_float(7.0), None, 1, L.ptr(edges), 4001, L.ptr(h.weight),
+                L.ptr(h.total), L.ptr(h.square), L.stream_of(x))
+        return (lambda: fn(*args)), x
+
+    algo = n * 4 + 3 * 4001 * 8
+    launches, bufs = rotate(make, algo)
+    return launches, dict(
         name="L1 LCQ calibration histogram: unit_scale (blocks of 64, quant_max 7) + 4001-bin fp64 moments of a "
              "fp32 4096x4096 N(0,1) seed 9",
-        elements=x.numel(), bytes=x.numel() * 4 + 3 * 4001 * 8, bound="hbm", dtype="f32->f64",
-        cpu_input=xc, keep=(h, edges))
+        elements=n, bytes=algo, bound="hbm", dtype="f32->f64", cpu_input=xc, keep=(h, edges, bufs))
 
 
 def setup_g1(vqx, torch, L):
@@ -463,7 +542,7 @@ def setup_g1(vqx, torch, L):
         return _timed(lambda: R.gptq_compensate_weight(wc, Hc.clone(), T, q, 7.0, 64, 0.01)), \
             "the oracle's compensate_weight on the full 4096x4096 weight"
 
-    return launch, dict(
+    return [launch], dict(
         name="G1 GPTQ compensate_weight: fp32 4096x4096 weight N(0,0.02) seed 11 onto int4 blocks of 64 "
              "(act_order, damping 0.01), Hessian of 16384 synthetic tokens; one step = the whole compensation "
              "(many launches: the block kernel, Cholesky, trailing GEMMs)",
@@ -497,42 +576,49 @@ def _outlier_csr(torch, L, x):
 
 def setup_o1(vqx, torch, L, mx=False):
     xc = outlier_input(torch)
-    x = xc.cuda()
-    R, C = x.shape
-    n = x.numel()
-    bufs, fargs, max_nnz = _outlier_csr(torch, L, x)
+    R, C = xc.shape
+    n = xc.numel()
+    max_nnz = int(R * C * OUTLIER_PCT)
     # the one-pass entry points: x read once, the outliers staged in a
     # workspace and placed by a second, small launch
     wsz = L.ctypes.c_int64(0)
     L.call("vqx_outlier_workspace_size", L.BF16, 1, R, C, max_nnz, L.ctypes.byref(wsz))
-    ws = torch.empty(max(wsz.value, 1), dtype=torch.uint8, device="cuda")
     filt = L.load().vqx_filter_outlier_ws
-    fargs = fargs[:-1] + (L.ptr(ws), wsz.value, fargs[-1])
-    L.call("vqx_filter_outlier_ws", *fargs)
-    torch.cuda.synchronize()
-    nnz = int(bufs["ptr"][-1])
-    csr_bytes = 6 * max_nnz + 4 * (R + 1)
-    common = dict(elements=n, bound="hbm", dtype="bf16", nnz=nnz,
-                  cpu_input=(xc, OUTLIER_THRESHOLD, OUTLIER_PCT))
-    if not mx:
-        return (lambda: filt(*fargs)), dict(
-            name=f"O1 filter_outlier, bf16 4096x11008 N(0,1) with 0.5% x32 seed 5, |x| > {OUTLIER_THRESHOLD}, "
-                 f"capacity 1% -> CSR ({nnz} outliers) + inliers",
-            bytes=4 * n + csr_bytes, keep=(ws, x, bufs), **common)
-    # the one-pass form: the split writes the quantized inliers and their
-    # block scales instead of the inliers
-    table = vqx.get_quantization_map("fp8_e4m3", "cuda")
-    sc = torch.empty(R, C // 32, dtype=torch.bfloat16, device="cuda")
-    qv = torch.empty_like(x)
     fused = L.load().vqx_quantize_mx_outlier_ws
-    margs = (L.ptr(x), 1, R, C, L.ctypes.c_float(OUTLIER_THRESHOLD), max_nnz, 0, 32, 0, 8, L.ctypes.c_float(448.0),
-             None, L.ptr(table), L.ptr(bufs["data"]), L.ptr(bufs["idx"]), L.ptr(bufs["ptr"]), L.ptr(sc), L.ptr(qv),
-             L.ptr(ws), wsz.value, L.stream_of(x))
-    L.call("vqx_quantize_mx_outlier_ws", *margs)
-    return (lambda: fused(*margs)), dict(
+    table = vqx.get_quantization_map("fp8_e4m3", "cuda")
+    csr_bytes = 6 * max_nnz + 4 * (R + 1)
+    algo = 4 * n + n // 32 * 2 + csr_bytes if mx else 4 * n + csr_bytes
+
+    def make(i):
+        x = xc.cuda()
+        bufs, fargs, _ = _outlier_csr(torch, L, x)
+        ws = torch.empty(max(wsz.value, 1), dtype=torch.uint8, device="cuda")
+        fargs = fargs[:-1] + (L.ptr(ws), wsz.value, fargs[-1])
+        if not mx:
+            L.call("vqx_filter_outlier_ws", *fargs)
+            return (lambda: filt(*fargs)), (x, bufs, ws)
+        # the one-pass form: the split writes the quantized inliers and their
+        # block scales instead of the inliers
+        sc = torch.empty(R, C // 32, dtype=torch.bfloat16, device="cuda")
+        qv = torch.empty_like(x)
+        margs = (L.ptr(x), 1, R, C, L.ctypes.c_float(OUTLIER_THRESHOLD), max_nnz, 0, 32, 0, 8,
+                 L.ctypes.c_float(448.0), None, L.ptr(table), L.ptr(bufs["data"]), L.ptr(bufs["idx"]),
+                 L.ptr(bufs["ptr"]), L.ptr(sc), L.ptr(qv), L.ptr(ws), wsz.value, L.stream_of(x))
+        L.call("vqx_quantize_mx_outlier_ws", *margs)
+        return (lambda: fused(*margs)), (x, bufs, ws, sc, qv)
+
+    launches, sets = rotate(make, algo)
+    torch.cuda.synchronize()
+    nnz = int(sets[0][1]["ptr"][-1])
+    common = dict(elements=n, bound="hbm", dtype="bf16", nnz=nnz, bytes=algo,
+                  cpu_input=(xc, OUTLIER_THRESHOLD, OUTLIER_PCT), keep=(sets, table))
+    if not mx:
+        return launches, dict(
+            name=f"O1 filter_outlier, bf16 4096x11008 N(0,1) with 0.5% x32 seed 5, |x| > {OUTLIER_THRESHOLD}, "
+                 f"capacity 1% -> CSR ({nnz} outliers) + inliers", **common)
+    return launches, dict(
         name=f"O2 quantize_mx_outlier: O1's CSR and, in the same split pass, MX block-32 fp8_e4m3 power-of-two "
-             f"scales and quantized values of the inliers -> CSR + bf16 scales + bf16 quantized inliers",
-        bytes=4 * n + n // 32 * 2 + csr_bytes, keep=(table, sc, qv, ws, x, bufs), **common)
+             f"scales and quantized values of the inliers -> CSR + bf16 scales + bf16 quantized inliers", **common)
 
 
 def setup_o3(vqx, torch, L):
@@ -546,17 +632,24 @@ def setup_o3(vqx, torch, L):
     del x
     g = torch.Generator().manual_seed(6)
     Bc = (0.02 * torch.randn(K, N, generator=g)).to(torch.bfloat16)
-    B = Bc.cuda()
-    out = torch.empty(R, N, dtype=torch.bfloat16, device="cuda")
     fn = L.load().vqx_spmm_csr
-    args = (L.ptr(bufs["data"]), L.BF16, L.ptr(bufs["idx"]), L.ptr(bufs["ptr"]), 1, R, max_nnz, L.ptr(B), L.BF16,
-            0, K, N, None, L.ptr(out), L.stream_of(B))
+    algo = nnz * 6 + 4 * (R + 1) + K * N * 2 + R * N * 2
+
+    def make(i):
+        # the CSR (a few MB) is shared; B and the output rotate
+        B = Bc.cuda()
+        out = torch.empty(R, N, dtype=torch.bfloat16, device="cuda")
+        args = (L.ptr(bufs["data"]), L.BF16, L.ptr(bufs["idx"]), L.ptr(bufs["ptr"]), 1, R, max_nnz, L.ptr(B),
+                L.BF16, 0, K, N, None, L.ptr(out), L.stream_of(B))
+        return (lambda: fn(*args)), (B, out)
+
+    launches, sets = rotate(make, algo)
     cpu = (bufs["data"].cpu(), bufs["idx"].cpu(), bufs["ptr"].cpu(), Bc)
-    return (lambda: fn(*args)), dict(
+    return launches, dict(
         name=f"O3 spmm_csr: O1's CSR [4096 x 11008] ({nnz} entries) x bf16 [11008, 4096] ('ck') -> bf16, "
              f"fp32 accumulate",
-        elements=R * N, bytes=nnz * 6 + 4 * (R + 1) + K * N * 2 + R * N * 2, gathered_bytes=nnz * N * 2,
-        flops=2 * nnz * N, bound="hbm", dtype="bf16", nnz=nnz, cpu_input=cpu, keep=(bufs, B, out))
+        elements=R * N, bytes=algo, gathered_bytes=nnz * N * 2,
+        flops=2 * nnz * N, bound="hbm", dtype="bf16", nnz=nnz, cpu_input=cpu, keep=(bufs, sets))
 
 
 CONFIGS = {
@@ -586,30 +679,42 @@ CONFIGS = {
 HEADLINE = "c2"
 
 
-def time_config(torch, launch, steps, warmup):
-    """Warm up, then time (1) the whole region of `steps` back-to-back launches
-    between two HIP events on the launch stream.  Each step is one C-ABI call
-    that launches one kernel, so region / steps is that kernel's average
-    duration (plus the back-to-back launch gap), and it is what every figure
-    below uses.  (2) A second pass times each launch between its own pair of
-    events, queued behind a GPU spin so that the host has enqueued every pair
-    before the GPU reaches it (otherwise the pair also spans the host's launch
-    latency); its median is reported alongside."""
-    for _ in range(warmup):
-        rc = launch()
-        if rc != 0:
-            raise RuntimeError(f"launch failed: {rc}")
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    w0 = time.perf_counter()
-    t0.record()
-    for _ in range(steps):
-        launch()
-    t1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - w0
-    region_ms = t0.elapsed_time(t1)
+def _check_rc(rc):
+    if rc != 0:
+        raise RuntimeError(f"launch failed: {rc}")
+
+
+def time_config(torch, launches, steps, warmup, warm=True):
+    """Time a config's launches, each step one C-ABI call that launches one
+    kernel, cycling through the config's buffer sets (launches[i % n]):
+
+    (1) the whole region of `steps` back-to-back launches between two HIP
+        events on the launch stream, after `warmup` untimed ones; region /
+        steps is the kernel's average duration (plus the back-to-back launch
+        gap), and every figure the bench reports uses it.  With n > 1 sets
+        the inputs come from HBM (cold MALL).
+    (2) each launch between its own pair of events, queued behind a GPU spin
+        so that the host has enqueued every pair before the GPU reaches it
+        (otherwise a pair also spans the host's launch latency); the median.
+    (3) with `warm` and n > 1: (1) again on the first set only, so that every
+        launch after the first finds its input in the MALL (the warm time)."""
+    n = len(launches)
+
+    def region(seq):
+        for i in range(warmup):
+            _check_rc(seq(i)())
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        t0.record()
+        for i in range(steps):
+            seq(i)()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1), time.perf_counter() - w0
+
+    region_ms, wall = region(lambda i: launches[i % n])
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     try:
@@ -618,12 +723,16 @@ def time_config(torch, launch, steps, warmup):
         pass
     for i in range(steps):
         starts[i].record()
-        launch()
+        launches[i % n]()
         ends[i].record()
     torch.cuda.synchronize()
     per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return {"kernel_ms_avg": region_ms / steps, "kernel_ms_isolated_median": statistics.median(per),
-            "region_ms": region_ms, "wall_s": wall}
+    out = {"kernel_ms_avg": region_ms / steps, "kernel_ms_isolated_median": statistics.median(per),
+           "region_ms": region_ms, "wall_s": wall, "buffer_sets": n}
+    if warm and n > 1:
+        warm_ms, _ = region(lambda i: launches[0])
+        out["kernel_ms_warm"] = warm_ms / steps
+    return out
 
 
 def cpu_baseline_c2(torch, x):
@@ -778,7 +887,7 @@ def hbm_ceiling(steps, warmup):
     res = {}
 
     def run(name, fn, nbytes):
-        tm = time_config(torch, lambda: (fn(), 0)[1], steps, warmup)
+        tm = time_config(torch, [lambda: (fn(), 0)[1]], steps, warmup)
         ms = tm["kernel_ms_avg"]
         res[name] = {"bytes": nbytes, "ms": ms, "GBps": nbytes / (ms * 1e-3) / 1e9,
                      "frac_of_8TBps": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
@@ -797,7 +906,9 @@ def hbm_ceiling(steps, warmup):
     # workgroup per 256 units) and with a persistent grid of 2048 workgroups
     import ctypes
 
-    probe = ctypes.CDLL(os.path.join(ROOT, "voyager-compiler_amd", "libvqx_probe.so"))
+    if not os.path.exists(PROBE_LIB):
+        sys.exit(f"bench.py --hbm-ceiling: {PROBE_LIB} is missing; build it first with python bench.py --build-probe")
+    probe = ctypes.CDLL(PROBE_LIB)
     fn = probe.vqx_probe_hbm_mix_loads
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
@@ -834,6 +945,22 @@ def hbm_ceiling(steps, warmup):
     print(json.dumps({"hbm_ceiling": res, "note": "1 GiB working sets, beyond the 256 MiB MALL"}))
 
 
+PROBE_SRC = os.path.join(ROOT, "bench_hbm_probe.hip")
+PROBE_LIB = os.path.join(ROOT, "bench_hbm_probe.so")
+
+
+def build_probe():
+    """Compile the HBM traffic-mix probe (bench_hbm_probe.hip) for gfx950, on
+    the host, before a GPU run of --hbm-ceiling."""
+    import subprocess
+
+    tmp = PROBE_LIB + ".tmp"
+    subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", PROBE_SRC, "-o", tmp], check=True)
+    os.replace(tmp, PROBE_LIB)
+    print(PROBE_LIB)
+
+
 def calibrate_copy():
     import torch
 
@@ -849,6 +976,9 @@ def calibrate_copy():
 
 def main():
     a = parse()
+    if a.build_probe:
+        build_probe()
+        return
     if a.calibrate_copy:
         calibrate_copy()
         return
@@ -875,8 +1005,8 @@ def main():
     info_head = None
     for k in keys:
         print(f"[bench] {k}: setup", file=sys.stderr, flush=True)
-        launch, info = {**CONFIGS, **ON_REQUEST}[k](vqx, torch, L)
-        tm = time_config(torch, launch, a.steps, a.warmup)
+        launches, info = {**CONFIGS, **ON_REQUEST}[k](vqx, torch, L)
+        tm = time_config(torch, launches, a.steps, a.warmup, warm=not a.no_warm)
         ms = tm["kernel_ms_avg"]
         gbs = info["bytes"] / (ms * 1e-3) / 1e9
         region = tm["region_ms"] / a.steps
@@ -886,7 +1016,15 @@ def main():
             "region_ms_per_step": region, "kernel": DOMINANT.get(k),
             "hbm_traffic_bytes": measured_traffic(k),
             "algorithmic_bytes": info["bytes"], "achieved_GBps": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
-            "dtype": info["dtype"]}
+            "dtype": info["dtype"], "buffer_sets": tm["buffer_sets"]}
+        if tm["buffer_sets"] > 1:
+            results[k]["buffer_set_bytes"] = info["bytes"]
+            results[k]["timing"] = (f"cold MALL: the timed launches cycle through {tm['buffer_sets']} sets of "
+                                    f"input and output buffers (> 512 MiB together)")
+        if "kernel_ms_warm" in tm:
+            mw = tm["kernel_ms_warm"]
+            results[k]["kernel_ms_warm"] = mw
+            results[k]["hbm_frac_warm"] = info["bytes"] / (mw * 1e-3) / 1e9 / HBM_PEAK_GBS
         if info.get("launches", 1) > 1:
             results[k]["launches_per_step"] = info["launches"]
         if info.get("multi_launch"):
@@ -907,8 +1045,12 @@ def main():
             print(f"[bench] {k}: {ms * 1e3:.1f} us/launch, {tf:.0f} TFLOP/s ({tf / BF16_PEAK_TFLOPS:.1%} of bf16 "
                   f"MFMA peak)", file=sys.stderr, flush=True)
         else:
-            print(f"[bench] {k}: {ms * 1e3:.1f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)",
-                  file=sys.stderr, flush=True)
+            warm_txt = ""
+            if "kernel_ms_warm" in results[k]:
+                warm_txt = (f"; warm MALL {results[k]['kernel_ms_warm'] * 1e3:.1f} us "
+                            f"({results[k]['hbm_frac_warm']:.1%})")
+            print(f"[bench] {k}: {ms * 1e3:.1f} us/launch, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak, "
+                  f"{tm['buffer_sets']} buffer sets){warm_txt}", file=sys.stderr, flush=True)
         if "nnz" in info:
             results[k]["nnz"] = info["nnz"]
         if "gathered_bytes" in info:
@@ -921,7 +1063,8 @@ def main():
                   f"({results[k]['cpu_oracle']['sample']})", file=sys.stderr, flush=True)
         if k == HEADLINE:
             info_head = info
-        del launch
+        del launches
+        info.pop("keep", None)
         torch.cuda.empty_cache()
     head = results[HEADLINE]
     cpu = None
@@ -946,7 +1089,8 @@ def main():
                      "frac": head["hbm_frac"], "traffic": head["hbm_traffic_bytes"],
                      "kernel": DOMINANT[HEADLINE],
                      "algorithmic_bytes_per_launch": head["algorithmic_bytes"],
-                     "kernel_ms_avg": head["kernel_ms"]},
+                     "kernel_ms_avg": head["kernel_ms"], "mall": "cold",
+                     "buffer_sets": head["buffer_sets"], "kernel_ms_warm": head.get("kernel_ms_warm")},
         "cpu_baseline": cpu,
         "configs": results,
     }

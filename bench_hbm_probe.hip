@@ -1,5 +1,6 @@
 // HBM bandwidth probe by traffic mix, for bench.py --hbm-ceiling: not part of
-// the quantization library (built into its own libvqx_probe.so).
+// the quantization library.  `python bench.py --build-probe` compiles it into
+// bench_hbm_probe.so beside this file.
 //
 // Each unit of work reads r 16-byte chunks and writes w 16-byte chunks.
 // Chunk j of unit u is at byte 16 (j * units + u) of its buffer, so every

@@ -363,8 +363,11 @@ int vqx_quantize_mx_outlier(const void* x, int64_t batches, int64_t rows, int64_
  * only the rows whose outliers did not fit their slots, and pads the unused
  * entries.  Same reference interfaces as the two entry points above
  * (src/vc/ops/quantized.py:532-630, :633-712).
+ * Matrices of more than 16384 rows take the two-pass form instead (the
+ * second launch's reads would grow as rows^2), and ignore the workspace.
  * vqx_outlier_workspace_size gives the bytes for the default slots per row
- * (0 when batches * rows == 0; workspace may then be NULL).  Any workspace of
+ * (0 when batches * rows == 0 or rows > 16384; workspace may then be NULL).
+ * Otherwise any workspace of
  * at least the 256-byte-aligned 4 * batches * rows bytes of the counts works:
  * the rest sets the slots per row (fewer slots, more rows read again).
  * workspace: 256-byte aligned device memory, contents ignored; calls that

@@ -67,6 +67,37 @@ def test_gwa_special_values_and_scale_qmap(vqx, dt):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("bs", [32, 64])
+def test_gwa_scale_qmap_rounding_scale_to_zero(vqx, bs):
+    # blocks of exact zeros plus values below fp8_e5m3's subnormals: the
+    # scale codebook rounds sf to 0, so a zero element gives 0 / 0 = NaN and
+    # the output keeps it (torch.clamp propagates NaN), while the nonzero
+    # elements give (qmax - zp) * 0.  Mixed with ordinary blocks in the same
+    # waves, so the fast path of those waves must step aside too.
+    from importlib import import_module
+
+    qops = import_module(vqx.__name__ + ".ops.quantized")
+    g = torch.Generator().manual_seed(23)
+    rows = []
+    for r in range(32):
+        if r % 3 == 0:
+            row = torch.zeros(128)
+            row[torch.randint(0, 128, (5,), generator=g)] = torch.rand(5, generator=g) * 1e-6
+        elif r % 3 == 1:
+            row = torch.where(torch.rand(128, generator=g) < 0.5, 0.0, torch.rand(128, generator=g) * 3e-6)
+        else:
+            row = torch.randn(128, generator=g)
+        rows.append(row)
+    x = torch.stack(rows).to(torch.bfloat16)
+    sq = R.table_tensor(F.quantization_table("fp8_e5m3"))
+    sf, zp, y = qops.gwa_fake_quantize(x.cuda(), -1, bs, 0, 3, sq.cuda())
+    rsf, rzp, ry = R.group_wise_affine_fake_quant(x, -1, bs, 0, 3, sq)
+    assert bool(torch.isnan(ry).any()), "the case needs NaN outputs"
+    assert same(sf, rsf) and same(zp, rzp), "scale / zero point"
+    assert same(y, ry), f"{int((~((y.cpu() == ry) | (torch.isnan(y.cpu()) & torch.isnan(ry)))).sum())} outputs differ"
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("bs", [8, 64])
 def test_gwa_quotients_near_and_below_the_normal_range(vqx, bs):
     # bf16 blocks whose quotients x / scale fall among the bf16 subnormals

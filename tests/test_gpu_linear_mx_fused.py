@@ -222,3 +222,40 @@ def test_linear_mx_unfusable_operands_still_match(vqx):
     want = R.linear_mx(A, idx, None, scale.float(), 64, code)
     assert out.dtype == want.dtype == torch.float32
     assert torch.allclose(out.cpu(), want, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.gpu
+def test_linear_mx_fused_offset_views(vqx):
+    # activations cut from a flat buffer at an odd element offset and a bias
+    # sliced at an offset that is not a multiple of 4 elements: contiguous
+    # views whose storage is not 16- (A) or 8-byte (bias) aligned still run
+    # fused and match the oracle
+    N, K, M = 256, 512, 48
+    idx, scale, code = random_convert_format(N, K, 15)
+    g = torch.Generator().manual_seed(16)
+    flat = torch.randn(M * K + 3, generator=g).to(torch.bfloat16).cuda()
+    x = flat[3:].view(M, K)
+    bflat = torch.randn(N + 5, generator=g).to(torch.bfloat16).cuda()
+    bias = bflat[5:]
+    assert x.data_ptr() % 16 and bias.data_ptr() % 8
+    with fused_only():
+        out = Q.linear_mx(x, idx.cuda(), bias, weight_scale=scale.cuda(), weight_code=code.cuda(), block_size=64)
+    within_tolerance(out, R.linear_mx(x.cpu(), idx, bias.cpu(), scale, 64, code))
+
+
+@pytest.mark.gpu
+def test_linear_mx_fused_under_inference_mode(vqx):
+    # operands made under torch.inference_mode carry no version counter; the
+    # packed-weight cache keys them on their storage and the call runs fused,
+    # twice (the second from the cache)
+    N, K, M = 256, 512, 32
+    idx, scale, code = random_convert_format(N, K, 17)
+    A = torch.randn(M, K, generator=torch.Generator().manual_seed(18)).to(torch.bfloat16)
+    with torch.inference_mode():
+        w, s, c, a = idx.cuda(), scale.cuda(), code.cuda(), A.cuda()
+        assert w.is_inference()
+        with fused_only():
+            first = Q.linear_mx(a, w, None, weight_scale=s, weight_code=c, block_size=64)
+            second = Q.linear_mx(a, w, None, weight_scale=s, weight_code=c, block_size=64)
+    assert torch.equal(first, second)
+    within_tolerance(first, R.linear_mx(A, idx, None, scale, 64, code))

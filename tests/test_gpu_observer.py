@@ -220,3 +220,28 @@ def test_derived_bias_scale(vqx, weight_spec):
     assert not bfq._observer_on()
     bfq.disable_fake_quant()
     assert bfq(bias.cuda()).equal(bias.cuda())
+
+
+@pytest.mark.gpu
+def test_module_built_and_run_under_inference_mode(vqx):
+    # a module made and run under torch.inference_mode: its buffers carry no
+    # version counter, so the enable flags are read on every forward and an
+    # in-place write to them (disable_observer) takes effect at once
+    print("observer under inference_mode", flush=True)
+    xs = steps((64, 96), torch.bfloat16, 7, 3, edge=False)
+    with torch.inference_mode():
+        fq = spec_module(vqx, "int8,qs=per_tensor_symmetric,ahl=2")
+        assert fq.observer_enabled.is_inference()
+        ora = oracle_for(fq, "int8")
+        for t, x in enumerate(xs[:5]):
+            assert_bitexact(fq(x.cuda()).cpu(), ora(x), f"step {t} output")
+            check_state(fq, ora, f"step {t}")
+        fq.disable_observer()
+        ora.observer_enabled = False
+        assert_bitexact(fq(xs[5].cuda()).cpu(), ora(xs[5]), "observer off")
+        check_state(fq, ora, "observer off")
+        mx = spec_module(vqx, "nf4_6,qs=microscaling,bs=64,ax=-1,scale=fp8_e5m3")
+        x = xs[6]
+        want = R.mx_fake_quantize(x, R.table_tensor(F.quantization_table("nf4_6")), [-1], 64, 31.0, False,
+                                  R.table_tensor(F.quantization_table("fp8_e5m3")))[1]
+        assert_bitexact(mx(x.cuda()).cpu(), want, "microscaling under inference_mode")

@@ -352,8 +352,10 @@ def test_filter_outlier_one_pass_equals_two_pass(vqx, dtype, shape, slots):
 
 @pytest.mark.gpu
 def test_filter_outlier_one_pass_dense_rows_and_many_rows(vqx):
-    # rows all outliers (more than the largest default staging), and more
-    # than 16384 rows per batch (256-row chunks in the second launch)
+    # rows all outliers (more than the largest default staging); 16384 rows
+    # per batch, the most the one-pass form takes (64-row chunks in its
+    # second launch), and 17000, which the _ws entry point hands to the
+    # two-pass form (its finalize reads would grow as rows^2)
     x = rand_outliers((2, 40, 3000), torch.bfloat16, seed=4)
     x[0, 5] = 100.0
     x[1, 39, 1000:] = -100.0
@@ -361,10 +363,11 @@ def test_filter_outlier_one_pass_dense_rows_and_many_rows(vqx):
     for pct in (0.5, 0.02):
         max_nnz = int(40 * 3000 * pct)
         check_all(_filter(vqx, x, 3.0, max_nnz, 0, None), _filter(vqx, x, 3.0, max_nnz, 0), CSR)
-    y = rand_outliers((2, 17000, 64), torch.bfloat16, seed=6, frac=0.01).cuda()
-    for slots in (None, 1):
-        check_all(_filter(vqx, y, 3.0, int(17000 * 64 * 0.01), 5, slots), _filter(vqx, y, 3.0, int(17000 * 64 * 0.01), 5),
-                  CSR)
+    for rows in (16384, 17000):
+        y = rand_outliers((2, rows, 64), torch.bfloat16, seed=6, frac=0.01).cuda()
+        for slots in (None, 1):
+            check_all(_filter(vqx, y, 3.0, int(rows * 64 * 0.01), 5, slots),
+                      _filter(vqx, y, 3.0, int(rows * 64 * 0.01), 5), CSR)
 
 
 def _qmx(vqx, x, qm, bs, pow2, sq, thr, max_nnz, offset, slots="two-pass"):

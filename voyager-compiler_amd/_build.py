@@ -1,8 +1,7 @@
 """Build libvqx.so (the HIP kernels and their C ABI) in-tree for gfx950.
 
 ``build()`` compiles every ``csrc/*.hip`` with hipcc into ``_build/`` and
-links ``libvqx.so`` next to this file, and builds ``libvqx_probe.so`` (the HBM
-traffic-mix probe that ``bench.py --hbm-ceiling`` times) from ``probe/``.  It always recompiles (the caller asks
+links ``libvqx.so`` next to this file.  It always recompiles (the caller asks
 for a fresh build); objects compile in parallel.
 """
 
@@ -16,7 +15,6 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libvqx.so")
-PROBE_LIB = os.path.join(HERE, "libvqx_probe.so")
 ARCH = os.environ.get("VQX_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep hipcc from forming packed fp32 instructions.
@@ -60,10 +58,6 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB)
-    # the HBM traffic-mix probe of bench.py --hbm-ceiling: its own library
-    tmp = PROBE_LIB + ".tmp"
-    _run([hipcc, *HIPCC_FLAGS, "-shared", os.path.join(HERE, "probe", "hbm_mix.hip"), "-o", tmp])
-    os.replace(tmp, PROBE_LIB)
     return LIB
 
 

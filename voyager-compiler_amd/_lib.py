@@ -169,3 +169,14 @@ def require_device(t, what):
     if not t.is_cuda:
         raise RuntimeError(
             f"vqx: {what} runs on the MI355X only (got a {t.device} tensor); there is no CPU path")
+
+
+INFERENCE = "inference"
+
+
+def version_of(t):
+    """t's version counter, the key the host-side caches use to notice an
+    in-place write.  Tensors made under torch.inference_mode carry no
+    counter (reading it raises); they give INFERENCE instead, so a cache
+    keyed on them relies on their storage (data_ptr) alone."""
+    return INFERENCE if t.is_inference() else t._version

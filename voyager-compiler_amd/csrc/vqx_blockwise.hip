@@ -154,10 +154,14 @@ __device__ __forceinline__ uint32_t e8m0_of(float s) {
 
 // x / s rounded as the input dtype divides: exactly by the reciprocal when s
 // is a power of two whose reciprocal is a normal-or-exact fp32, else IEEE.
+// A NaN quotient (a NaN x, or +-Inf / Inf) takes x's sign, so that the code
+// of a NaN value (the format's all-ones magnitude) has a defined sign bit:
+// the reference's values are NaN either way, and it writes no codes.
 template <typename T>
 __device__ __forceinline__ uint32_t div_to_bf16(float x, float s, float rcp, bool pow2) {
   float q = pow2 ? x * rcp : x / s;
-  return f2bf(BT<T>::val(BT<T>::round_bits(q)));
+  const uint32_t h = f2bf(BT<T>::val(BT<T>::round_bits(q)));
+  return q == q ? h : (h & 0x7FFFu) | ((f2u(x) >> 16) & 0x8000u);
 }
 
 // ---------------------------------------------------------------------------
@@ -481,11 +485,14 @@ __global__ __launch_bounds__(256) void gwa_fq_rows_kernel(const T* __restrict__ 
       for (int i = 0; i < 8; ++i) qd[i] = v[i] / sf;
     }
     float o[8];
-    // bf16 and only finite values in all of the wave's blocks: then sf, zp
-    // and every intermediate are finite (|x / sf| stays below about 3 * 2^8,
-    // the block's range being at least one bf16 step of its values), so the
-    // clamp is one v_med3 and the stores go through v_cvt_pk_bf16_f32
-    const bool finite = __builtin_isfinite(mn) && __builtin_isfinite(mx);
+    // bf16, only finite values in all of the wave's blocks, a normal sf
+    // whose reciprocal is normal, and a finite zp: then no intermediate is a
+    // NaN (a quotient can still overflow to +-Inf, which v_med3 clamps as the
+    // compares do), so the clamp is one v_med3 and the stores go through
+    // v_cvt_pk_bf16_f32.  A scale_qmap can round sf to 0 (fp8_e5m3 below its
+    // subnormals): then 0 / 0 is a NaN that must reach the output, and
+    // v_med3 would turn it into quant_min, so such waves take the compares.
+    const bool finite = __builtin_isfinite(mn) && __builtin_isfinite(mx) && __builtin_isfinite(zp) && !slow;
     const bool fast = sizeof(T) == 2 && __builtin_amdgcn_ballot_w64(!finite) == 0;
     if (fast) {
       u32x4 w;
@@ -806,7 +813,11 @@ __global__ __launch_bounds__(kMxLutThreads) void mx_lut_kernel(const uint16_t* _
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         uint32_t xb = (j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16);
-        uint32_t e = full[f2bf(u2f(xb) / s)];
+        const float q = u2f(xb) / s;
+        uint32_t h = f2bf(q);
+        // a NaN quotient takes x's sign (as div_to_bf16 gives it)
+        h = q == q ? h : (h & 0x7FFFu) | ((xb >> 16) & 0x8000u);
+        uint32_t e = full[h];
         if constexpr (CT) e = (CB == 4 && (j & 1)) ? (e >> 16) << 4 : e >> 16;
         ent[j] = e;
       }

@@ -994,6 +994,13 @@ int quantize_mx_outlier_fused(const void* x, int64_t nb, int64_t rows, int64_t c
   return check_launch("quantize_mx_outlier");
 }
 
+// The one-pass finalize sums, in each of its (about 256) workgroups, the
+// counts of every row of the batch before its chunk, so its reads grow as
+// rows^2 / chunk; past this many rows per matrix the _ws entry points take
+// the two-pass form (count, one scan per batch, split), whose reads are
+// linear in rows.
+constexpr int64_t kOnePassMaxRows = 16384;
+
 int64_t outlier_stage_slots(int64_t rows, int64_t cols, int64_t max_nnz) {
   if (max_nnz <= 0 || rows <= 0 || cols <= 0) return 0;
   const int64_t per = (max_nnz + rows - 1) / rows;
@@ -1014,7 +1021,7 @@ int outlier_workspace_size(int dtype, int64_t nb, int64_t rows, int64_t cols, in
     default: return set_error(kErrInvalid, "outlier_workspace_size: dtype %d not supported (fp32, bf16, fp16)", dtype);
   }
   const int64_t nrows = nb * rows;
-  *bytes = nrows == 0 ? 0
+  *bytes = nrows == 0 || rows > kOnePassMaxRows ? 0
                       : (int64_t)(stage_counts_bytes(nrows) +
                                   (size_t)nrows * (size_t)outlier_stage_slots(rows, cols, max_nnz) * (size_t)(4 + es));
   return kOk;
@@ -1032,6 +1039,9 @@ int filter_outlier_ws(const void* x, int dtype, int64_t nb, int64_t rows, int64_
   const int es = dtype == kF32 ? 4 : 2;
   if (dtype != kF32 && dtype != kBF16 && dtype != kF16)
     return set_error(kErrInvalid, "filter_outlier: dtype %d not supported (fp32, bf16, fp16)", dtype);
+  if (rows > kOnePassMaxRows)
+    return filter_outlier(x, dtype, nb, rows, cols, threshold, max_nnz, indptr_offset, data, indices, indptr, inlier,
+                          st);
   Stage sg;
   if (stage_from_workspace(workspace, workspace_bytes, nb * rows, cols, es, &sg, "filter_outlier") != kOk)
     return kErrInvalid;
@@ -1059,6 +1069,9 @@ int quantize_mx_outlier_fused_ws(const void* x, int64_t nb, int64_t rows, int64_
     return set_error(kErrInvalid, "quantize_mx_outlier: sizes beyond int32 indices");
   if (!aligned(x, 16) || !aligned(values, 16))
     return set_error(kErrInvalid, "quantize_mx_outlier: input and values must be 16-byte aligned");
+  if (rows > kOnePassMaxRows)
+    return quantize_mx_outlier_fused(x, nb, rows, cols, threshold, max_nnz, indptr_offset, block_size, sp, qmap, data,
+                                     indices, indptr, scale, values, st);
   Stage sg;
   if (stage_from_workspace(workspace, workspace_bytes, nb * rows, cols, 2, &sg, "quantize_mx_outlier") != kOk)
     return kErrInvalid;

@@ -149,7 +149,7 @@ _TABLE_FMT = {}  # data_ptr -> (weakref to table tensor, version, Format)
 def register_table(t: torch.Tensor, fmt: Format):
     """Remember that table ``t`` is ``fmt``'s, so ops given ``t`` as a qmap
     can run the closed-form encoder instead of the table gather."""
-    _TABLE_FMT[t.data_ptr()] = (weakref.ref(t), t._version, fmt)
+    _TABLE_FMT[t.data_ptr()] = (weakref.ref(t), _lib.version_of(t), fmt)
 
 
 def _format_of_table(qmap: torch.Tensor) -> Optional[Format]:
@@ -157,7 +157,7 @@ def _format_of_table(qmap: torch.Tensor) -> Optional[Format]:
     if ent is None:
         return None
     ref, ver, fmt = ent
-    if ref() is not qmap or qmap._version != ver:
+    if ref() is not qmap or _lib.version_of(qmap) != ver:
         return None
     return fmt
 
@@ -171,7 +171,7 @@ def _table_bf16(qmap: torch.Tensor) -> torch.Tensor:
         raise ValueError(f"qmap must have 65536 entries (one per bf16 pattern), got {qmap.numel()}")
     if qmap.dtype == torch.bfloat16 and qmap.is_contiguous():
         return qmap
-    key = (qmap.data_ptr(), qmap._version, qmap.dtype)
+    key = (qmap.data_ptr(), _lib.version_of(qmap), qmap.dtype)
     hit = _BF16_TABLES.get(key)
     if hit is not None and hit[0]() is qmap:
         return hit[1]
@@ -453,7 +453,7 @@ def _code_lut(code: torch.Tensor) -> torch.Tensor:
     negative index counting from the end.  Patterns whose index falls outside
     the table (and NaN / Inf) map to NaN, where the reference raises
     IndexError."""
-    key = (code.data_ptr(), code._version, code.numel(), code.dtype)
+    key = (code.data_ptr(), _lib.version_of(code), code.numel(), code.dtype)
     hit = _CODE_LUTS.get(key)
     if hit is not None and hit[0]() is code:
         return hit[1]
@@ -475,7 +475,7 @@ _BF16_EXACT = {}
 def _bf16_exact(code: torch.Tensor) -> bool:
     """Whether every code value survives a round trip through bf16 (the
     65536-entry table the lookup uses holds bf16 values)."""
-    key = (code.data_ptr(), code._version, code.numel(), code.dtype)
+    key = (code.data_ptr(), _lib.version_of(code), code.numel(), code.dtype)
     hit = _BF16_EXACT.get(key)
     if hit is not None and hit[0]() is code:
         return hit[1]
@@ -535,7 +535,7 @@ def _packed_weight(weight, weight_code, weight_scale, transposed):
     path then reproduces the reference's behaviour)."""
     key = (id(weight), bool(transposed))
     deps = (weight, weight_code, weight_scale)
-    versions = tuple(None if t is None else (t.data_ptr(), t._version) for t in deps)
+    versions = tuple(None if t is None else (t.data_ptr(), _lib.version_of(t)) for t in deps)
     hit = _PACKED.get(key)
     if hit is not None and hit.versions == versions and all(
             (r is None and t is None) or (r is not None and r() is t) for r, t in zip(hit.refs, deps)):
@@ -608,8 +608,15 @@ def _fused_linear(x, weight, bias, weight_scale, weight_code, transposed):
         return None
     K = x.shape[-1]
     N = weight.shape[1] if transposed else weight.shape[0]
+    # the kernel reads A in 16-byte and the bias in 8-byte units: a view
+    # with an odd storage offset (a slice of a flat buffer) is copied first
     b = None if bias is None else bias.contiguous()
-    out = _nf4_product(x.reshape(-1, K).contiguous(), *packed, b, N)
+    if b is not None and b.data_ptr() % 8:
+        b = b.clone()
+    x2 = x.reshape(-1, K).contiguous()
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    out = _nf4_product(x2, *packed, b, N)
     return out.reshape(*x.shape[:-1], N)
 
 

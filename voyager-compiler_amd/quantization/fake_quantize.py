@@ -148,11 +148,15 @@ class _BufferFlags:
     moves with the enable_ / disable_ methods, load_state_dict and in-place
     writes such as lcq.py's fake_quant_enabled.zero_() / .copy_(), and a moved
     buffer is a new tensor.  So a forward reads the device only after a
-    change."""
+    change.  Buffers made under torch.inference_mode have no version counter
+    and can be written in place there unseen, so they are read on every
+    forward, as the reference reads them."""
 
     def _flag(self, name):
         cache = self.__dict__.setdefault("_flag_cache", {})
         buf = getattr(self, name)
+        if buf.is_inference():
+            return int(buf[0].item())
         key = (id(buf), buf.data_ptr(), buf.device, buf._version)
         hit = cache.get(name)
         if hit is not None and hit[0] == key:
@@ -248,11 +252,11 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
         if self.scale_dtype is not None and (self.scale_qmap is None or self.scale_qmap.numel() == 0):
             self.scale_qmap = self._build_scale_qmap(device).to(device)
         if self._qmap_sig is None:
-            self._qmap_sig = (self.qmap.data_ptr(), self.qmap._version)
+            self._qmap_sig = (self.qmap.data_ptr(), _lib.version_of(self.qmap))
 
     def _closed_form(self):
         """The format's closed form applies while qmap is the table it built."""
-        return self._qmap_sig == (self.qmap.data_ptr(), self.qmap._version)
+        return self._qmap_sig == (self.qmap.data_ptr(), _lib.version_of(self.qmap))
 
     # max_outlier_pct: the largest fraction of outliers seen so far
     # (fake_quantize.py:389-391).  The device keeps the (count, numel) pair of
