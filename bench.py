@@ -652,6 +652,36 @@ def setup_o3(vqx, torch, L):
         flops=2 * nnz * N, bound="hbm", dtype="bf16", nnz=nnz, cpu_input=cpu, keep=(bufs, sets))
 
 
+def setup_f1(vqx, torch, L, spec, shape, seed=13):
+    """FusedAmaxObsFakeQuantize forward with outliers, as the reference's
+    LLaMA outlier configs quantize a Linear's activation (opct: the top 1%
+    by magnitude, with the threshold's running average) or the attention's
+    value operand (othr: |x| >= 6), on bf16 activations N(0,1) with 1% of
+    the entries scaled by 20.  One step is one module forward: the top-k
+    threshold passes (opct) and the fused mask / MX fake-quant / restore /
+    count pass, all on the device."""
+    g = torch.Generator().manual_seed(seed)
+    xc = torch.randn(*shape, generator=g)
+    xc = torch.where(torch.rand(shape, generator=g) < 0.01, xc * 20, xc).to(torch.bfloat16)
+    fq = vqx.quantization.QuantizationSpec.from_str(spec).make_fake_quantize("cuda").cuda()
+    n = xc.numel()
+
+    def make(i):
+        x = xc.cuda()
+        return (lambda: (fq(x), 0)[1]), x
+
+    # the fused pass reads x and writes y and the scales; the opct threshold
+    # needs x read once more before it (the select's minimum)
+    algo = 4 * n + n // 64 * 2 + (2 * n if "opct" in spec else 0)
+    launches, bufs = rotate(make, 4 * n)
+    launches[0]()
+    torch.cuda.synchronize()
+    return launches, dict(
+        name=f"F1 FusedAmaxObsFakeQuantize('{spec}') forward, bf16 {list(shape)} N(0,1) with 1% x20 outliers seed "
+             f"{seed}: every kernel on the device, no host synchronisation",
+        elements=n, bytes=algo, bound="hbm", dtype="bf16", multi_launch=True, keep=(fq, bufs))
+
+
 CONFIGS = {
     "c2": lambda v, t, L: setup_c2(v, t, L),
     "c1": lambda v, t, L: setup_c1(v, t, L),
@@ -674,6 +704,10 @@ CONFIGS = {
     "o2_quantize_mx_outlier": lambda v, t, L: setup_o1(v, t, L, mx=True),
     "o3_spmm": lambda v, t, L: setup_o3(v, t, L),
     "l1_histogram": lambda v, t, L: setup_l1(v, t, L),
+    "f1_outlier_opct": lambda v, t, L: setup_f1(v, t, L, "nf4_6,qs=microscaling,bs=64,ax=-1,scale=fp8_e5m3,opct=0.01",
+                                                (2048, 4096)),
+    "f1_outlier_othr_ax2": lambda v, t, L: setup_f1(v, t, L, "nf4_6,qs=microscaling,bs=64,ax=-2,scale=fp8_e5m3,othr=6.0",
+                                                    (1, 32, 2048, 128)),
     "g1_gptq": lambda v, t, L: setup_g1(v, t, L),
 }
 HEADLINE = "c2"
@@ -854,6 +888,8 @@ DOMINANT = {
     "o3_spmm": "spmm_csr_kernel<1, 8>",
     "l1_histogram": "lcq_hist_kernel<0, true, false>",
     "g1_gptq": "gptq_block_kernel",
+    "f1_outlier_opct": "mx_lut_kernel<0, 4, true, 2, false, true>",
+    "f1_outlier_othr_ax2": "mx_block_kernel<unsigned short, vqx::EncLevels>",
 }
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
 
@@ -1033,11 +1069,18 @@ def main():
             for key in ("kernel_ms", "kernel_ms_isolated_median", "hbm_traffic_bytes", "algorithmic_bytes",
                         "achieved_GBps", "hbm_frac"):
                 results[k].pop(key)
-            tf = info["flops"] / (ms * 1e-3) / 1e12
-            results[k].update({"step_is_many_launches": True, "step_ms": ms,
-                               "trailing_update_flops": info["flops"], "trailing_update_TFLOPs_over_step": tf})
-            print(f"[bench] {k}: {ms:.2f} ms/step (many launches), trailing updates at {tf:.1f} TFLOP/s over "
-                  f"the step", file=sys.stderr, flush=True)
+            results[k].update({"step_is_many_launches": True, "step_ms": ms})
+            if "flops" in info:
+                tf = info["flops"] / (ms * 1e-3) / 1e12
+                results[k].update({"trailing_update_flops": info["flops"], "trailing_update_TFLOPs_over_step": tf})
+                print(f"[bench] {k}: {ms:.2f} ms/step (many launches), trailing updates at {tf:.1f} TFLOP/s over "
+                      f"the step", file=sys.stderr, flush=True)
+            else:
+                gbs = info["bytes"] / (ms * 1e-3) / 1e9
+                results[k].update({"algorithmic_bytes": info["bytes"], "step_GBps": gbs,
+                                   "step_hbm_frac": gbs / HBM_PEAK_GBS})
+                print(f"[bench] {k}: {ms * 1e3:.1f} us/step (many launches), {gbs:.0f} GB/s of algorithmic bytes "
+                      f"over the step ({gbs / HBM_PEAK_GBS:.1%} of HBM peak)", file=sys.stderr, flush=True)
         elif info["bound"] == "mfma":
             tf = info["flops"] / (ms * 1e-3) / 1e12
             results[k].update({"algorithmic_flops": info["flops"], "achieved_TFLOPs": tf,

@@ -207,6 +207,60 @@ int vqx_mx_quantize(const void* x, int32_t x_dtype, int64_t outer, int64_t L, in
                     void* fq, void* codes, int32_t code_layout, vqx_stream_t stream);
 
 /*
+ * FakeQuantize outlier masking (FusedAmaxObsFakeQuantize.forward,
+ * src/vc/quantization/fake_quantize.py:373-395).  An element is an outlier
+ * when |x| >= t, compared in x's dtype (t rounded to it, as torch casts the
+ * threshold); a NaN t skips nothing, a t <= -0 every non-NaN element.  t is
+ * read from threshold_dev (fp32, device) when it is not NULL, else it is
+ * `threshold`.
+ * stats (optional): 32 bytes of device memory, zeroed once by the caller,
+ * that keep the largest fraction of outliers seen (max_outlier_pct,
+ * :389-391) as the fp64 at byte offset 16 (count / numel, as Python divides);
+ * calls sharing one stats buffer must be ordered (one stream).
+ */
+
+/*
+ * The outlier_pct threshold (fake_quantize.py:373-387): the k-th largest |x|
+ * (torch.topk(|x|, k).values.min(); NaN when x holds a NaN), k in [1, n],
+ * then written to *threshold (fp32, device): ema 0 stores it, ema 1 updates
+ * *threshold = *threshold * decay + (value * one_minus_decay rounded to x's
+ * dtype), in fp32 (F32, BF16 or F16 x; 16-byte aligned).  workspace:
+ * vqx_outlier_topk_workspace_size bytes of 16-byte aligned device memory,
+ * zeroed once before its first use (calls leave it ready for the next);
+ * calls sharing one workspace must be ordered.
+ */
+int vqx_outlier_topk_workspace_size(int64_t* bytes);
+int vqx_outlier_topk_threshold(const void* x, int32_t x_dtype, int64_t n, int64_t k, int32_t ema, float decay,
+                               float one_minus_decay, float* threshold, void* workspace, int64_t workspace_bytes,
+                               vqx_stream_t stream);
+
+/*
+ * MXFakeQuantizeFunction.forward between the outlier mask and restore
+ * (fake_quantize.py:388-395 around :397-408) in one pass: vqx_mx_quantize's
+ * fake-quant values and scale of x with its outliers zeroed, the outliers
+ * written back unchanged into fq, and counted into stats.  Same geometry and
+ * scale arguments as vqx_mx_quantize; the scale goes to scale_out (x's
+ * dtype) and / or scale_f32 (its value in fp32), each optional.
+ */
+int vqx_mx_fake_quant_outlier(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
+                              int64_t block_size, const vqx_format* fmt, int32_t scale_mode, int32_t pow2_shift,
+                              float quant_max, const uint16_t* scale_qmap, const float* threshold_dev,
+                              float threshold, void* stats, void* scale_out, float* scale_f32, void* fq,
+                              vqx_stream_t stream);
+
+/*
+ * The mask and the restore around the other quantization schemes
+ * (fake_quantize.py:388-391, :429-430): masked = x.masked_fill(|x| >= t, 0)
+ * (optional: with masked NULL only the count is taken, into stats), and
+ * y[i] = x[i] where x[i] is an outlier (y is written only there).  F32, BF16
+ * or F16; 16-byte aligned x and masked.
+ */
+int vqx_outlier_mask(const void* x, int32_t x_dtype, int64_t n, const float* threshold_dev, float threshold,
+                     void* stats, void* masked, vqx_stream_t stream);
+int vqx_outlier_restore(const void* x, int32_t x_dtype, int64_t n, const float* threshold_dev, float threshold,
+                        void* y, vqx_stream_t stream);
+
+/*
  * quantized_ops::dequantize with input_qmap (src/vc/ops/quantized.py:175-227),
  * on packed codes: out[i] = decode_table[code(i)] * scale[i / block_size],
  * rounded to out_dtype (F32 or BF16).  scale_kind 0 = fp32, 1 = bf16,

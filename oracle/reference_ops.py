@@ -30,6 +30,7 @@ __all__ = [
     "codebook_encode_rows",
     "convert_weight",
     "AmaxObserverFakeQuantize",
+    "OutlierFakeQuantize",
     "codebook_decode_rows",
     "linear_mx",
     "filter_outlier",
@@ -227,6 +228,51 @@ class AmaxObserverFakeQuantize:
         if not self.fake_quant_enabled:
             return x
         return fake_quantize_per_tensor(x, self.qmap, self.scale)
+
+
+class OutlierFakeQuantize:
+    """FusedAmaxObsFakeQuantize.forward's outlier handling (src/vc/
+    quantization/fake_quantize.py:373-395, :429-430) around a fake-quant
+    step, on CPU tensors, over many forwards: with outlier_pct, the top-k
+    threshold of |x| (k = max(1, ceil(pct * numel))) copied into the fp32
+    outlier_threshold on the first observed forward, then folded in as
+    threshold * decay + value * (1 - decay) (in-place ops on the fp32 buffer,
+    the product in x's dtype); the outliers |x| >= threshold masked to 0
+    before the fake-quant and put back after it; max_outlier_pct the largest
+    count / numel seen.  fake_quant: a callable x -> y (the scheme's
+    fake-quant of the masked input), or None when fake-quant is disabled."""
+
+    def __init__(self, outlier_pct=None, outlier_threshold=None, decay=0.9):
+        self.outlier_pct = outlier_pct
+        self.outlier_ema_decay = decay
+        self.outlier_threshold = torch.tensor([], dtype=torch.float32) if outlier_pct is not None \
+            else outlier_threshold
+        self.max_outlier_pct = 0
+        self.observer_enabled = True
+
+    def __call__(self, x, fake_quant):
+        if self.outlier_pct is not None and self.observer_enabled:
+            flat = x.abs().flatten()
+            k = max(1, math.ceil(self.outlier_pct * flat.numel()))
+            threshold = torch.topk(flat, k, largest=True, sorted=False).values.min()
+            if self.outlier_threshold.numel() == 0:
+                self.outlier_threshold.resize_as_(threshold)
+                self.outlier_threshold.copy_(threshold)
+            else:
+                self.outlier_threshold.mul_(self.outlier_ema_decay).add_(
+                    threshold * (1.0 - self.outlier_ema_decay))
+        skip = None
+        if self.outlier_threshold is not None:
+            skip = x.abs() >= self.outlier_threshold
+            orig_x = x.clone()
+            x = x.masked_fill(skip, 0.0)
+            pct = skip.sum().item() / x.numel()
+            self.max_outlier_pct = max(pct, self.max_outlier_pct)
+        if fake_quant is not None:
+            x = fake_quant(x)
+        if skip is not None:
+            x = torch.where(skip, orig_x, x)
+        return x
 
 
 def codebook_encode_rows(x, cb):

@@ -278,3 +278,54 @@ def test_llama_qconfig_specs(vqx, spec):
         wy = torch.where(skip, x, wy)
         assert bool(skip.any())
     assert_bitexact(y, wy, spec)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape,axis,bs", [((4, 100, 24), 1, 32), ((2, 256, 136), 1, 64), ((3, 128, 64), 1, 128),
+                                           ((2, 40, 16), 1, 16), ((64, 200), 0, 32), ((2, 3, 96, 40), 2, 64)])
+@pytest.mark.parametrize("dtype,qmax,pow2", [("fp8_e4m3", 448.0, True), ("nf4_6", 31.0, False),
+                                             ("int6", 31.0, False)])
+def test_mx_middle_axis_tiles(vqx, xdt, shape, axis, bs, dtype, qmax, pow2):
+    # blocks along a middle (or first) axis whose inner size is a multiple of
+    # 16 bytes: the tiled column kernel, with short last blocks, partial
+    # column tiles, every block size up to 128 rows, NaN / Inf / zero /
+    # subnormal elements; quantize_mx values and scales, the fake-quant, and
+    # the per-element codes, which decode to the values
+    print(f"middle-axis tiles {xdt} {shape} axis={axis} bs={bs} {dtype}", flush=True)
+    n = math.prod(shape)
+    x = c3_input(1, n, seed=n + bs).reshape(shape).to(xdt)
+    flat = x.view(-1)
+    flat[7], flat[n // 3], flat[n // 2], flat[n - 5] = float("nan"), float("inf"), -0.0, 2.0**-130
+    sq = None if pow2 else oracle_qmap("fp8_e5m3")
+    qm = vqx.get_quantization_map(dtype, "cuda")
+    if isinstance(qm, tuple):  # NormalFloat: (indices, levels), as FakeQuantize combines them
+        qm = qm[1][qm[0]]
+    s, q = Q.quantize_mx(x.cuda(), qm, [axis], bs, qmax, pow2, None if sq is None else sq.cuda(), None)
+    ws, wq = R.quantize_mx(x, oracle_qmap(dtype), [axis], bs, qmax, pow2, sq)
+    assert_bitexact(s.cpu(), ws, "scales")
+    assert_bitexact(q.cpu(), wq, "values")
+    qops = vqx.ops.quantized
+    fmt = vqx.parse_format(dtype)
+    fs, fy = qops.mx_fake_quantize(x.cuda(), fmt, axis, bs, qmax, pow2, None if sq is None else sq.cuda())
+    wfs, wfy = R.mx_fake_quantize(x, oracle_qmap(dtype), [axis], bs, qmax, pow2, sq)
+    assert_bitexact(fs.cpu(), wfs, "fake-quant scales")
+    assert_bitexact(fy.cpu(), wfy, "fake-quant values")
+    # one code per element: the format's decode table maps it to the value
+    xd = x.contiguous().cuda()
+    _, ax, L, inner = vqx.ops.quantized._axis_geometry(list(shape), axis)
+    outer = n // (L * inner)
+    codes = torch.empty(n, dtype=torch.uint8, device="cuda")
+    qv = torch.empty_like(xd)
+    desc = fmt.desc(xd.device)
+    shift = math.floor(math.log2(qmax)) if pow2 else 0
+    vqx._lib.call("vqx_mx_quantize", vqx._lib.ptr(xd), vqx._lib.dtype_tag(xd.dtype), outer, L, inner, bs,
+                  vqx._lib.ctypes.byref(desc), 0 if pow2 else 1, shift, vqx._lib.ctypes.c_float(qmax),
+                  None if sq is None else vqx._lib.ptr(sq.cuda()), None, None, None, vqx._lib.ptr(qv), None,
+                  vqx._lib.ptr(codes), 1, vqx._lib.stream_of(xd))
+    assert_bitexact(qv.cpu(), wq, "values beside the codes")
+    dtab = fmt.tables(xd.device)["decode"]
+    dec = dtab[codes.long() & (dtab.numel() - 1)].float().cpu()  # two's-complement codes: their low bits
+    val = wq.float().reshape(-1)
+    ok = (dec == val) | torch.isnan(val)
+    assert bool(ok.all()), f"{int((~ok).sum())} codes do not decode to their values"

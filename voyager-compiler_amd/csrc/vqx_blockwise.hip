@@ -17,6 +17,7 @@ struct BT;
 
 template <>
 struct BT<uint16_t> {  // bf16 bits
+  static constexpr uint32_t kSign = 0x8000u;
   static constexpr uint32_t kMagMask = 0x7FFFu;
   static constexpr uint32_t kInf = 0x7F80u;
   __device__ static uint32_t bits(const uint16_t* p) { return *p; }
@@ -45,6 +46,7 @@ struct BT<uint16_t> {  // bf16 bits
 
 template <>
 struct BT<float> {
+  static constexpr uint32_t kSign = 0x80000000u;
   static constexpr uint32_t kMagMask = 0x7FFFFFFFu;
   static constexpr uint32_t kInf = 0x7F800000u;
   __device__ static uint32_t bits(const float* p) { return f2u(*p); }
@@ -164,6 +166,13 @@ __device__ __forceinline__ uint32_t div_to_bf16(float x, float s, float rcp, boo
   return q == q ? h : (h & 0x7FFFu) | ((f2u(x) >> 16) & 0x8000u);
 }
 
+// The outlier bound of an input of type T (0xFFFFFFFF when masking is off).
+template <typename T>
+__device__ __forceinline__ uint32_t outlier_bound_t(const OutlierArgs& oa) {
+  if (!oa.active) return 0xFFFFFFFFu;
+  return outlier_bound(oa, [](float f) { return BT<T>::round_bits(f); }, BT<T>::kSign);
+}
+
 // ---------------------------------------------------------------------------
 // packing helpers: element i of a group of 16 at bits [cb*i, cb*i + cb)
 // ---------------------------------------------------------------------------
@@ -212,11 +221,25 @@ __device__ __forceinline__ void store_group_codes(uint8_t* base, int64_t g, cons
 // thread one 16-element group, the LPB threads of a block adjacent in the wave.
 template <typename T, typename Enc, int CB, int LPB>
 __global__ __launch_bounds__(256) void mx_group_kernel(const T* __restrict__ x, int64_t ngroups,
-                                                       ScaleParams sp, Enc enc, MxOut out) {
+                                                       ScaleParams sp, Enc enc, MxOut out, OutlierArgs oa) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const uint32_t bound = outlier_bound_t<T>(oa);
+  uint32_t nskip = 0;
   for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ngroups; g += stride) {
-    uint32_t b[16];
+    uint32_t b[16], xo[16];
     BT<T>::load16(x + g * 16, b);
+    uint32_t skip = 0;
+    if (oa.active) {
+      // outliers: zeros in the block max and the encode, restored below
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        xo[j] = b[j];
+        const bool sk = outlier_skip(b[j] & BT<T>::kMagMask, bound, BT<T>::kInf);
+        skip |= (uint32_t)sk << j;
+        b[j] = sk ? 0u : b[j];
+      }
+      nskip += __builtin_popcount(skip);
+    }
     uint32_t amax = 0;
 #pragma unroll
     for (int j = 0; j < 16; ++j) amax = umax32(amax, b[j] & BT<T>::kMagMask);
@@ -237,6 +260,10 @@ __global__ __launch_bounds__(256) void mx_group_kernel(const T* __restrict__ x, 
       if (std::is_same<T, uint16_t>::value) qv[j] = r.value;
       fv[j] = BT<T>::round_bits(v * s);
     }
+    if (skip) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) fv[j] = (skip >> j) & 1u ? xo[j] : fv[j];
+    }
     if (out.qvals) BT<T>::store16(static_cast<T*>(out.qvals) + g * 16, qv);
     if (out.fq) BT<T>::store16(static_cast<T*>(out.fq) + g * 16, fv);
     if constexpr (CB > 0) store_group_codes<CB>(static_cast<uint8_t*>(out.codes), g, code);
@@ -247,6 +274,7 @@ __global__ __launch_bounds__(256) void mx_group_kernel(const T* __restrict__ x, 
       if (out.scale_e8m0) __builtin_nontemporal_store((uint8_t)e8m0_of(s), out.scale_e8m0 + blk);
     }
   }
+  outlier_tally(nskip, oa);
 }
 
 // General path: x viewed as [outer, L, inner], blocks of bs along L (the last
@@ -255,10 +283,14 @@ __global__ __launch_bounds__(256) void mx_group_kernel(const T* __restrict__ x, 
 template <typename T, typename Enc>
 __global__ __launch_bounds__(256) void mx_block_kernel(const T* __restrict__ x, int64_t outer, int64_t L,
                                                        int64_t inner, int64_t bs, ScaleParams sp, Enc enc,
-                                                       MxOut out, int code_bytes) {
+                                                       MxOut out, int code_bytes, OutlierArgs oa) {
   const int64_t nblk_l = (L + bs - 1) / bs;
   const int64_t total = outer * nblk_l * inner;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const uint32_t bound = outlier_bound_t<T>(oa);
+  // an outlier reads as zero (+0.0 bits), as masked_fill(skip, 0.0) leaves it
+  auto masked = [&](uint32_t b) { return outlier_skip(b & BT<T>::kMagMask, bound, BT<T>::kInf) ? 0u : b; };
+  uint32_t nskip = 0;
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
     // scale tensor index order = [outer, nblk_l, inner]
     int64_t in = t % inner;
@@ -269,20 +301,23 @@ __global__ __launch_bounds__(256) void mx_block_kernel(const T* __restrict__ x, 
     int64_t l1 = l0 + bs < L ? l0 + bs : L;
     const T* base = x + (o * L) * inner + in;
     uint32_t amax = 0;
-    for (int64_t l = l0; l < l1; ++l) amax = umax32(amax, BT<T>::bits(base + l * inner) & BT<T>::kMagMask);
+    for (int64_t l = l0; l < l1; ++l) amax = umax32(amax, masked(BT<T>::bits(base + l * inner)) & BT<T>::kMagMask);
     float s = block_scale<T>(amax, sp);
     uint32_t sb = f2u(s);
     bool pow2 = (sb & 0x7FFFFFu) == 0 && ((sb >> 23) & 0xFF) >= 1 && ((sb >> 23) & 0xFF) <= 253;
     float rcp = pow2 ? u2f((uint32_t)(254 - ((sb >> 23) & 0xFF)) << 23) : 0.0f;
     for (int64_t l = l0; l < l1; ++l) {
       int64_t i = (o * L + l) * inner + in;
-      uint32_t xb = BT<T>::bits(x + i);
+      const uint32_t xo = BT<T>::bits(x + i);
+      const uint32_t xb = masked(xo);
+      const bool sk = xb != xo;
+      nskip += sk ? 1u : 0u;
       uint32_t h = div_to_bf16<T>(BT<T>::val(xb), s, rcp, pow2);
       Result r = enc.encode(h);
       float v = BT<T>::val(BT<T>::round_bits(bf2f(r.value)));
       uint32_t q = std::is_same<T, uint16_t>::value ? r.value : BT<T>::round_bits(v);
       if (out.qvals) BT<T>::put(static_cast<T*>(out.qvals) + i, q);
-      if (out.fq) BT<T>::put(static_cast<T*>(out.fq) + i, BT<T>::round_bits(v * s));
+      if (out.fq) BT<T>::put(static_cast<T*>(out.fq) + i, sk ? xo : BT<T>::round_bits(v * s));
       if (out.codes) {
         if (code_bytes == 1) static_cast<uint8_t*>(out.codes)[i] = (uint8_t)r.code;
         else static_cast<uint16_t*>(out.codes)[i] = (uint16_t)r.code;
@@ -292,6 +327,135 @@ __global__ __launch_bounds__(256) void mx_block_kernel(const T* __restrict__ x, 
     if (out.scale_f32) out.scale_f32[t] = s;
     if (out.scale_e8m0) out.scale_e8m0[t] = (uint8_t)e8m0_of(s);
   }
+  outlier_tally(nskip, oa);
+}
+
+// Blocks along a middle axis (inner > 1, e.g. ax=-2 of an attention operand):
+// x viewed as [outer, L, inner], blocks of bs <= 128 rows along L, inner a
+// multiple of VE = 16 / sizeof(T).  A 256-thread workgroup takes a tile of
+// bs rows x 16 column chunks of VE elements (256 contiguous bytes per row):
+// thread (chunk c = tid % 16, row group g = tid / 16) loads rows g, g + 16,
+// ... of its chunk with 16-byte loads, the per-column block maxima meet in
+// LDS, and each thread encodes its elements from registers and stores them
+// in the layout it loaded.  Rows past L (a short last block, zero-padded in
+// the reference) and chunks past inner are left out.  Same per-element
+// arithmetic and outputs as mx_block_kernel (codes unpacked, 1 or 2 bytes).
+constexpr int kColChunks = 16;
+constexpr int kColRowsMax = 8;  // rows per thread: bs <= 128
+
+template <typename T, typename Enc>
+__global__ __launch_bounds__(256) void mx_cols_kernel(const T* __restrict__ x, int64_t outer, int64_t L,
+                                                      int64_t inner, int bs, ScaleParams sp, Enc enc, MxOut out,
+                                                      int code_bytes, OutlierArgs oa) {
+  constexpr int VE = 16 / sizeof(T);
+  constexpr int TW = kColChunks * VE;  // columns per tile
+  __shared__ uint32_t s_amax[256 / kColChunks][TW];
+  __shared__ float s_scale[TW];
+  const int tid = threadIdx.x, cg = tid % kColChunks, rg = tid / kColChunks;
+  const int64_t nblk = (L + bs - 1) / bs;
+  const int64_t ntc = (inner + TW - 1) / TW;
+  const int64_t ntiles = outer * nblk * ntc;
+  const uint32_t bound = outlier_bound_t<T>(oa);
+  uint32_t nskip = 0;
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t tc = tile % ntc, rest = tile / ntc;
+    const int64_t bl = rest % nblk, o = rest / nblk;
+    const int64_t l0 = bl * bs;
+    const int64_t col = tc * TW + (int64_t)cg * VE;  // first column of this thread's chunk
+    const bool cok = col < inner;
+    uint32_t v[kColRowsMax][VE];  // the input, outliers included
+    uint32_t skip[kColRowsMax];
+    uint32_t m[VE];
+#pragma unroll
+    for (int e = 0; e < VE; ++e) m[e] = 0;
+#pragma unroll
+    for (int i = 0; i < kColRowsMax; ++i) {
+      const int r = rg + 16 * i;
+      const int64_t l = l0 + r;
+      skip[i] = 0;
+      if (r < bs && l < L && cok) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(x + (o * L + l) * inner + col);
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+          const uint32_t b = sizeof(T) == 2 ? ((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) : w[e];
+          v[i][e] = b;
+          const bool sk = outlier_skip(b & BT<T>::kMagMask, bound, BT<T>::kInf);
+          skip[i] |= (uint32_t)sk << e;
+          m[e] = umax32(m[e], sk ? 0u : b & BT<T>::kMagMask);
+        }
+        nskip += __builtin_popcount(skip[i]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < VE; ++e) s_amax[rg][cg * VE + e] = m[e];
+    __syncthreads();
+    if (tid < TW) {
+      uint32_t a = 0;
+#pragma unroll
+      for (int g = 0; g < 256 / kColChunks; ++g) a = umax32(a, s_amax[g][tid]);
+      const float sc = block_scale<T>(a, sp);
+      s_scale[tid] = sc;
+      const int64_t c = tc * TW + tid;
+      if (c < inner) {
+        const int64_t si = (o * nblk + bl) * inner + c;
+        if (out.scale) BT<T>::put(static_cast<T*>(out.scale) + si, BT<T>::round_bits(sc));
+        if (out.scale_f32) out.scale_f32[si] = sc;
+        if (out.scale_e8m0) out.scale_e8m0[si] = (uint8_t)e8m0_of(sc);
+      }
+    }
+    __syncthreads();
+    float s[VE], rcp[VE];
+    bool pw[VE];
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      s[e] = s_scale[cg * VE + e];
+      const uint32_t sb = f2u(s[e]);
+      pw[e] = (sb & 0x7FFFFFu) == 0 && ((sb >> 23) & 0xFF) >= 1 && ((sb >> 23) & 0xFF) <= 253;
+      rcp[e] = pw[e] ? u2f((uint32_t)(254 - ((sb >> 23) & 0xFF)) << 23) : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kColRowsMax; ++i) {
+      const int r = rg + 16 * i;
+      const int64_t l = l0 + r;
+      if (!(r < bs && l < L && cok)) continue;
+      uint32_t qv[VE], fv[VE], cd[VE];
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        const bool sk = (skip[i] >> e) & 1u;  // an outlier: encoded as +0, output unchanged
+        const uint32_t h = div_to_bf16<T>(BT<T>::val(sk ? 0u : v[i][e]), s[e], rcp[e], pw[e]);
+        const Result rr = enc.encode(h);
+        const float val = BT<T>::val(BT<T>::round_bits(bf2f(rr.value)));
+        qv[e] = std::is_same<T, uint16_t>::value ? rr.value : BT<T>::round_bits(val);
+        fv[e] = sk ? v[i][e] : BT<T>::round_bits(val * s[e]);
+        cd[e] = rr.code;
+      }
+      const int64_t base = (o * L + l) * inner + col;
+      auto store = [&](void* p, const uint32_t(&b)[VE]) {
+        u32x4 w;
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = (b[2 * j] & 0xFFFFu) | (b[2 * j + 1] << 16);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = b[j];
+        }
+        *reinterpret_cast<u32x4*>(static_cast<T*>(p) + base) = w;
+      };
+      if (out.qvals) store(out.qvals, qv);
+      if (out.fq) store(out.fq, fv);
+      if (out.codes) {
+        if (code_bytes == 1) {
+#pragma unroll
+          for (int e = 0; e < VE; ++e) static_cast<uint8_t*>(out.codes)[base + e] = (uint8_t)cd[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < VE; ++e) static_cast<uint16_t*>(out.codes)[base + e] = (uint16_t)cd[e];
+        }
+      }
+    }
+    __syncthreads();  // s_amax / s_scale are rewritten by the next tile
+  }
+  outlier_tally(nskip, oa);
 }
 
 // ---------------------------------------------------------------------------
@@ -677,10 +841,16 @@ __device__ __forceinline__ void half_swap(u32x4& a, u32x4& b) {
 // 51.2 -> 49.4; e3m2 unchanged)
 constexpr int kMxLutThreads = 1024;
 
-template <int CB, int LPB, bool ABSMAX, int WANT, bool CT>
+// OUTL: outlier masking (fake-quant output only): elements with |x| at or
+// above the threshold are zeros for the block max and the encode, and the
+// output restores them; the kernel counts them into the device stats.
+template <int CB, int LPB, bool ABSMAX, int WANT, bool CT, bool OUTL = false>
 __global__ __launch_bounds__(kMxLutThreads) void mx_lut_kernel(const uint16_t* __restrict__ x, int64_t ngroups,
-                                                     ScaleParams sp, LutView lv, MxOut out) {
+                                                     ScaleParams sp, LutView lv, MxOut out, OutlierArgs oa) {
   static_assert(!CT || (WANT == 0 && (CB == 4 || CB == 8)), "code tables serve packed 4- or 8-bit codes only");
+  static_assert(!OUTL || (WANT == 2 && CB == 0 && !CT), "outlier masking serves the fake-quant output only");
+  const uint32_t obound = OUTL ? outlier_bound_t<uint16_t>(oa) : 0xFFFFFFFFu;
+  uint32_t nskip = 0;
   extern __shared__ uint32_t lds_lut[];
   __shared__ uint8_t thr8[256];
   const int lane = threadIdx.x & 63;
@@ -723,10 +893,24 @@ __global__ __launch_bounds__(kMxLutThreads) void mx_lut_kernel(const uint16_t* _
   const bool qmax_pow2 = (f2u(sp.quant_max) & 0x807FFFFFu) == 0 && ((f2u(sp.quant_max) >> 23) - 1u) < 253u;
   const float qmax_rcp = u2f((254u - (f2u(sp.quant_max) >> 23)) << 23);
 
-  // One group of 16 consecutive elements (w, as bf16 pairs), group index gl.
+  // One group of 16 consecutive elements (wx, as bf16 pairs), group index gl.
   // SW: a whole chunk in the swapped layout (every lane of the wave active).
-  auto group = [&](auto sw, const uint32_t(&w)[8], int64_t gl) {
+  auto group = [&](auto sw, const uint32_t(&wx)[8], int64_t gl) {
     constexpr bool SW = decltype(sw)::value;
+    // w: the group with its outliers zeroed (OUTL), else the input itself
+    uint32_t w[8];
+    uint32_t skip = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      w[j] = wx[j];
+      if constexpr (OUTL) {
+        const bool lo = outlier_skip(wx[j] & 0x7FFFu, obound, 0x7F80u);
+        const bool hi = outlier_skip((wx[j] >> 16) & 0x7FFFu, obound, 0x7F80u);
+        skip |= ((uint32_t)lo << (2 * j)) | ((uint32_t)hi << (2 * j + 1));
+        w[j] &= (lo ? 0xFFFF0000u : 0xFFFFFFFFu) & (hi ? 0x0000FFFFu : 0xFFFFFFFFu);
+      }
+    }
+    if constexpr (OUTL) nskip += __builtin_popcount(skip);
     u16x2 m2 = {0, 0};  // magnitude maxima of the low and high halves
 #pragma unroll
     for (int j = 0; j < 8; ++j) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, w[j] & 0x7FFF7FFFu));
@@ -831,6 +1015,13 @@ __global__ __launch_bounds__(kMxLutThreads) void mx_lut_kernel(const uint16_t* _
         // pow2 scales on the fast path multiply exactly
         fv[j] = (ABSMAX || !fast) ? f2bf(u2f(v << 16) * s) : (f2u(u2f(v << 16) * s) >> 16);
       }
+      if constexpr (OUTL) {
+        if (skip) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            fv[j] = (skip >> j) & 1u ? ((j & 1) ? wx[j >> 1] >> 16 : wx[j >> 1] & 0xFFFFu) : fv[j];
+        }
+      }
       auto store = [&](uint16_t* base, const uint32_t(&b)[16]) {
         if constexpr (SW) {
           u32x4 a0 = {b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
@@ -889,6 +1080,7 @@ __global__ __launch_bounds__(kMxLutThreads) void mx_lut_kernel(const uint16_t* _
     const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     group(std::false_type{}, w, g);
   }
+  if constexpr (OUTL) outlier_tally(nskip, oa);
 }
 
 template <int CB, int LPB, bool ABSMAX, int WANT>
@@ -905,14 +1097,25 @@ static int launch_lut_k(const uint16_t* x, int64_t ngroups, const ScaleParams& s
     // against 36.7 at full occupancy; every other form of this kernel is
     // fastest at full occupancy)
     if (CB == 8 && grid > (unsigned)num_cus()) grid = (unsigned)num_cus();
-    hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out, OutlierArgs{});
   } else {
     auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT, false>;
     size_t lds = sizeof(uint32_t) * 2 * lv.len;
     unsigned grid = persistent_grid((const void*)k, bs, lds, ngroups);
-    hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out, OutlierArgs{});
   }
   return check_launch("mx_quantize(lut)");
+}
+
+// The fake-quant output with outlier masking (mx_lut_kernel's OUTL form).
+template <int LPB, bool ABSMAX>
+static int launch_lut_outlier(const uint16_t* x, int64_t ngroups, const ScaleParams& sp, const LutView& lv,
+                              const MxOut& out, const OutlierArgs& oa, hipStream_t st) {
+  auto k = mx_lut_kernel<0, LPB, ABSMAX, 2, false, true>;
+  const size_t lds = sizeof(uint32_t) * 2 * lv.len;
+  const unsigned grid = persistent_grid((const void*)k, kMxLutThreads, lds, ngroups);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(kMxLutThreads), lds, st, x, ngroups, sp, lv, out, oa);
+  return check_launch("mx_quantize(lut, outliers)");
 }
 
 template <int CB, int LPB, bool ABSMAX>
@@ -957,7 +1160,7 @@ static int launch_lut(const uint16_t* x, int64_t n, int lpb, int cb, const Scale
 
 template <typename T, typename Enc, int CB>
 static int launch_group(const T* x, int64_t n, int lpb, const ScaleParams& sp, const Enc& enc,
-                        const MxOut& out, hipStream_t st) {
+                        const MxOut& out, hipStream_t st, const OutlierArgs& oa = OutlierArgs{}) {
   int64_t ngroups = n / 16;
   const int bs = 256;
   unsigned grid = grid_for(ngroups, bs);
@@ -965,7 +1168,7 @@ static int launch_group(const T* x, int64_t n, int lpb, const ScaleParams& sp, c
 #define VQX_LPB(L)                                                                                 \
   case L:                                                                                          \
     hipLaunchKernelGGL((mx_group_kernel<T, Enc, CB, L>), dim3(grid), dim3(bs), 0, st, x, ngroups, \
-                       sp, enc, out);                                                              \
+                       sp, enc, out, oa);                                                          \
     break;
     VQX_LPB(1)
     VQX_LPB(2)
@@ -981,7 +1184,7 @@ static int launch_group(const T* x, int64_t n, int lpb, const ScaleParams& sp, c
 template <typename T, typename Enc>
 static int mx_quantize_t(const T* x, int64_t outer, int64_t L, int64_t inner, int64_t bs,
                          const ScaleParams& sp, const Enc& enc, const MxOut& out, int code_layout,
-                         int code_bits, hipStream_t st) {
+                         int code_bits, hipStream_t st, const OutlierArgs& oa) {
   int64_t n = outer * L * inner;
   if (n == 0) return kOk;
   int64_t lpb = bs / 16;
@@ -1008,19 +1211,31 @@ static int mx_quantize_t(const T* x, int64_t outer, int64_t L, int64_t inner, in
       }
     }
   }
-  if (fast && !out.codes) return launch_group<T, Enc, 0>(x, n, (int)lpb, sp, enc, out, st);
+  if (fast && !out.codes) return launch_group<T, Enc, 0>(x, n, (int)lpb, sp, enc, out, st, oa);
   if (out.codes && code_layout != 1 && code_layout != 2)
     return set_error(kErrInvalid, "unpacked code layout must be 1 or 2 bytes");
+  constexpr int VE = 16 / sizeof(T);
+  if (inner > 1 && inner % VE == 0 && bs <= 16 * kColRowsMax && aligned(x, 16) &&
+      (!out.qvals || aligned(out.qvals, 16)) && (!out.fq || aligned(out.fq, 16))) {
+    const int64_t tiles = outer * ((L + bs - 1) / bs) * ((inner + kColChunks * VE - 1) / (kColChunks * VE));
+    const unsigned grid = persistent_grid((const void*)mx_cols_kernel<T, Enc>, 256, 0, tiles * 256);
+    hipLaunchKernelGGL((mx_cols_kernel<T, Enc>), dim3(grid), dim3(256), 0, st, x, outer, L, inner, (int)bs, sp,
+                       enc, out, code_layout, oa);
+    return check_launch("mx_quantize(cols)");
+  }
   int64_t nblocks = outer * ((L + bs - 1) / bs) * inner;
   unsigned grid = grid_for(nblocks, 256);
   hipLaunchKernelGGL((mx_block_kernel<T, Enc>), dim3(grid), dim3(256), 0, st, x, outer, L, inner, bs, sp,
-                     enc, out, code_layout);
+                     enc, out, code_layout, oa);
   return check_launch("mx_quantize");
 }
 
 int mx_quantize(const void* x, int dtype, int64_t outer, int64_t L, int64_t inner, int64_t bs,
                 const FormatDesc& fmt, const ScaleParams& sp, const MxOut& out, int code_layout,
-                hipStream_t st) {
+                hipStream_t st, const OutlierArgs* oap) {
+  const OutlierArgs oa = oap ? *oap : OutlierArgs{};
+  if (oa.active && (out.qvals || out.codes || out.scale_e8m0))
+    return set_error(kErrInvalid, "mx_quantize: outlier masking writes the fake-quant values and scales only");
   if (outer < 0 || L < 0 || inner < 1 || bs < 1)
     return set_error(kErrInvalid, "bad block geometry outer=%lld L=%lld inner=%lld bs=%lld",
                      (long long)outer, (long long)L, (long long)inner, (long long)bs);
@@ -1036,6 +1251,22 @@ int mx_quantize(const void* x, int dtype, int64_t outer, int64_t L, int64_t inne
                 (!out.qvals || aligned(out.qvals, 16)) && (!out.fq || aligned(out.fq, 16)) &&
                 (!out.codes || aligned(out.codes, 16)) && (!out.codes || packed);
     if (n == 0) return kOk;
+    if (fast && oa.active) {
+      if (!out.fq) return set_error(kErrInvalid, "mx_quantize: outlier masking needs the fake-quant output");
+      LutView lv{fmt.lut, fmt.lut_len};
+      const int64_t ng = n / 16;
+      const bool am = sp.mode == 1;
+      switch (lpb) {
+        case 1: return am ? launch_lut_outlier<1, true>((const uint16_t*)x, ng, sp, lv, out, oa, st)
+                          : launch_lut_outlier<1, false>((const uint16_t*)x, ng, sp, lv, out, oa, st);
+        case 2: return am ? launch_lut_outlier<2, true>((const uint16_t*)x, ng, sp, lv, out, oa, st)
+                          : launch_lut_outlier<2, false>((const uint16_t*)x, ng, sp, lv, out, oa, st);
+        case 4: return am ? launch_lut_outlier<4, true>((const uint16_t*)x, ng, sp, lv, out, oa, st)
+                          : launch_lut_outlier<4, false>((const uint16_t*)x, ng, sp, lv, out, oa, st);
+        default: return am ? launch_lut_outlier<8, true>((const uint16_t*)x, ng, sp, lv, out, oa, st)
+                           : launch_lut_outlier<8, false>((const uint16_t*)x, ng, sp, lv, out, oa, st);
+      }
+    }
     if (fast) {
       LutView lv{fmt.lut, fmt.lut_len};
       return launch_lut((const uint16_t*)x, n, (int)lpb, packed ? fmt.code_bits : 0, sp, lv, out, st);
@@ -1045,10 +1276,10 @@ int mx_quantize(const void* x, int dtype, int64_t outer, int64_t L, int64_t inne
     using E = decltype(enc);
     if (dtype == kBF16)
       return mx_quantize_t<uint16_t, E>((const uint16_t*)x, outer, L, inner, bs, sp, enc, out,
-                                        code_layout, fmt.code_bits, st);
+                                        code_layout, fmt.code_bits, st, oa);
     if (dtype == kF32)
       return mx_quantize_t<float, E>((const float*)x, outer, L, inner, bs, sp, enc, out, code_layout,
-                                     fmt.code_bits, st);
+                                     fmt.code_bits, st, oa);
     return set_error(kErrInvalid, "blockwise input dtype %d not supported (float32, bfloat16)", dtype);
   });
 }

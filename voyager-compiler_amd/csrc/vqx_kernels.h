@@ -42,6 +42,82 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// FakeQuantize outlier masking (quantization/fake_quantize.py:373-395): the
+// elements with |x| >= threshold are left out of the quantization (zeroed
+// before it, so they drop out of block maxima) and come back unchanged after
+// it; the largest skipped fraction seen so far is kept on the device.
+// ---------------------------------------------------------------------------
+// Device state of the skipped-element count (32 bytes, zero-initialised once
+// by the caller; every launch leaves `tally` at zero again).
+struct OutlierStats {
+  unsigned long long tally;  // the running launch: finished workgroups << 40 | skipped elements
+  unsigned long long pad;
+  unsigned long long best;   // the largest count / numel so far, fp64 bits
+  unsigned long long reserved;
+};
+constexpr int kTallyShift = 40;  // up to 2^40 - 1 elements per launch, 2^24 - 1 workgroups
+
+struct OutlierArgs {
+  int32_t active;        // 0: no masking (the other fields unused)
+  const float* thr_dev;  // the threshold in device memory (fp32), or null: thr_host
+  float thr_host;
+  OutlierStats* stats;   // null: nothing counted
+  int64_t numel;         // the fraction's denominator (the whole tensor)
+};
+
+// The threshold as a bound on the magnitude bits of x's dtype: |x| >= t is
+// compared in x's dtype, so t rounds (RNE) to it first, as torch casts the
+// fp32 threshold (or the Python float) to the tensor's dtype.  A NaN t skips
+// nothing (0xFFFFFFFF), a t at or below -0 every non-NaN element (0).
+// round_bits: fp32 -> the dtype's bits; sign: the dtype's sign bit.
+template <typename F>
+__device__ __forceinline__ uint32_t outlier_bound(const OutlierArgs& oa, F round_bits, uint32_t sign) {
+  const float t = oa.thr_dev ? *oa.thr_dev : oa.thr_host;
+  if (t != t) return 0xFFFFFFFFu;
+  const uint32_t tb = round_bits(t);
+  return (tb & sign) ? 0u : tb;
+}
+
+// Whether an element of magnitude bits mag (NaN: above inf) is an outlier.
+__device__ __forceinline__ bool outlier_skip(uint32_t mag, uint32_t bound, uint32_t inf) {
+  return mag >= bound && mag <= inf;
+}
+
+// End of an outlier-masking launch: the workgroup's skipped elements (cnt per
+// thread) join the launch's count, and the last workgroup to finish folds
+// count / numel into the largest fraction and clears the tally for the next
+// launch.  Every thread of every workgroup calls it once.  Each workgroup
+// adds its count and its arrival in one device-scope atomic (coherent across
+// the XCDs' L2s at the access), so the workgroup that brings the arrivals to
+// the grid size reads the whole count in the value it gets back.
+__device__ __forceinline__ void outlier_tally(uint32_t cnt, const OutlierArgs& oa) {
+  if (!oa.stats) return;
+  __shared__ unsigned long long s_tot;
+  if (threadIdx.x == 0) s_tot = 0;
+  __syncthreads();
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) cnt += (uint32_t)__shfl_xor((int)cnt, o, 64);
+  if ((threadIdx.x & 63) == 0 && cnt) atomicAdd(&s_tot, (unsigned long long)cnt);
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  OutlierStats* st = oa.stats;
+  const unsigned long long add = (1ull << kTallyShift) + s_tot;
+  const unsigned long long prev = __hip_atomic_fetch_add(&st->tally, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long grid = (unsigned long long)gridDim.x * gridDim.y * gridDim.z;
+  if ((prev >> kTallyShift) != grid - 1) return;
+  const unsigned long long c = (prev + add) & ((1ull << kTallyShift) - 1);
+  __hip_atomic_store(&st->tally, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Python's count / numel: both below 2^53, so the fp64 division is the
+  // correctly rounded quotient Python's int / int gives
+  const double f = (double)c / (double)oa.numel;
+  const double b = __builtin_bit_cast(double, __hip_atomic_load(&st->best, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT));
+  if (f > b)
+    __hip_atomic_store(&st->best, __builtin_bit_cast(unsigned long long, f), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct MxOut {
   void* scale;          // input dtype [blocks]
   float* scale_f32;     // [blocks]
@@ -76,9 +152,11 @@ int level_tables(const float* levels, int K, int mode, uint8_t* index_table, flo
                  uint32_t* work, int* bad, hipStream_t st);
 
 // vqx_blockwise.hip
+// oa: optional outlier masking (the fake-quant output restores the skipped
+// elements; they count as zeros in the block maxima and the other outputs)
 int mx_quantize(const void* x, int dtype, int64_t outer, int64_t L, int64_t inner, int64_t bs,
                 const FormatDesc& fmt, const ScaleParams& sp, const MxOut& out, int code_layout,
-                hipStream_t st);
+                hipStream_t st, const OutlierArgs* oa = nullptr);
 int mx_decode(const uint8_t* codes, int code_bits, const uint16_t* decode_table, int ntab,
               const void* scale, int scale_kind, int64_t n, int64_t bs, void* out, int out_dtype,
               hipStream_t st);
@@ -153,6 +231,13 @@ int csr_slice(const void* data, int dtype, const int32_t* indices, const int32_t
               int32_t* indices_out, int32_t* indptr_out, hipStream_t st);
 int csr_decode(const CsrDecode& d, hipStream_t st);
 int spmm_csr(const SpmmArgs& a, hipStream_t st);
+
+// vqx_outlier_fq.hip
+int64_t outlier_topk_workspace_bytes();
+int outlier_topk_threshold(const void* x, int dtype, int64_t n, int64_t k, int ema, float decay, float omd,
+                           float* thr, void* workspace, int64_t workspace_bytes, hipStream_t st);
+int outlier_mask(const void* x, int dtype, int64_t n, const OutlierArgs& oa, void* masked, hipStream_t st);
+int outlier_restore(const void* x, int dtype, int64_t n, const OutlierArgs& oa, void* y, hipStream_t st);
 
 // vqx_calib.hip
 constexpr int kHistMaxBins = 4096;

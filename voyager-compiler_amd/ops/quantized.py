@@ -407,12 +407,119 @@ def quantize_mx(input, qmap, axes, block_size, quant_max, force_scale_power_of_t
     return scale, qv
 
 
-def mx_fake_quantize(input, fmt: Format, axis, block_size, quant_max, force_pow2, scale_qmap=None):
+def mx_fake_quantize(input, fmt: Format, axis, block_size, quant_max, force_pow2, scale_qmap=None,
+                     scale_f32=None):
     """MXFakeQuantizeFunction.forward's numerics (fake_quantize.py:143-153):
-    (scale, quantize_mx values * expand(scale)) in one pass."""
+    (scale, quantize_mx values * expand(scale)) in one pass.  With scale_f32
+    (a contiguous fp32 tensor of the scale shape) the scale is written there
+    and returned as it, instead of a new tensor in x's dtype."""
+    if scale_f32 is not None:
+        _, _, fq = _mx_call(input, axis, block_size, quant_max, force_pow2, scale_qmap,
+                            fmt.desc(input.device), want_scale=False, want_fq=True, scale_f32=scale_f32)
+        return scale_f32, fq
     scale, _, fq = _mx_call(input, axis, block_size, quant_max, force_pow2, scale_qmap,
                             fmt.desc(input.device), want_fq=True)
     return scale, fq
+
+
+def mx_scale_shape(shape, axis, block_size):
+    """The block-scale shape of an MX quantization of `shape` along `axis`."""
+    axis, _, L, _ = _axis_geometry(list(shape), axis)
+    sshape = list(shape)
+    sshape[axis] = -(-L // block_size)
+    return sshape
+
+
+def mx_fake_quantize_outlier(input, desc, axis, block_size, quant_max, force_pow2, scale_qmap, threshold, stats,
+                             scale_f32=None):
+    """FakeQuantize's outlier masking around MXFakeQuantizeFunction.forward
+    (fake_quantize.py:388-395 around :397-408) in one pass: the elements with
+    |x| >= threshold (a float, or an fp32 device tensor) are zeros for the
+    block scales and the fake-quant, come back unchanged in the output, and
+    are counted into stats (32 bytes of device memory, see
+    vqx_mx_fake_quant_outlier).  Returns (scale, output): the scale in x's
+    dtype, or written into scale_f32 (a contiguous fp32 tensor of the scale
+    shape) and returned as it."""
+    if input.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"vqx: block scales are computed for bfloat16/float32 inputs, not {input.dtype}")
+    if block_size <= 0:
+        raise AssertionError("block_size must be positive")
+    x = input.contiguous()
+    axis, outer, L, inner = _axis_geometry(list(x.shape), axis)
+    sshape = mx_scale_shape(x.shape, axis, block_size)
+    scale = torch.empty(sshape, dtype=x.dtype, device=x.device) if scale_f32 is None else None
+    y = torch.empty_like(x)
+    sq = _table_bf16(scale_qmap.to(x.device)) if (scale_qmap is not None and not force_pow2) else None
+    shift = math.floor(math.log2(quant_max)) if force_pow2 else 0
+    thr_dev, thr = _threshold_args(threshold, x.device)
+    _lib.call("vqx_mx_fake_quant_outlier", _lib.ptr(x), _lib.dtype_tag(x.dtype), outer, L, inner, block_size,
+              _lib.ctypes.byref(desc), 0 if force_pow2 else 1, shift, float(quant_max), _lib.ptr(sq), thr_dev, thr,
+              _lib.ptr(stats), _lib.ptr(scale), _lib.ptr(scale_f32), _lib.ptr(y), _lib.stream_of(x))
+    return (scale if scale_f32 is None else scale_f32), y
+
+
+def _threshold_args(threshold, device):
+    """(device pointer or None, host float) of an outlier threshold: a tensor
+    is read on the device (its fp32 value), a number passes by value."""
+    if isinstance(threshold, torch.Tensor):
+        if threshold.dtype != torch.float32 or threshold.numel() != 1 or threshold.device != device:
+            raise ValueError("vqx: an outlier threshold tensor must be one fp32 value on the input's device")
+        return _lib.ptr(threshold), 0.0
+    return None, float(threshold)
+
+
+def outlier_mask(input, threshold, stats, masked=True):
+    """x.masked_fill(|x| >= threshold, 0) (fake_quantize.py:388-391), with the
+    outliers counted into stats; masked=False only counts (returns None)."""
+    x = input.contiguous()
+    out = torch.empty_like(x) if masked else None
+    thr_dev, thr = _threshold_args(threshold, x.device)
+    _lib.call("vqx_outlier_mask", _lib.ptr(x), _lib.dtype_tag(x.dtype), x.numel(), thr_dev, thr, _lib.ptr(stats),
+              _lib.ptr(out), _lib.stream_of(x))
+    return out
+
+
+def outlier_restore_(input, threshold, y):
+    """y = torch.where(|x| >= threshold, x, y) in place (fake_quantize.py:
+    429-430); y contiguous, shaped and typed like x."""
+    x = input.contiguous()
+    if y.shape != x.shape or y.dtype != x.dtype or not y.is_contiguous():
+        raise ValueError("vqx: outlier restore needs a contiguous output shaped and typed like the input")
+    thr_dev, thr = _threshold_args(threshold, x.device)
+    _lib.call("vqx_outlier_restore", _lib.ptr(x), _lib.dtype_tag(x.dtype), x.numel(), thr_dev, thr, _lib.ptr(y),
+              _lib.stream_of(x))
+    return y
+
+
+_TOPK_WS_BYTES = None
+
+
+def outlier_topk_threshold_(input, outlier_pct, threshold, ema, decay, workspace):
+    """The outlier_pct threshold (fake_quantize.py:373-387) on the device:
+    the k-th largest |x| (k = max(1, ceil(outlier_pct * numel)); NaN when x
+    holds a NaN) stored into threshold (ema False) or folded into it as
+    threshold * decay + value * (1 - decay) (ema True).  threshold: one fp32
+    value on x's device; workspace: outlier_topk_workspace(device)."""
+    x = input.contiguous()
+    n = x.numel()
+    k = max(1, math.ceil(outlier_pct * n))
+    if k > n:
+        raise RuntimeError(f"selected index k out of range: k = {k} for {n} elements (outlier_pct {outlier_pct})")
+    _threshold_args(threshold, x.device)
+    _lib.call("vqx_outlier_topk_threshold", _lib.ptr(x), _lib.dtype_tag(x.dtype), n, k, 1 if ema else 0,
+              float(decay), float(1.0 - decay), _lib.ptr(threshold), _lib.ptr(workspace), workspace.numel(),
+              _lib.stream_of(x))
+
+
+def outlier_topk_workspace(device):
+    """Zeroed device memory for outlier_topk_threshold_ (each call leaves it
+    ready for the next; calls that share one must be ordered)."""
+    global _TOPK_WS_BYTES
+    if _TOPK_WS_BYTES is None:
+        n = ctypes.c_int64(0)
+        _lib.call("vqx_outlier_topk_workspace_size", ctypes.byref(n))
+        _TOPK_WS_BYTES = n.value
+    return torch.zeros(_TOPK_WS_BYTES, dtype=torch.uint8, device=device)
 
 
 def gwa_fake_quantize(input, axis, block_size, quant_min, quant_max, scale_qmap=None):

@@ -16,11 +16,18 @@ kernels:
 * group-wise affine: one fused pass over each block's min / max, scale, zero
   point and the affine fake-quant (``gwa_fake_quantize``).
 
+Outliers (``outlier_pct`` / ``outlier_threshold``, fake_quantize.py:373-395)
+stay on the device: the share's threshold and its running average come from
+a radix select over |x| (``vqx_outlier_topk_threshold``); microscaling masks,
+fake-quantizes, restores and counts in one pass
+(``vqx_mx_fake_quant_outlier``); the other schemes run between a mask and a
+restore pass.  The largest outlier fraction is kept on the device and read
+when ``max_outlier_pct`` is.
+
 Every autograd function passes gradients straight through to the input.
 """
 
 import logging
-import math
 from typing import Optional
 
 import torch
@@ -36,6 +43,7 @@ __all__ = [
     "MXFakeQuantizeFunction",
     "GroupWiseAffineFakeQuantFunction",
     "ObservedFakeQuantizeFunction",
+    "OutlierFakeQuantizeFunction",
     "FusedAmaxObsFakeQuantize",
     "_DerivedObserverOrFakeQuantize",
     "get_quantization_map",
@@ -77,6 +85,15 @@ class FakeQuantizeFunction(torch.autograd.Function):
         return (grad_output,) + (None,) * 4
 
 
+def _direct_scale(scale, input, axis, block_size):
+    """The scale buffer resized to the block-scale shape, when the kernel can
+    write it in place (fp32, on the input's device), else None."""
+    if scale.dtype != torch.float32 or scale.device != input.device:
+        return None
+    scale.resize_(qops.mx_scale_shape(input.shape, axis, block_size))
+    return scale if scale.is_contiguous() else None
+
+
 class MXFakeQuantizeFunction(torch.autograd.Function):
     """Microscaling fake-quant: block scales from the block amax, quantize,
     multiply back, all in one kernel pass; straight-through gradient."""
@@ -87,15 +104,20 @@ class MXFakeQuantizeFunction(torch.autograd.Function):
         if not fake_quant_enabled:
             return input
         axis = qops._single_axis(axes)
+        # scale.resize_(sf.shape).copy_(sf) (:152): an fp32 buffer on the
+        # input's device takes the kernel's fp32 scale output directly
+        direct = _direct_scale(scale, input, axis, block_size)
         if fmt is not None:
             sf, y = qops.mx_fake_quantize(input, fmt, axis, block_size, quant_max,
-                                          force_scale_power_of_two, scale_qmap)
+                                          force_scale_power_of_two, scale_qmap, scale_f32=direct)
         else:
             desc, keep = qops._table_desc(qmap.to(input.device), input.device)
             sf, _, y = qops._mx_call(input, axis, block_size, quant_max, force_scale_power_of_two,
-                                     scale_qmap, desc, want_fq=True)
+                                     scale_qmap, desc, want_scale=direct is None, want_fq=True, scale_f32=direct)
+            sf = direct if direct is not None else sf
             del keep
-        scale.resize_(sf.shape).copy_(sf)
+        if direct is None:
+            scale.resize_(sf.shape).copy_(sf)
         return y
 
     @staticmethod
@@ -139,6 +161,22 @@ class GroupWiseAffineFakeQuantFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output):
         return (grad_output,) + (None,) * 8
+
+
+class OutlierFakeQuantizeFunction(torch.autograd.Function):
+    """FusedAmaxObsFakeQuantize.forward with outliers (fake_quantize.py:
+    388-432): the outliers are masked out, the rest fake-quantized by the
+    module's scheme, the outliers put back; the whole composite passes the
+    gradient straight through (masked_fill's and where's gradients add up to
+    the identity around the straight-through fake-quant)."""
+
+    @staticmethod
+    def forward(ctx, input, module, fake_quant_enabled, fmt=None):
+        return module._outlier_forward(input, fake_quant_enabled, fmt)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        return (grad_output,) + (None,) * 3
 
 
 class _BufferFlags:
@@ -208,7 +246,8 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
             self.register_buffer("histogram", torch.zeros(254, **fk), persistent=False)
         self.observer_enabled[0] = self.qscheme is not None
         self._max_outlier_host = 0.0
-        self._outlier_frac = None
+        self._outlier_stats = None
+        self._topk_ws = None
         self.is_per_channel = self.qscheme == QScheme.PER_CHANNEL_SYMMETRIC
         if outlier_pct is not None:
             self.outlier_ema_decay = kwargs.get("outlier_ema_decay", 0.9)
@@ -259,30 +298,89 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
         return self._qmap_sig == (self.qmap.data_ptr(), _lib.version_of(self.qmap))
 
     # max_outlier_pct: the largest fraction of outliers seen so far
-    # (fake_quantize.py:389-391).  The device keeps the (count, numel) pair of
-    # the largest fraction, compared exactly in int64, and the host divides
-    # only when the value is read (convert reads it), so the forward does not
-    # synchronise and the value is Python's count / numel, as in the reference.
+    # (fake_quantize.py:389-391).  The device keeps it (count / numel in fp64,
+    # as Python divides) in a 32-byte stats buffer the kernels update, so the
+    # forward does not synchronise; the host reads it when the value is read
+    # (convert reads it).
     @property
     def max_outlier_pct(self):
-        if self._outlier_frac is not None:
-            c, n = self._outlier_frac.tolist()
-            return max(self._max_outlier_host, c / n)
-        return self._max_outlier_host
+        st = self._outlier_stats
+        dev = 0.0 if st is None else float(st.view(torch.float64)[2].item())
+        return max(self._max_outlier_host, dev)
 
     @max_outlier_pct.setter
     def max_outlier_pct(self, value):
         self._max_outlier_host = float(value)
-        self._outlier_frac = None
+        if self._outlier_stats is not None:
+            self._outlier_stats.zero_()
 
-    def _fold_outlier_count(self, skip):
-        cnt = skip.sum()
-        cur = torch.stack([cnt, torch.full_like(cnt, skip.numel())])
-        if self._outlier_frac is None:
-            self._outlier_frac = cur
+    def _stats_on(self, device):
+        """The outlier stats buffer on `device` (a move folds the old one's
+        fraction into the host value)."""
+        st = self._outlier_stats
+        if st is not None and st.device != device:
+            self._max_outlier_host = self.max_outlier_pct
+            st = None
+        if st is None:
+            st = torch.zeros(4, dtype=torch.int64, device=device)
+            self._outlier_stats = st
+        return st
+
+    @torch.no_grad()
+    def _update_outlier_threshold(self, x):
+        """The outlier_pct threshold (fake_quantize.py:373-387): the top-k
+        minimum of |x|, copied into outlier_threshold on the first call and
+        folded in with the running average after."""
+        first = self.outlier_threshold.numel() == 0
+        if first:
+            self.outlier_threshold.resize_(())
+        t = self.outlier_threshold
+        if t.dtype != torch.float32 or t.device != x.device:
+            raise RuntimeError("FusedAmaxObsFakeQuantize: outlier_threshold must be float32 on the input's device")
+        if self._topk_ws is None or self._topk_ws.device != x.device:
+            self._topk_ws = qops.outlier_topk_workspace(x.device)
+        qops.outlier_topk_threshold_(x, self.outlier_pct, t, not first, self.outlier_ema_decay, self._topk_ws)
+
+    @torch.no_grad()
+    def _outlier_forward(self, x, fake_quant, fmt):
+        """fake_quantize.py:388-432 on the device: returns the output."""
+        thr = self.outlier_threshold
+        stats = self._stats_on(x.device)
+        xc = x.contiguous()
+        if self.qscheme == QScheme.MICROSCALING and x.dtype in (torch.bfloat16, torch.float32):
+            if not fake_quant:  # MXFakeQuantizeFunction returns its input: only the count
+                qops.outlier_mask(xc, thr, stats, masked=False)
+                return x
+            if fmt is not None:
+                desc, keep = fmt.desc(xc.device), None
+            else:
+                desc, keep = qops._table_desc(self.qmap.to(xc.device), xc.device)
+            axis = qops._single_axis(self.ch_axis)
+            direct = _direct_scale(self.scale, xc, axis, self.block_size)
+            sf, y = qops.mx_fake_quantize_outlier(xc, desc, axis, self.block_size, self.quant_max,
+                                                  self.force_scale_power_of_two, self.scale_qmap, thr, stats,
+                                                  scale_f32=direct)
+            del keep
+            if direct is None:
+                self.scale.resize_(sf.shape).copy_(sf)
+            return y
+        xm = qops.outlier_mask(xc, thr, stats)
+        if self.qscheme == QScheme.MICROSCALING:
+            y = MXFakeQuantizeFunction.forward(None, xm, fake_quant, self.scale, self.qmap, self.ch_axis,
+                                               self.block_size, self.quant_max, self.force_scale_power_of_two,
+                                               self.scale_qmap, fmt)
+        elif self.qscheme == QScheme.GROUP_WISE_AFFINE:
+            y = GroupWiseAffineFakeQuantFunction.forward(None, xm, fake_quant, self.scale, self.zero_point,
+                                                         self.ch_axis, self.block_size, self.quant_min,
+                                                         self.quant_max, self.scale_qmap)
+        elif self._observer_on():
+            y = self._observe_fake_quant(xm, fake_quant, fmt)
+            y = xm if y is None else y
         else:
-            best = self._outlier_frac
-            self._outlier_frac = torch.where(cur[0] * best[1] > best[0] * cur[1], cur, best)
+            y = FakeQuantizeFunction.forward(None, xm, fake_quant, self.qmap, self.scale, fmt)
+        if not y.is_contiguous() or y.data_ptr() == xc.data_ptr():
+            y = y.contiguous() if y.data_ptr() != xc.data_ptr() else y.clone()
+        return qops.outlier_restore_(xc, thr, y).view(x.shape)
 
     # -- observer -----------------------------------------------------------
     def _channel_geometry(self, x):
@@ -348,25 +446,12 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
             self.histogram += torch.histc(exp, 254, min=-126, max=127)
 
         if self.outlier_pct is not None and self._observer_on():
-            flat = x.abs().flatten()
-            k = max(1, math.ceil(self.outlier_pct * flat.numel()))
-            threshold = torch.topk(flat, k, largest=True, sorted=False).values.min()
-            if self.outlier_threshold.numel() == 0:
-                self.outlier_threshold.resize_as_(threshold)
-                self.outlier_threshold.copy_(threshold)
-            else:
-                self.outlier_threshold.mul_(self.outlier_ema_decay).add_(
-                    threshold * (1.0 - self.outlier_ema_decay))
-
-        skip = None
-        if self.outlier_threshold is not None:
-            skip = x.abs() >= self.outlier_threshold
-            orig_x = x
-            x = x.masked_fill(skip, 0.0)
-            self._fold_outlier_count(skip)
+            self._update_outlier_threshold(x)
 
         fmt = self._fmt if self._closed_form() else None
         fq_on = self._fake_quant_on()
+        if self.outlier_threshold is not None:
+            return OutlierFakeQuantizeFunction.apply(x, self, fq_on, fmt)
         if self.qscheme == QScheme.MICROSCALING:
             x = MXFakeQuantizeFunction.apply(x, fq_on, self.scale, self.qmap, self.ch_axis,
                                              self.block_size, self.quant_max,
@@ -379,9 +464,6 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
             x = ObservedFakeQuantizeFunction.apply(x, fq_on, self, fmt)
         else:
             x = FakeQuantizeFunction.apply(x, fq_on, self.qmap, self.scale, fmt)
-
-        if skip is not None:
-            x = torch.where(skip, orig_x, x)
         return x
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
