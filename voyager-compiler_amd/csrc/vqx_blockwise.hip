@@ -861,11 +861,12 @@ __global__ __launch_bounds__(kMxLutThreads) void mx_lut_kernel(const uint16_t* _
   const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x / 64);
   int64_t c = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6)));
   const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-  // input loads: plain for the power-of-two (MX) forms, non-temporal for the
-  // absmax forms (three alternating rounds on one box: C3 e4m3 36.5 -> 34.1,
-  // e3m2 34.0 -> 31.1, e2m1 31.1 -> 29.5, fake-quant 50.1 -> 44.5 us with
-  // plain loads; C2's absmax NF4 encode 20.3 -> 20.5 us, so it keeps them)
-  auto ld_x = [](const u32x4* p) { return ABSMAX ? ld_nt(p) : *p; };
+  // input loads non-temporal: with the input streaming from HBM (inputs
+  // larger than the MALL, or not left there by the launch before) they are
+  // faster than plain loads (C3 e4m3 38.5 -> 36.9, e3m2 35.4 -> 33.9, e2m1
+  // 33.6 -> 32.1, fake-quant 51.5 -> 50.6 us); plain loads win only when the
+  // same input is re-read from the MALL back to back
+  auto ld_x = [](const u32x4* p) { return ld_nt(p); };
   const uint32_t slot = half_slot(lane);
   // the first chunk's loads are in flight while the tables fill LDS
   u32x4 n0 = {0, 0, 0, 0}, n1 = {0, 0, 0, 0};
@@ -1056,11 +1057,13 @@ __global__ __launch_bounds__(kMxLutThreads) void mx_lut_kernel(const uint16_t* _
     }
     if ((gl & (LPB - 1)) == 0) {
       int64_t blk = gl / LPB;
-      // non-temporal like the codes: a plain store of these scattered
-      // scale words costs about a tenth of the kernel's time at C2's size
-      if (out.scale) __builtin_nontemporal_store((uint16_t)f2bf(s), static_cast<uint16_t*>(out.scale) + blk);
-      if (out.scale_f32) __builtin_nontemporal_store(s, out.scale_f32 + blk);
-      if (out.scale_e8m0) __builtin_nontemporal_store((uint8_t)e8m0_of(s), out.scale_e8m0 + blk);
+      // plain stores: a chunk's scales are 32-64 contiguous bytes, and the
+      // L2 merges the neighbouring chunks' pieces into whole lines before
+      // they reach HBM (non-temporal stores sent each piece on its own:
+      // C3 e4m3 36.9 -> 35.8, fake-quant 50.6 -> 49.4, C2 22.6 -> 22.1 us)
+      if (out.scale) static_cast<uint16_t*>(out.scale)[blk] = (uint16_t)f2bf(s);
+      if (out.scale_f32) out.scale_f32[blk] = s;
+      if (out.scale_e8m0) out.scale_e8m0[blk] = (uint8_t)e8m0_of(s);
     }
   };
 
@@ -1093,10 +1096,6 @@ static int launch_lut_k(const uint16_t* x, int64_t ngroups, const ScaleParams& s
     auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT, kCodes>;
     size_t lds = CB == 4 ? kCodeCopy2 + (size_t)lv.len * 2 : (size_t)lv.len * 2;
     unsigned grid = persistent_grid((const void*)k, bs, lds, ngroups);
-    // byte codes stream fastest from 16 waves per CU (C3 e4m3 35.4 us
-    // against 36.7 at full occupancy; every other form of this kernel is
-    // fastest at full occupancy)
-    if (CB == 8 && grid > (unsigned)num_cus()) grid = (unsigned)num_cus();
     hipLaunchKernelGGL(k, dim3(grid), dim3(bs), lds, st, x, ngroups, sp, lv, out, OutlierArgs{});
   } else {
     auto k = mx_lut_kernel<CB, LPB, ABSMAX, WANT, false>;
