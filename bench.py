@@ -440,6 +440,32 @@ def setup_c5_linear_mx(vqx, torch, L, M=2048):
         bound="mfma", dtype="bf16", cpu=cpu_c5(torch, Ac, N), keep=(A, idx, scale, code))
 
 
+def setup_c5_linear_mx_skinny(vqx, torch, L, M=1, N=11008):
+    """The decode-time call as a converted model makes it: one
+    torch.ops.quantized_ops.linear_mx per step on convert-format operands
+    (bf16 indices, weight_code, bf16 weight_scale) with an [M, 4096]
+    activation, host dispatch included: the step time is the rate at which
+    the op can be called back to back (the weight is packed once, cached)."""
+    g = torch.Generator().manual_seed(4)
+    K = 4096
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+    idx = torch.randint(0, 16, (N, K), generator=g).to(torch.bfloat16).cuda()
+    scale = (torch.rand(N, K // 64, generator=g) * 0.05 + 0.001).to(torch.bfloat16).cuda()
+    code = vqx.parse_format("nf4").tables(A.device)["levels_bf16"].clone()
+    Q = torch.ops.quantized_ops
+
+    def launch():
+        Q.linear_mx(A, idx, None, weight_scale=scale, weight_code=code, block_size=64)
+        return 0
+
+    launch()  # packs the weight once
+    return [launch], dict(
+        name=f"C5 decode-time call: quantized_ops::linear_mx per step, A bf16 [{M},4096] x convert-format NF4 weight "
+             f"[{N},4096] (bf16 indices + weight_code + bf16 weight_scale, block 64) -> bf16; host dispatch included",
+        elements=M * N, bytes=N * K // 2 + N * K // 64 * 4 + M * K * 2 + M * N * 2, flops=2 * M * N * K,
+        bound="hbm", dtype="bf16", keep=(A, idx, scale, code))
+
+
 def setup_c5_skinny(vqx, torch, L, M, N=11008):
     """C5's weight with a decode-time batch of M rows (the skinny kernel,
     bound by the 4-bit weight's bytes); N = 4096 is a 7B attention
@@ -699,6 +725,7 @@ CONFIGS = {
     "c5_m1": lambda v, t, L: setup_c5_skinny(v, t, L, 1),
     "c5_m16": lambda v, t, L: setup_c5_skinny(v, t, L, 16),
     "c5_m1_n4096": lambda v, t, L: setup_c5_skinny(v, t, L, 1, N=4096),
+    "c5_linear_mx_m1": lambda v, t, L: setup_c5_linear_mx_skinny(v, t, L, 1),
     "f3_gwa": lambda v, t, L: setup_f3(v, t, L),
     "o1_filter": lambda v, t, L: setup_o1(v, t, L),
     "o2_quantize_mx_outlier": lambda v, t, L: setup_o1(v, t, L, mx=True),
@@ -882,6 +909,7 @@ DOMINANT = {
     "c5_m1": "nf4_skinny_kernel",
     "c5_m16": "nf4_skinny_kernel",
     "c5_m1_n4096": "nf4_skinny_kernel",
+    "c5_linear_mx_m1": "nf4_skinny_kernel",
     "f3_gwa": "gwa_fq_rows_kernel<unsigned short, 8>",
     "o1_filter": "outlier_split_kernel<1, 8, false, 1, true>",
     "o2_quantize_mx_outlier": "outlier_split_kernel<1, 8, true, 4, true>",

@@ -147,16 +147,24 @@ def _check(rc, what):
     raise RuntimeError(f"{what} failed ({rc}): {msg}")
 
 
+_FNS = {}
+
+
 def call(name, *args):
-    fn = getattr(load(), name)
-    _check(fn(*args), name)
+    fn = _FNS.get(name)
+    if fn is None:
+        fn = _FNS[name] = getattr(load(), name)
+    rc = fn(*args)
+    if rc != 0:
+        _check(rc, name)
 
 
 def ptr(t):
-    """Device pointer of a tensor (None -> NULL)."""
+    """Device pointer of a tensor (None -> NULL), as the int ctypes passes
+    for a void* argument."""
     if t is None:
         return None
-    return ctypes.c_void_p(t.data_ptr())
+    return t.data_ptr()
 
 
 def dtype_tag(dt):
@@ -167,8 +175,10 @@ def dtype_tag(dt):
 
 
 def stream_of(t):
-    """The current torch stream of t's device, as a hipStream_t."""
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """The current torch stream of t's device, as a hipStream_t (the raw
+    handle, without building a torch Stream object on every call)."""
+    idx = t.device.index
+    return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device() if idx is None else idx)
 
 
 def require_device(t, what):
