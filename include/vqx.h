@@ -213,11 +213,18 @@ int vqx_mx_quantize(const void* x, int32_t x_dtype, int64_t outer, int64_t L, in
  * threshold); a NaN t skips nothing, a t <= -0 every non-NaN element.  t is
  * read from threshold_dev (fp32, device) when it is not NULL, else it is
  * `threshold`.
- * stats (optional): 32 bytes of device memory, zeroed once by the caller,
- * that keep the largest fraction of outliers seen (max_outlier_pct,
- * :389-391) as the fp64 at byte offset 16 (count / numel, as Python divides);
- * calls sharing one stats buffer must be ordered (one stream).
+ * stats (optional): vqx_outlier_stats_size bytes of 256-byte aligned device
+ * memory, zeroed once by the caller, that keep the largest fraction of
+ * outliers seen (max_outlier_pct, :389-391; count / numel as Python divides).
+ * A call counts into one of two sets, named by stats_parity; calls sharing a
+ * buffer must be ordered (one stream) and alternate parities.  Each call
+ * folds the other set (the previous call's) into the fp64 at byte offset 0.
+ * Set p starts at byte 256 + 2176 p: its uint64 numel (the last call's
+ * element count), then 16 uint64 partial counts 128 bytes apart (bytes
+ * 128, 256, ..., 2048 of the set).  The current fraction is the maximum of
+ * the fp64 and the last call's set (sum of its counts / its numel).
  */
+int vqx_outlier_stats_size(int64_t* bytes);
 
 /*
  * The outlier_pct threshold (fake_quantize.py:373-387): the k-th largest |x|
@@ -245,8 +252,8 @@ int vqx_outlier_topk_threshold(const void* x, int32_t x_dtype, int64_t n, int64_
 int vqx_mx_fake_quant_outlier(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
                               int64_t block_size, const vqx_format* fmt, int32_t scale_mode, int32_t pow2_shift,
                               float quant_max, const uint16_t* scale_qmap, const float* threshold_dev,
-                              float threshold, void* stats, void* scale_out, float* scale_f32, void* fq,
-                              vqx_stream_t stream);
+                              float threshold, void* stats, int32_t stats_parity, void* scale_out,
+                              float* scale_f32, void* fq, vqx_stream_t stream);
 
 /*
  * The mask and the restore around the other quantization schemes
@@ -256,7 +263,7 @@ int vqx_mx_fake_quant_outlier(const void* x, int32_t x_dtype, int64_t outer, int
  * or F16; 16-byte aligned x and masked.
  */
 int vqx_outlier_mask(const void* x, int32_t x_dtype, int64_t n, const float* threshold_dev, float threshold,
-                     void* stats, void* masked, vqx_stream_t stream);
+                     void* stats, int32_t stats_parity, void* masked, vqx_stream_t stream);
 int vqx_outlier_restore(const void* x, int32_t x_dtype, int64_t n, const float* threshold_dev, float threshold,
                         void* y, vqx_stream_t stream);
 

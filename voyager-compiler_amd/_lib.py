@@ -79,8 +79,9 @@ _SIGNATURES = {
     "vqx_outlier_topk_workspace_size": ([ctypes.POINTER(_I64)], ctypes.c_int),
     "vqx_outlier_topk_threshold": ([_P, _I32, _I64, _I64, _I32, _F, _F, _P, _P, _I64, _P], ctypes.c_int),
     "vqx_mx_fake_quant_outlier": ([_P, _I32, _I64, _I64, _I64, _I64, ctypes.POINTER(VqxFormat), _I32, _I32, _F, _P,
-                                   _P, _F, _P, _P, _P, _P, _P], ctypes.c_int),
-    "vqx_outlier_mask": ([_P, _I32, _I64, _P, _F, _P, _P, _P], ctypes.c_int),
+                                   _P, _F, _P, _I32, _P, _P, _P, _P], ctypes.c_int),
+    "vqx_outlier_stats_size": ([ctypes.POINTER(_I64)], ctypes.c_int),
+    "vqx_outlier_mask": ([_P, _I32, _I64, _P, _F, _P, _I32, _P, _P], ctypes.c_int),
     "vqx_outlier_restore": ([_P, _I32, _I64, _P, _F, _P, _P], ctypes.c_int),
     "vqx_decode_table": ([ctypes.POINTER(VqxFormat), _P, _I32, _P], ctypes.c_int),
     "vqx_gwa_fake_quant": ([_P, _I32, _I64, _I64, _I64, _I64, _F, _F, _P, _P, _P, _P, _P], ctypes.c_int),

@@ -207,6 +207,13 @@ int vqx_mx_quantize(const void* x, int32_t x_dtype, int64_t outer, int64_t L, in
   return mx_quantize(x, x_dtype, outer, L, inner, block_size, d, sp, out, code_layout, (hipStream_t)stream);
 }
 
+int vqx_outlier_stats_size(int64_t* bytes) {
+  g_err[0] = 0;
+  if (!bytes) return set_error(kErrInvalid, "outlier_stats_size: null result pointer");
+  *bytes = kOutlierStatsBytes;
+  return kOk;
+}
+
 int vqx_outlier_topk_workspace_size(int64_t* bytes) {
   g_err[0] = 0;
   if (!bytes) return set_error(kErrInvalid, "outlier_topk_workspace_size: null result pointer");
@@ -223,15 +230,16 @@ int vqx_outlier_topk_threshold(const void* x, int32_t x_dtype, int64_t n, int64_
                                 workspace_bytes, (hipStream_t)stream);
 }
 
-static OutlierArgs outlier_args(const float* threshold_dev, float threshold, void* stats, int64_t numel) {
-  return OutlierArgs{1, threshold_dev, threshold, (OutlierStats*)stats, numel};
+static OutlierArgs outlier_args(const float* threshold_dev, float threshold, void* stats, int64_t numel,
+                                int32_t parity) {
+  return OutlierArgs{1, threshold_dev, threshold, (OutlierStats*)stats, numel, parity};
 }
 
 int vqx_mx_fake_quant_outlier(const void* x, int32_t x_dtype, int64_t outer, int64_t L, int64_t inner,
                               int64_t block_size, const vqx_format* fmt, int32_t scale_mode, int32_t pow2_shift,
                               float quant_max, const uint16_t* scale_qmap, const float* threshold_dev,
-                              float threshold, void* stats, void* scale_out, float* scale_f32, void* fq,
-                              vqx_stream_t stream) {
+                              float threshold, void* stats, int32_t stats_parity, void* scale_out,
+                              float* scale_f32, void* fq, vqx_stream_t stream) {
   g_err[0] = 0;
   FormatDesc d;
   VQX_TRY(to_desc(fmt, &d));
@@ -239,26 +247,29 @@ int vqx_mx_fake_quant_outlier(const void* x, int32_t x_dtype, int64_t outer, int
   if (!fq && outer * L * inner > 0) return set_error(kErrInvalid, "mx_fake_quant_outlier: null output");
   if (scale_mode != 0 && scale_mode != 1)
     return set_error(kErrInvalid, "mx_fake_quant_outlier: scale_mode must be 0 or 1");
-  if (stats && !aligned(stats, 8)) return set_error(kErrInvalid, "mx_fake_quant_outlier: stats must be 8-byte aligned");
+  if (stats && !aligned(stats, 256)) return set_error(kErrInvalid, "mx_fake_quant_outlier: stats must be 256-byte aligned");
+  if (stats_parity != 0 && stats_parity != 1) return set_error(kErrInvalid, "mx_fake_quant_outlier: parity must be 0 or 1");
   ScaleParams sp{scale_mode, pow2_shift, quant_max, scale_qmap};
   MxOut out{scale_out, scale_f32, nullptr, nullptr, fq, nullptr};
-  const OutlierArgs oa = outlier_args(threshold_dev, threshold, stats, outer * L * inner);
+  const OutlierArgs oa = outlier_args(threshold_dev, threshold, stats, outer * L * inner, stats_parity);
   return mx_quantize(x, x_dtype, outer, L, inner, block_size, d, sp, out, 1, (hipStream_t)stream, &oa);
 }
 
 int vqx_outlier_mask(const void* x, int32_t x_dtype, int64_t n, const float* threshold_dev, float threshold,
-                     void* stats, void* masked, vqx_stream_t stream) {
+                     void* stats, int32_t stats_parity, void* masked, vqx_stream_t stream) {
   g_err[0] = 0;
   if (n < 0) return set_error(kErrInvalid, "outlier_mask: negative size");
-  if (stats && !aligned(stats, 8)) return set_error(kErrInvalid, "outlier_mask: stats must be 8-byte aligned");
-  return outlier_mask(x, x_dtype, n, outlier_args(threshold_dev, threshold, stats, n), masked, (hipStream_t)stream);
+  if (stats && !aligned(stats, 256)) return set_error(kErrInvalid, "outlier_mask: stats must be 256-byte aligned");
+  if (stats_parity != 0 && stats_parity != 1) return set_error(kErrInvalid, "outlier_mask: parity must be 0 or 1");
+  return outlier_mask(x, x_dtype, n, outlier_args(threshold_dev, threshold, stats, n, stats_parity), masked,
+                      (hipStream_t)stream);
 }
 
 int vqx_outlier_restore(const void* x, int32_t x_dtype, int64_t n, const float* threshold_dev, float threshold,
                         void* y, vqx_stream_t stream) {
   g_err[0] = 0;
   if (n < 0) return set_error(kErrInvalid, "outlier_restore: negative size");
-  return outlier_restore(x, x_dtype, n, outlier_args(threshold_dev, threshold, nullptr, n), y, (hipStream_t)stream);
+  return outlier_restore(x, x_dtype, n, outlier_args(threshold_dev, threshold, nullptr, n, 0), y, (hipStream_t)stream);
 }
 
 int vqx_mx_decode(const uint8_t* codes, int32_t code_bits, const uint16_t* decode_table, int32_t ntab,

@@ -48,15 +48,21 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v) {
 // before it, so they drop out of block maxima) and come back unchanged after
 // it; the largest skipped fraction seen so far is kept on the device.
 // ---------------------------------------------------------------------------
-// Device state of the skipped-element count (32 bytes, zero-initialised once
-// by the caller; every launch leaves `tally` at zero again).
-struct OutlierStats {
-  unsigned long long tally;  // the running launch: finished workgroups << 40 | skipped elements
-  unsigned long long pad;
-  unsigned long long best;   // the largest count / numel so far, fp64 bits
-  unsigned long long reserved;
-};
-constexpr int kTallyShift = 40;  // up to 2^40 - 1 elements per launch, 2^24 - 1 workgroups
+// Device state of the skipped-element counts (kOutlierStatsBytes, zeroed
+// once by the caller).  A launch adds its count into the 16 slots of the set
+// its parity names (workgroup i into slot i % 16, one fire-and-forget atomic
+// each, the slots 128 bytes apart so they do not contend), and its workgroup
+// 0 records the launch's numel there and folds the other set (the previous
+// launch's, complete by then) into `best`, then clears it.  Launches that
+// share a stats buffer alternate parities; the host folds the last launch's
+// set when it reads the fraction.
+constexpr int kOutlierSlots = 16;
+constexpr int kOutlierStride = 128;                                     // bytes between slots
+constexpr int kOutlierBest = 0;                                         // fp64 bits of the largest fraction
+constexpr int kOutlierSet0 = 256;                                       // set p at kOutlierSet0 + p * kOutlierSetBytes
+constexpr int kOutlierSetBytes = kOutlierStride * (1 + kOutlierSlots);  // numel, then the slots
+constexpr int kOutlierStatsBytes = kOutlierSet0 + 2 * kOutlierSetBytes;
+struct OutlierStats;  // opaque: the byte layout above
 
 struct OutlierArgs {
   int32_t active;        // 0: no masking (the other fields unused)
@@ -64,6 +70,7 @@ struct OutlierArgs {
   float thr_host;
   OutlierStats* stats;   // null: nothing counted
   int64_t numel;         // the fraction's denominator (the whole tensor)
+  int32_t parity;        // the stats set this launch counts into (0 or 1)
 };
 
 // The threshold as a bound on the magnitude bits of x's dtype: |x| >= t is
@@ -84,13 +91,16 @@ __device__ __forceinline__ bool outlier_skip(uint32_t mag, uint32_t bound, uint3
   return mag >= bound && mag <= inf;
 }
 
+__device__ __forceinline__ unsigned long long* outlier_word(OutlierStats* st, int byte_offset) {
+  return reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(st) + byte_offset);
+}
+
 // End of an outlier-masking launch: the workgroup's skipped elements (cnt per
-// thread) join the launch's count, and the last workgroup to finish folds
-// count / numel into the largest fraction and clears the tally for the next
-// launch.  Every thread of every workgroup calls it once.  Each workgroup
-// adds its count and its arrival in one device-scope atomic (coherent across
-// the XCDs' L2s at the access), so the workgroup that brings the arrivals to
-// the grid size reads the whole count in the value it gets back.
+// thread) go into a slot of the launch's set with one atomic whose result
+// nobody waits for; workgroup 0 also records the launch's numel and folds
+// the previous launch's set into the largest fraction (count / numel in
+// fp64: both below 2^53, so this is the quotient Python's int / int gives)
+// and clears that set.  Every thread of every workgroup calls it once.
 __device__ __forceinline__ void outlier_tally(uint32_t cnt, const OutlierArgs& oa) {
   if (!oa.stats) return;
   __shared__ unsigned long long s_tot;
@@ -102,20 +112,26 @@ __device__ __forceinline__ void outlier_tally(uint32_t cnt, const OutlierArgs& o
   __syncthreads();
   if (threadIdx.x != 0) return;
   OutlierStats* st = oa.stats;
-  const unsigned long long add = (1ull << kTallyShift) + s_tot;
-  const unsigned long long prev = __hip_atomic_fetch_add(&st->tally, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const unsigned long long grid = (unsigned long long)gridDim.x * gridDim.y * gridDim.z;
-  if ((prev >> kTallyShift) != grid - 1) return;
-  const unsigned long long c = (prev + add) & ((1ull << kTallyShift) - 1);
-  __hip_atomic_store(&st->tally, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // Python's count / numel: both below 2^53, so the fp64 division is the
-  // correctly rounded quotient Python's int / int gives
-  const double f = (double)c / (double)oa.numel;
-  const double b = __builtin_bit_cast(double, __hip_atomic_load(&st->best, __ATOMIC_RELAXED,
-                                                                __HIP_MEMORY_SCOPE_AGENT));
-  if (f > b)
-    __hip_atomic_store(&st->best, __builtin_bit_cast(unsigned long long, f), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  const int cur = kOutlierSet0 + oa.parity * kOutlierSetBytes, prev = kOutlierSet0 + (1 - oa.parity) * kOutlierSetBytes;
+  const unsigned bid = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  if (s_tot)
+    __hip_atomic_fetch_add(outlier_word(st, cur + kOutlierStride * (1 + (int)(bid % kOutlierSlots))), s_tot,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (bid != 0) return;
+  __hip_atomic_store(outlier_word(st, cur), (unsigned long long)oa.numel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long n = __hip_atomic_load(outlier_word(st, prev), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (n == 0) return;
+  unsigned long long c = 0;
+  for (int s = 1; s <= kOutlierSlots; ++s) {
+    unsigned long long* w = outlier_word(st, prev + kOutlierStride * s);
+    c += __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __hip_atomic_store(outlier_word(st, prev), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const double f = (double)c / (double)n;
+  unsigned long long* best = outlier_word(st, kOutlierBest);
+  const double b = __builtin_bit_cast(double, __hip_atomic_load(best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  if (f > b) __hip_atomic_store(best, __builtin_bit_cast(unsigned long long, f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct MxOut {

@@ -431,12 +431,12 @@ def mx_scale_shape(shape, axis, block_size):
 
 
 def mx_fake_quantize_outlier(input, desc, axis, block_size, quant_max, force_pow2, scale_qmap, threshold, stats,
-                             scale_f32=None):
+                             parity=0, scale_f32=None):
     """FakeQuantize's outlier masking around MXFakeQuantizeFunction.forward
     (fake_quantize.py:388-395 around :397-408) in one pass: the elements with
     |x| >= threshold (a float, or an fp32 device tensor) are zeros for the
     block scales and the fake-quant, come back unchanged in the output, and
-    are counted into stats (32 bytes of device memory, see
+    are counted into stats (outlier_stats(), set `parity`; see
     vqx_mx_fake_quant_outlier).  Returns (scale, output): the scale in x's
     dtype, or written into scale_f32 (a contiguous fp32 tensor of the scale
     shape) and returned as it."""
@@ -454,7 +454,7 @@ def mx_fake_quantize_outlier(input, desc, axis, block_size, quant_max, force_pow
     thr_dev, thr = _threshold_args(threshold, x.device)
     _lib.call("vqx_mx_fake_quant_outlier", _lib.ptr(x), _lib.dtype_tag(x.dtype), outer, L, inner, block_size,
               _lib.ctypes.byref(desc), 0 if force_pow2 else 1, shift, float(quant_max), _lib.ptr(sq), thr_dev, thr,
-              _lib.ptr(stats), _lib.ptr(scale), _lib.ptr(scale_f32), _lib.ptr(y), _lib.stream_of(x))
+              _lib.ptr(stats), int(parity), _lib.ptr(scale), _lib.ptr(scale_f32), _lib.ptr(y), _lib.stream_of(x))
     return (scale if scale_f32 is None else scale_f32), y
 
 
@@ -468,15 +468,48 @@ def _threshold_args(threshold, device):
     return None, float(threshold)
 
 
-def outlier_mask(input, threshold, stats, masked=True):
+def outlier_mask(input, threshold, stats, parity=0, masked=True):
     """x.masked_fill(|x| >= threshold, 0) (fake_quantize.py:388-391), with the
-    outliers counted into stats; masked=False only counts (returns None)."""
+    outliers counted into stats (set `parity`); masked=False only counts
+    (returns None)."""
     x = input.contiguous()
     out = torch.empty_like(x) if masked else None
     thr_dev, thr = _threshold_args(threshold, x.device)
     _lib.call("vqx_outlier_mask", _lib.ptr(x), _lib.dtype_tag(x.dtype), x.numel(), thr_dev, thr, _lib.ptr(stats),
-              _lib.ptr(out), _lib.stream_of(x))
+              int(parity), _lib.ptr(out), _lib.stream_of(x))
     return out
+
+
+# The stats buffer's layout (include/vqx.h, vqx_outlier_stats_size): the fp64
+# of the largest fraction folded so far at byte 0; set p at byte 256 + 2176 p,
+# its numel there and 16 partial counts at 128-byte steps after it.
+_STATS_SET0, _STATS_SET_BYTES, _STATS_STRIDE, _STATS_SLOTS = 256, 2176, 128, 16
+_STATS_BYTES = None
+
+
+def outlier_stats(device):
+    """Zeroed device memory for the outlier counts (vqx_outlier_stats_size
+    bytes, 256-byte aligned by the caching allocator)."""
+    global _STATS_BYTES
+    if _STATS_BYTES is None:
+        n = ctypes.c_int64(0)
+        _lib.call("vqx_outlier_stats_size", ctypes.byref(n))
+        _STATS_BYTES = n.value
+    return torch.zeros(_STATS_BYTES // 8, dtype=torch.int64, device=device)
+
+
+def outlier_stats_fraction(stats, last_parity):
+    """The largest fraction of outliers in a stats buffer (one host read):
+    the folded maximum, or the last call's count / numel (set last_parity)
+    when larger."""
+    w = stats.cpu()
+    best = float(w.view(torch.float64)[0])
+    base = (_STATS_SET0 + last_parity * _STATS_SET_BYTES) // 8
+    n = int(w[base])
+    if n:
+        c = sum(int(w[base + _STATS_STRIDE // 8 * (1 + s)]) for s in range(_STATS_SLOTS))
+        best = max(best, c / n)
+    return best
 
 
 def outlier_restore_(input, threshold, y):

@@ -247,6 +247,7 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
         self.observer_enabled[0] = self.qscheme is not None
         self._max_outlier_host = 0.0
         self._outlier_stats = None
+        self._outlier_parity = 0
         self._topk_ws = None
         self.is_per_channel = self.qscheme == QScheme.PER_CHANNEL_SYMMETRIC
         if outlier_pct is not None:
@@ -298,15 +299,16 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
         return self._qmap_sig == (self.qmap.data_ptr(), _lib.version_of(self.qmap))
 
     # max_outlier_pct: the largest fraction of outliers seen so far
-    # (fake_quantize.py:389-391).  The device keeps it (count / numel in fp64,
-    # as Python divides) in a 32-byte stats buffer the kernels update, so the
-    # forward does not synchronise; the host reads it when the value is read
-    # (convert reads it).
+    # (fake_quantize.py:389-391).  The kernels keep it on the device in a
+    # stats buffer (count / numel in fp64, as Python divides), each forward
+    # counting into the set after the previous one's, so the forward does not
+    # synchronise; the host reads it when the value is read (convert reads it).
     @property
     def max_outlier_pct(self):
         st = self._outlier_stats
-        dev = 0.0 if st is None else float(st.view(torch.float64)[2].item())
-        return max(self._max_outlier_host, dev)
+        if st is None:
+            return self._max_outlier_host
+        return max(self._max_outlier_host, qops.outlier_stats_fraction(st, self._outlier_parity ^ 1))
 
     @max_outlier_pct.setter
     def max_outlier_pct(self, value):
@@ -315,16 +317,19 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
             self._outlier_stats.zero_()
 
     def _stats_on(self, device):
-        """The outlier stats buffer on `device` (a move folds the old one's
-        fraction into the host value)."""
+        """(stats buffer on `device`, parity of this forward's set); a move
+        folds the old buffer's fraction into the host value."""
         st = self._outlier_stats
         if st is not None and st.device != device:
             self._max_outlier_host = self.max_outlier_pct
             st = None
         if st is None:
-            st = torch.zeros(4, dtype=torch.int64, device=device)
+            st = qops.outlier_stats(device)
             self._outlier_stats = st
-        return st
+            self._outlier_parity = 0
+        parity = self._outlier_parity
+        self._outlier_parity ^= 1
+        return st, parity
 
     @torch.no_grad()
     def _update_outlier_threshold(self, x):
@@ -345,11 +350,11 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
     def _outlier_forward(self, x, fake_quant, fmt):
         """fake_quantize.py:388-432 on the device: returns the output."""
         thr = self.outlier_threshold
-        stats = self._stats_on(x.device)
+        stats, parity = self._stats_on(x.device)
         xc = x.contiguous()
         if self.qscheme == QScheme.MICROSCALING and x.dtype in (torch.bfloat16, torch.float32):
             if not fake_quant:  # MXFakeQuantizeFunction returns its input: only the count
-                qops.outlier_mask(xc, thr, stats, masked=False)
+                qops.outlier_mask(xc, thr, stats, parity, masked=False)
                 return x
             if fmt is not None:
                 desc, keep = fmt.desc(xc.device), None
@@ -359,12 +364,12 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
             direct = _direct_scale(self.scale, xc, axis, self.block_size)
             sf, y = qops.mx_fake_quantize_outlier(xc, desc, axis, self.block_size, self.quant_max,
                                                   self.force_scale_power_of_two, self.scale_qmap, thr, stats,
-                                                  scale_f32=direct)
+                                                  parity, scale_f32=direct)
             del keep
             if direct is None:
                 self.scale.resize_(sf.shape).copy_(sf)
             return y
-        xm = qops.outlier_mask(xc, thr, stats)
+        xm = qops.outlier_mask(xc, thr, stats, parity)
         if self.qscheme == QScheme.MICROSCALING:
             y = MXFakeQuantizeFunction.forward(None, xm, fake_quant, self.scale, self.qmap, self.ch_axis,
                                                self.block_size, self.quant_max, self.force_scale_power_of_two,
