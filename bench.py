@@ -488,6 +488,112 @@ def setup_c5_skinny(vqx, torch, L, M, N=11008):
         bound="hbm", dtype="bf16", keep=(A, codes, sc, lv, out), cpu=cpu_c5(torch, Ac, N))
 
 
+def _mx_desc(L, data, scale, code, k_major, bstride, ld, sbstride, sld, bs):
+    o = L.VqxMxOperand()
+    o.data = data.data_ptr()
+    o.scale = None if scale is None else scale.data_ptr()
+    o.code = None if code is None else code.data_ptr()
+    o.batch_stride, o.ld, o.scale_batch_stride, o.scale_ld = bstride, ld, sbstride, sld
+    o.k_major, o.block_size = k_major, bs
+    o.code_len = 0 if code is None else code.numel()
+    return o
+
+
+def _e5m3_scales(torch, g, shape):
+    e = torch.randint(-10, 1, shape, generator=g).float()
+    m = torch.randint(0, 8, shape, generator=g).float()
+    return (torch.exp2(e) * (1 + m / 8)).to(torch.bfloat16).cuda()
+
+
+def setup_c6_attention(vqx, torch, L, which, coded=False):
+    """The LLaMA-7B attention products of a converted model (B 1, 32 heads,
+    2048 positions, head dim 128) with the reference's attention specs:
+    int6 operands (or nf4_6 indices with the 16-entry code), the left one
+    blocked along -1 and the right one along -2 (the contraction dim), bf16
+    scales on the fp8_e5m3 grid; both decoded inside the kernel
+    (vqx_mx_matmul, what quantized_ops::matmul_mx runs for them).  qk:
+    [32,2048,128] x [32,128,2048]; pv: [32,2048,2048] x [32,2048,128], the
+    right operand N-major ([K][N]) in both."""
+    g = torch.Generator().manual_seed(6)
+    H, S, D, bs = 32, 2048, 128, 64
+    hi, lo = (16, 0) if coded else (32, -32)
+    M, N, K = (S, S, D) if which == "qk" else (S, D, S)
+    a = torch.randint(lo, hi, (H, M, K), generator=g).to(torch.bfloat16).cuda()
+    b = torch.randint(lo, hi, (H, K, N), generator=g).to(torch.bfloat16).cuda()
+    a_s = _e5m3_scales(torch, g, (H, M, K // bs))
+    b_s = _e5m3_scales(torch, g, (H, K // bs, N))
+    code = None
+    if coded:
+        code = torch.tensor([-31., -22., -16., -12., -9., -6., -3., 0., 2., 5., 8., 10., 14., 17., 22., 31.],
+                            dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(H, M, N, dtype=torch.bfloat16, device="cuda")
+    oa = _mx_desc(L, a, a_s, code, 1, M * K, K, M * (K // bs), K // bs, bs)
+    ob = _mx_desc(L, b, b_s, code, 0, K * N, N, (K // bs) * N, N, bs)
+    fn = L.load().vqx_mx_matmul
+    import ctypes
+    args = (ctypes.byref(oa), ctypes.byref(ob), None, L.ptr(out), H, M, N, K, L.stream_of(a))
+    fmt = "nf4_6 indices + 16-entry code" if coded else "int6"
+    nbytes = 2 * H * (M * K + K * N + M * (K // bs) + (K // bs) * N + M * N)
+    return [lambda: fn(*args)], dict(
+        name=f"C6 attention {which.upper()} of LLaMA-7B through vqx_mx_matmul: [32,{M},{K}] x [32,{K},{N}] "
+             f"({fmt}, bf16 fp8_e5m3-grid scales per 64 along K on both sides, decoded in the kernel) -> bf16",
+        elements=H * M * N, flops=2 * H * M * N * K, bytes=nbytes, bound="hbm", dtype="bf16",
+        keep=(a, b, a_s, b_s, code, out, oa, ob))
+
+
+def setup_c6_mxint8_linear(vqx, torch, L, M=2048, N=11008, K=4096):
+    """The MXINT8 CI scheme's linear at the LLaMA-7B MLP shape: int8
+    activations and weights (integer-valued bf16, as convert writes them),
+    power-of-two bf16 scales per 16 along K on both sides, decoded inside
+    the kernel (vqx_mx_matmul, what quantized_ops::linear_mx runs for them)."""
+    g = torch.Generator().manual_seed(7)
+    bs = 16
+    x = torch.randint(-127, 128, (M, K), generator=g).to(torch.bfloat16).cuda()
+    w = torch.randint(-127, 128, (N, K), generator=g).to(torch.bfloat16).cuda()
+    xs = torch.exp2(torch.randint(-12, -4, (M, K // bs), generator=g).float()).to(torch.bfloat16).cuda()
+    ws = torch.exp2(torch.randint(-12, -4, (N, K // bs), generator=g).float()).to(torch.bfloat16).cuda()
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    oa = _mx_desc(L, x, xs, None, 1, 0, K, 0, K // bs, bs)
+    ob = _mx_desc(L, w, ws, None, 1, 0, K, 0, K // bs, bs)
+    fn = L.load().vqx_mx_matmul
+    import ctypes
+    args = (ctypes.byref(oa), ctypes.byref(ob), None, L.ptr(out), 1, M, N, K, L.stream_of(x))
+    return [lambda: fn(*args)], dict(
+        name=f"C6 MXINT8 linear through vqx_mx_matmul: int8 A [{M},{K}] x int8 W [{N},{K}]^T, bf16 power-of-two "
+             f"scales per 16 along K on both sides, decoded in the kernel -> bf16",
+        elements=M * N, flops=2 * M * N * K, bytes=2 * (M * K + N * K + (M + N) * (K // bs) + M * N),
+        bound="mfma", dtype="bf16", keep=(x, w, xs, ws, out, oa, ob))
+
+
+def setup_c6_dense_library(vqx, torch, L, which):
+    """Comparison point, not this build's code: the C6 products on operands
+    already decoded to dense bf16, through torch.matmul / F.linear
+    (hipBLASLt): the GEMM half of the reference's decode-then-product, with
+    the decode not counted."""
+    g = torch.Generator().manual_seed(6)
+    if which == "linear":
+        M, N, K = 2048, 11008, 4096
+        a = torch.randn(M, K, generator=g).to(torch.bfloat16).cuda()
+        b = torch.randn(N, K, generator=g).to(torch.bfloat16).cuda()
+        F = torch.nn.functional
+        fn, H = (lambda: F.linear(a, b)), 1
+    else:
+        H, S, D = 32, 2048, 128
+        M, N, K = (S, S, D) if which == "qk" else (S, D, S)
+        a = torch.randn(H, M, K, generator=g).to(torch.bfloat16).cuda()
+        b = torch.randn(H, K, N, generator=g).to(torch.bfloat16).cuda()
+        fn = lambda: torch.matmul(a, b)
+
+    def launch():
+        fn()
+        return 0
+
+    return [launch], dict(
+        name=f"comparison: library bf16 GEMM on pre-decoded operands, [{H}] x [{M},{K}] x [{K},{N}] (hipBLASLt)",
+        elements=H * M * N, flops=2 * H * M * N * K, bytes=2 * H * (M * K + K * N + M * N),
+        bound="mfma" if which == "linear" else "hbm", dtype="bf16", keep=(a, b))
+
+
 def setup_c5_dense_library(vqx, torch, L, N=11008, M=2048):
     """Comparison point, not this build's code: C5's product with an already
     dense bf16 weight through torch.nn.functional.linear (hipBLASLt), i.e. the
@@ -736,6 +842,10 @@ CONFIGS = {
     "f1_outlier_othr_ax2": lambda v, t, L: setup_f1(v, t, L, "nf4_6,qs=microscaling,bs=64,ax=-2,scale=fp8_e5m3,othr=6.0",
                                                     (1, 32, 2048, 128)),
     "g1_gptq": lambda v, t, L: setup_g1(v, t, L),
+    "c6_attn_qk_int6": lambda v, t, L: setup_c6_attention(v, t, L, "qk"),
+    "c6_attn_pv_int6": lambda v, t, L: setup_c6_attention(v, t, L, "pv"),
+    "c6_attn_qk_nf4_6": lambda v, t, L: setup_c6_attention(v, t, L, "qk", coded=True),
+    "c6_mxint8_linear": lambda v, t, L: setup_c6_mxint8_linear(v, t, L),
 }
 HEADLINE = "c2"
 
@@ -889,6 +999,9 @@ ON_REQUEST = {
     "c5_m256_whole_tiles": lambda v, t, L: setup_c5(v, t, L, whole_tiles=True, M=256),
     "c5_dense_library": lambda v, t, L: setup_c5_dense_library(v, t, L),
     "c5_dense_library_n8192": lambda v, t, L: setup_c5_dense_library(v, t, L, N=8192),
+    "c6_qk_dense_library": lambda v, t, L: setup_c6_dense_library(v, t, L, "qk"),
+    "c6_pv_dense_library": lambda v, t, L: setup_c6_dense_library(v, t, L, "pv"),
+    "c6_linear_dense_library": lambda v, t, L: setup_c6_dense_library(v, t, L, "linear"),
 }
 
 DOMINANT = {
@@ -918,6 +1031,10 @@ DOMINANT = {
     "g1_gptq": "gptq_block_kernel",
     "f1_outlier_opct": "mx_lut_kernel<0, 4, true, 2, false, true>",
     "f1_outlier_othr_ax2": "mx_block_kernel<unsigned short, vqx::EncLevels>",
+    "c6_attn_qk_int6": "mx_gemm_kernel<1, 1, false>",
+    "c6_attn_pv_int6": "mx_gemm_kernel<1, 1, false>",
+    "c6_attn_qk_nf4_6": "mx_gemm_kernel<3, 3, false>",
+    "c6_mxint8_linear": "mx_gemm_kernel<1, 1, true>",
 }
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
 

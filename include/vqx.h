@@ -381,6 +381,55 @@ int vqx_nf4_pack_weight(const void* weight, int32_t w_dtype, const void* scale, 
                         int32_t* bad, vqx_stream_t stream);
 
 /*
+ * One operand of vqx_mx_matmul in the convert format, read in place: `data`
+ * holds bf16 values, or integer-valued bf16 code indices when `code` is set;
+ * the decoded operand is bf16(code[trunc(data)] * scale[block]) with either
+ * part optional, as src/vc/ops/quantized.py:313-326 (linear_mx) and :388-398
+ * (matmul_mx) decode it.  An index outside the code table (the reference
+ * raises IndexError) decodes to NaN.
+ *   k_major = 1: rows of K contiguous values, row r at data + r * ld;
+ *                scales [rows][ceil(K / block_size)], row r at
+ *                scale + r * scale_ld.
+ *   k_major = 0: K rows of contiguous columns, k row at data + k * ld (right
+ *                operand only); scales [ceil(K / block_size)][cols], block
+ *                row at scale + j * scale_ld (16-byte aligned, scale_ld and
+ *                scale_batch_stride multiples of 8).
+ * batch_stride / scale_batch_stride: elements between batch items (0: the
+ * same matrix for every item).  data 16-byte aligned, ld and batch_stride
+ * multiples of 8; block_size a power of two >= 8; code: bf16, code_len
+ * 1..256 entries.
+ */
+typedef struct VqxMxOperand {
+  const void* data;
+  const void* scale;
+  const void* code;
+  int64_t batch_stride;
+  int64_t ld;
+  int64_t scale_batch_stride;
+  int64_t scale_ld;
+  int32_t k_major;
+  int32_t block_size;
+  int32_t code_len;
+  int32_t reserved;
+} VqxMxOperand;
+
+/*
+ * The dense product of linear_mx / matmul_mx (src/vc/ops/quantized.py:
+ * 295-348 and 371-421) with both operands decoded inside the kernel:
+ * out[b][M][N] = A'[b] . B'[b] (+ bias), fp32 accumulation, bf16 out
+ * (contiguous, 8-byte aligned).  a: the left operand [M][K], k_major = 1;
+ * b: the right operand, [N][K] (k_major = 1: linear_mx "kc", matmul_mx
+ * "kc") or [K][N] (k_major = 0: matmul_mx "ck", linear_mx "ck").  bias: bf16
+ * [N] (8-byte aligned) or NULL.  K % 8 == 0, N % 4 == 0 (N % 8 == 0 when
+ * b is N-major).  Replaces the decode + aten.linear / aten.matmul sequence
+ * for operands outside vqx_nf4_linear's format (code tables of more than
+ * 16 entries, no code table, blocks other than 64, coded activations,
+ * batched right operands).
+ */
+int vqx_mx_matmul(const VqxMxOperand* a, const VqxMxOperand* b, const uint16_t* bias, uint16_t* out,
+                  int64_t batch, int64_t M, int64_t N, int64_t K, vqx_stream_t stream);
+
+/*
  * quantized_ops::filter_outlier (src/vc/ops/quantized.py:532-630, with
  * _pad_csr at :537-569), and the outlier half of quantize_mx_outlier
  * (:633-712, indptr_offset added to the row pointers).

@@ -51,6 +51,22 @@ class VqxScaleMap(ctypes.Structure):
     ]
 
 
+class VqxMxOperand(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("code", ctypes.c_void_p),
+        ("batch_stride", ctypes.c_int64),
+        ("ld", ctypes.c_int64),
+        ("scale_batch_stride", ctypes.c_int64),
+        ("scale_ld", ctypes.c_int64),
+        ("k_major", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("code_len", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
@@ -90,6 +106,7 @@ _SIGNATURES = {
     "vqx_nf4_linear": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
     "vqx_nf4_linear_workspace_size": ([_I64, _I64, _I64, ctypes.POINTER(_I64)], ctypes.c_int),
     "vqx_nf4_linear_ws": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P], ctypes.c_int),
+    "vqx_mx_matmul": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P], ctypes.c_int),
     "vqx_nf4_linear_noalloc": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
     "vqx_nf4_pack_weight": ([_P, _I32, _P, _I32, _I64, _I64, _I32, _I32, _P, _P, _P, _P], ctypes.c_int),
     "vqx_filter_outlier": ([_P, _I32, _I64, _I64, _I64, _F, _I64, _I32, _P, _P, _P, _P, _P], ctypes.c_int),

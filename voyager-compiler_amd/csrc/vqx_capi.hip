@@ -347,6 +347,15 @@ int vqx_nf4_linear_noalloc(const uint16_t* A, const uint8_t* codes, const float*
   return nf4_gemm_noalloc(A, codes, scale, levels, bias, out, M, N, K, (hipStream_t)stream);
 }
 
+int vqx_mx_matmul(const VqxMxOperand* a, const VqxMxOperand* b, const uint16_t* bias, uint16_t* out,
+                  int64_t batch, int64_t M, int64_t N, int64_t K, vqx_stream_t stream) {
+  g_err[0] = 0;
+  static_assert(sizeof(VqxMxOperand) == sizeof(MxOperand), "VqxMxOperand and MxOperand differ");
+  if (!a || !b) return set_error(kErrInvalid, "mx_matmul: null operand descriptor");
+  return mx_gemm(*reinterpret_cast<const MxOperand*>(a), *reinterpret_cast<const MxOperand*>(b), bias, out, batch, M,
+                 N, K, (hipStream_t)stream);
+}
+
 int vqx_nf4_pack_weight(const void* weight, int32_t w_dtype, const void* scale, int32_t s_dtype, int64_t N,
                         int64_t K, int32_t transposed, int32_t ncode, uint8_t* codes, float* scale_out,
                         int32_t* bad, vqx_stream_t stream) {

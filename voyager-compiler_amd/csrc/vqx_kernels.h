@@ -197,6 +197,23 @@ int nf4_gemm_noalloc(const uint16_t* A, const uint8_t* codes, const float* scale
 int nf4_pack(const void* weight, int w_dtype, const void* scale, int s_dtype, int64_t N, int64_t K, int transposed,
              int ncode, uint8_t* codes, float* scale_out, int* bad, hipStream_t st);
 
+// vqx_mx_gemm.hip (the layout of VqxMxOperand in vqx.h)
+struct MxOperand {
+  const void* data;          // bf16 values or integer-valued bf16 code indices
+  const void* scale;         // bf16 scales, one per block_size along K, or null
+  const void* code;          // bf16 code table of code_len entries, or null
+  int64_t batch_stride;      // elements between batch items (0: one matrix for every item)
+  int64_t ld;                // elements between rows ([rows][K]) or between k rows ([K][cols])
+  int64_t scale_batch_stride;
+  int64_t scale_ld;          // scale elements between rows, or between block rows
+  int32_t k_major;           // 1: [rows][K], K contiguous; 0: [K][cols]
+  int32_t block_size;
+  int32_t code_len;
+  int32_t reserved;
+};
+int mx_gemm(const MxOperand& a, const MxOperand& b, const uint16_t* bias, uint16_t* out, int64_t batch, int64_t M,
+            int64_t N, int64_t K, hipStream_t st);
+
 // vqx_sparse.hip
 struct CsrDecode {
   const void* B;        // [nb, br, bc], dtype b_dtype (float tags or kU8)

@@ -760,22 +760,184 @@ def _fused_linear(x, weight, bias, weight_scale, weight_code, transposed):
     return out.reshape(*x.shape[:-1], N)
 
 
+# The product with both operands decoded inside the kernel (vqx_mx_matmul):
+# every other bf16 convert-format pair whose scales run along the contraction
+# dim -- coded activations, code tables of up to 256 entries or none (int6,
+# int8), power-of-two blocks from 8 up, batched right operands (the attention
+# products), either storage layout of the right operand.
+_BF16_CODES = {}
+
+
+def _code_bf16(code: torch.Tensor, device) -> torch.Tensor:
+    """The code table as the bf16 values the kernel reads (the reference casts
+    the looked-up values to the operand's dtype, bf16 here), cached per code
+    tensor and version."""
+    key = (code.data_ptr(), _lib.version_of(code), code.numel(), code.dtype, str(device))
+    hit = _BF16_CODES.get(key)
+    if hit is not None and hit[0]() is code:
+        return hit[1]
+    t = code.reshape(-1).to(device=device, dtype=torch.bfloat16).contiguous()
+    _BF16_CODES[key] = (weakref.ref(code), t)
+    return t
+
+
+def _mx_side_ok(t, code, scale, block_size, kdim):
+    """Whether one operand fits vqx_mx_matmul: bf16 data, at most 256 code
+    entries, bf16 scales with the operand's shape but ceil(K / block_size)
+    along the contraction dim kdim, a power-of-two block size >= 8."""
+    if t.dtype != torch.bfloat16 or not t.is_cuda or t.dim() < 2:
+        return False
+    if code is not None and (code.dim() != 1 or not 1 <= code.numel() <= 256):
+        return False
+    if scale is not None:
+        if block_size is None or block_size < 8 or block_size & (block_size - 1) or scale.dtype != torch.bfloat16:
+            return False
+        want = list(t.shape)
+        want[kdim] = -(-want[kdim] // block_size)
+        if list(scale.shape) != want or scale.device != t.device:
+            return False
+    return True
+
+
+def _coded(*parts):
+    """Whether any operand carries a code table or scales (a product of two
+    plain bf16 operands is the library GEMM's)."""
+    return any(p is not None for p in parts)
+
+
+def _aligned16(t):
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _mx_operand(data, code, scale, block_size, k_major, batch_stride, ld, scale_batch_stride, scale_ld):
+    op = _lib.VqxMxOperand()
+    op.data = data.data_ptr()
+    op.scale = None if scale is None else scale.data_ptr()
+    op.code = None if code is None else code.data_ptr()
+    op.batch_stride, op.ld = batch_stride, ld
+    op.scale_batch_stride, op.scale_ld = scale_batch_stride, scale_ld
+    op.k_major = 1 if k_major else 0
+    op.block_size = 0 if scale is None else int(block_size)
+    op.code_len = 0 if code is None else code.numel()
+    return op
+
+
+def _right_operand(b, code, scale, block_size, stored_kn):
+    """Descriptor pieces of the right operand [*, K, N] (stored_kn) or
+    [*, N, K]: K-major when K is the contiguous dim in memory, else N-major;
+    the scales laid out to match.  Returns (data, scale, k_major, ld, K, N)."""
+    K, N = (b.shape[-2], b.shape[-1]) if stored_kn else (b.shape[-1], b.shape[-2])
+    # the memory order: which of the last two dims is contiguous
+    kn = b if stored_kn else b.transpose(-2, -1)   # logical [*, K, N]
+    if kn.transpose(-2, -1).is_contiguous() and not kn.is_contiguous():
+        k_major = True
+    elif kn.is_contiguous():
+        k_major = False
+    else:
+        k_major = not stored_kn
+    if k_major:
+        data = _aligned16(kn.transpose(-2, -1))    # [*, N, K]
+        s = None if scale is None else (scale.transpose(-2, -1) if stored_kn else scale).contiguous()
+        ld = K
+    else:
+        data = _aligned16(kn)                      # [*, K, N]
+        s = None if scale is None else _aligned16(scale if stored_kn else scale.transpose(-2, -1))
+        ld = N
+    return data, s, k_major, ld, K, N
+
+
+def _mx_product(a, a_code, a_scale, b, b_code, b_scale, block_size, b_stored_kn, bias):
+    """A'[*, M, K] . B' through vqx_mx_matmul, or None when the operands fall
+    outside it.  b: [*, K, N] when b_stored_kn, else [*, N, K]; batch dims
+    equal, or one side without them."""
+    if not (_mx_side_ok(a, a_code, a_scale, block_size, -1)
+            and _mx_side_ok(b, b_code, b_scale, block_size, -2 if b_stored_kn else -1)):
+        return None
+    M, K = a.shape[-2], a.shape[-1]
+    Kb, N = (b.shape[-2], b.shape[-1]) if b_stored_kn else (b.shape[-1], b.shape[-2])
+    if Kb != K or M < 1 or N < 1 or K < 1 or K % 8 or N % 4:
+        return None
+    if bias is not None and (bias.dtype != torch.bfloat16 or tuple(bias.shape) != (N,) or bias.device != a.device):
+        return None
+    ba, bb = tuple(a.shape[:-2]), tuple(b.shape[:-2])
+    if ba == bb:
+        batch_shape, a_shared, b_shared = ba, False, False
+    elif len(bb) == 0:
+        batch_shape, a_shared, b_shared = ba, False, True
+    elif len(ba) == 0:
+        batch_shape, a_shared, b_shared = bb, True, False
+    else:
+        return None
+    batch = math.prod(batch_shape)
+    if batch < 1:
+        return None
+    bd, bs_, bk_major, bld, _, _ = _right_operand(b, b_code, b_scale, block_size, b_stored_kn)
+    if not bk_major and N % 8:
+        return None
+    nkb = 0 if a_scale is None else a_scale.shape[-1]
+    if b_shared and not a_shared:
+        # one right matrix for every item: the items' rows run as one product
+        ad = _aligned16(a).reshape(-1, K)
+        asc = None if a_scale is None else a_scale.contiguous().reshape(-1, nkb)
+        rows, nbatch = ad.shape[0], 1
+    else:
+        ad = _aligned16(a)
+        asc = None if a_scale is None else a_scale.contiguous()
+        rows, nbatch = M, batch
+    dev = a.device
+    ac = None if a_code is None else _code_bf16(a_code, dev)
+    bc = None if b_code is None else _code_bf16(b_code, dev)
+    opa = _mx_operand(ad, ac, asc, block_size, True, 0 if (a_shared or nbatch == 1) else M * K, K,
+                      0 if (asc is None or a_shared or nbatch == 1) else M * nkb, nkb)
+    if bk_major:
+        s_b = 0 if bs_ is None else bs_.shape[-1] * N
+        s_ld = 0 if bs_ is None else bs_.shape[-1]
+    else:
+        s_b = 0 if bs_ is None else bs_.shape[-2] * N
+        s_ld = N
+    opb = _mx_operand(bd, bc, bs_, block_size, bk_major, 0 if b_shared else K * N, bld,
+                      0 if (bs_ is None or b_shared) else s_b, s_ld)
+    bias_c = None if bias is None else bias.contiguous()
+    if bias_c is not None and bias_c.data_ptr() % 8:
+        bias_c = bias_c.clone()
+    out = torch.empty(nbatch, rows, N, dtype=torch.bfloat16, device=dev)
+    _lib.call("vqx_mx_matmul", _lib.ctypes.byref(opa), _lib.ctypes.byref(opb), _lib.ptr(bias_c), _lib.ptr(out),
+              nbatch, rows, N, K, _lib.stream_of(a))
+    return out.reshape(*batch_shape, M, N)
+
+
 @_impl("linear_mx")
 def linear_mx(input, weight, bias=None, *, input_scale=None, weight_scale=None, block_size=None,
               input_code=None, weight_code=None, A_data=None, A_indices=None, A_indptr=None,
               weight_layout="kc"):
-    """quantized.py:295-348.  A convert-format weight (bf16 indices, up to 16
-    bf16 levels, bf16 scales in blocks of 64 along K) with bf16 activations
-    runs the fused NF4-style product; anything else decodes on the GPU and
+    """quantized.py:295-348.  A convert-format weight of up to 16 levels with
+    blocks of 64 along K runs the packed-weight product (the activations
+    decoded first); other bf16 convert-format operands run the product that
+    decodes both inside the kernel; anything else decodes on the GPU and
     calls the library GEMM."""
     assert weight_layout in ("kc", "ck"), weight_layout
     _lib.require_device(input, "linear_mx")
-    x = _decode_operand(input, input_code, input_scale, block_size)
     transposed = weight_layout == "ck"
     dense = None
-    if _fusable(x, weight, bias, weight_scale, block_size, weight_code, transposed):
-        dense = _fused_linear(x, weight, bias, weight_scale, weight_code, transposed)
+    x = None
+    if weight_code is not None and weight_code.numel() <= 16:
+        x = _decode_operand(input, input_code, input_scale, block_size)
+        if _fusable(x, weight, bias, weight_scale, block_size, weight_code, transposed):
+            dense = _fused_linear(x, weight, bias, weight_scale, weight_code, transposed)
+    if dense is None and _coded(input_code, input_scale, weight_code, weight_scale) and input.dim() >= 1 \
+            and weight.dim() == 2 and input.shape[-1] > 0 and (
+                input_scale is None or tuple(input_scale.shape[:-1]) == tuple(input.shape[:-1])):
+        # the activation's rows as one [M, K] product
+        K = input.shape[-1]
+        a = input.reshape(-1, K)
+        s = None if input_scale is None else input_scale.reshape(a.shape[0], input_scale.shape[-1])
+        dense = _mx_product(a, input_code, s, weight, weight_code, weight_scale, block_size, transposed, bias)
+        if dense is not None:
+            dense = dense.reshape(*input.shape[:-1], dense.shape[-1])
     if dense is None:
+        if x is None:
+            x = _decode_operand(input, input_code, input_scale, block_size)
         w = _decode_operand(weight, weight_code, weight_scale, block_size)
         if weight_layout == "kc":
             dense = torch.nn.functional.linear(x, w, bias)
@@ -791,16 +953,26 @@ def linear_mx(input, weight, bias=None, *, input_scale=None, weight_scale=None, 
 def matmul_mx(self, other, *, input_scale=None, weight_scale=None, block_size=None, input_code=None,
               weight_code=None, A_data=None, A_indices=None, A_indptr=None, weight_layout="ck"):
     """quantized.py:371-421.  A 2-D convert-format right operand ([K, N] for
-    "ck", [N, K] for "kc") with bf16 left operands runs the fused product, as
-    in linear_mx; anything else decodes and calls the library GEMM."""
+    "ck", [N, K] for "kc") of up to 16 levels with blocks of 64 runs the
+    packed-weight product, as in linear_mx; other bf16 convert-format
+    operands (both sides coded, batched, as the attention products are) run
+    the product that decodes both inside the kernel; anything else decodes
+    and calls the library GEMM."""
     assert weight_layout in ("kc", "ck"), weight_layout
     _lib.require_device(self, "matmul_mx")
-    a = _decode_operand(self, input_code, input_scale, block_size)
     transposed = weight_layout == "ck"
     dense = None
-    if a.dim() >= 1 and _fusable(a, other, None, weight_scale, block_size, weight_code, transposed):
-        dense = _fused_linear(a, other, None, weight_scale, weight_code, transposed)
+    a = None
+    if weight_code is not None and weight_code.numel() <= 16 and other.dim() == 2:
+        a = _decode_operand(self, input_code, input_scale, block_size)
+        if a.dim() >= 1 and _fusable(a, other, None, weight_scale, block_size, weight_code, transposed):
+            dense = _fused_linear(a, other, None, weight_scale, weight_code, transposed)
+    if dense is None and _coded(input_code, input_scale, weight_code, weight_scale):
+        dense = _mx_product(self, input_code, input_scale, other, weight_code, weight_scale, block_size,
+                            transposed, None)
     if dense is None:
+        if a is None:
+            a = _decode_operand(self, input_code, input_scale, block_size)
         b = _decode_operand(other, weight_code, weight_scale, block_size)
         if weight_layout == "ck":
             dense = torch.matmul(a, b.contiguous())
