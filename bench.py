@@ -488,21 +488,28 @@ def setup_c5_skinny(vqx, torch, L, M, N=11008):
         bound="hbm", dtype="bf16", keep=(A, codes, sc, lv, out), cpu=cpu_c5(torch, Ac, N))
 
 
-def _mx_desc(L, data, scale, code, k_major, bstride, ld, sbstride, sld, bs):
-    o = L.VqxMxOperand()
-    o.data = data.data_ptr()
-    o.scale = None if scale is None else scale.data_ptr()
-    o.code = None if code is None else code.data_ptr()
-    o.batch_stride, o.ld, o.scale_batch_stride, o.scale_ld = bstride, ld, sbstride, sld
-    o.k_major, o.block_size = k_major, bs
-    o.code_len = 0 if code is None else code.numel()
-    return o
-
-
 def _e5m3_scales(torch, g, shape):
     e = torch.randint(-10, 1, shape, generator=g).float()
     m = torch.randint(0, 8, shape, generator=g).float()
     return (torch.exp2(e) * (1 + m / 8)).to(torch.bfloat16).cuda()
+
+
+def _graph_of(torch, op):
+    """One call of `op` captured in a HIP graph (after a warm-up call that
+    fills the host caches), replayed once per step: the step is exactly the
+    GPU work the op launches, without its host dispatch."""
+    op()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = op()
+    torch.cuda.synchronize()
+
+    def launch():
+        g.replay()
+        return 0
+
+    return launch, (g, out)
 
 
 def setup_c6_attention(vqx, torch, L, which, coded=False):
@@ -510,59 +517,54 @@ def setup_c6_attention(vqx, torch, L, which, coded=False):
     2048 positions, head dim 128) with the reference's attention specs:
     int6 operands (or nf4_6 indices with the 16-entry code), the left one
     blocked along -1 and the right one along -2 (the contraction dim), bf16
-    scales on the fp8_e5m3 grid; both decoded inside the kernel
-    (vqx_mx_matmul, what quantized_ops::matmul_mx runs for them).  qk:
-    [32,2048,128] x [32,128,2048]; pv: [32,2048,2048] x [32,2048,128], the
-    right operand N-major ([K][N]) in both."""
+    scales on the fp8_e5m3 grid, through quantized_ops::matmul_mx (graph
+    replay of one call: the decode of the operands that many tiles read, then
+    vqx_mx_matmul).  qk: [1,32,2048,128] x [1,32,128,2048]; pv:
+    [1,32,2048,2048] x [1,32,2048,128]."""
     g = torch.Generator().manual_seed(6)
     H, S, D, bs = 32, 2048, 128, 64
     hi, lo = (16, 0) if coded else (32, -32)
     M, N, K = (S, S, D) if which == "qk" else (S, D, S)
-    a = torch.randint(lo, hi, (H, M, K), generator=g).to(torch.bfloat16).cuda()
-    b = torch.randint(lo, hi, (H, K, N), generator=g).to(torch.bfloat16).cuda()
-    a_s = _e5m3_scales(torch, g, (H, M, K // bs))
-    b_s = _e5m3_scales(torch, g, (H, K // bs, N))
+    a = torch.randint(lo, hi, (1, H, M, K), generator=g).to(torch.bfloat16).cuda()
+    b = torch.randint(lo, hi, (1, H, K, N), generator=g).to(torch.bfloat16).cuda()
+    a_s = _e5m3_scales(torch, g, (1, H, M, K // bs))
+    b_s = _e5m3_scales(torch, g, (1, H, K // bs, N))
     code = None
     if coded:
         code = torch.tensor([-31., -22., -16., -12., -9., -6., -3., 0., 2., 5., 8., 10., 14., 17., 22., 31.],
                             dtype=torch.bfloat16, device="cuda")
-    out = torch.empty(H, M, N, dtype=torch.bfloat16, device="cuda")
-    oa = _mx_desc(L, a, a_s, code, 1, M * K, K, M * (K // bs), K // bs, bs)
-    ob = _mx_desc(L, b, b_s, code, 0, K * N, N, (K // bs) * N, N, bs)
-    fn = L.load().vqx_mx_matmul
-    import ctypes
-    args = (ctypes.byref(oa), ctypes.byref(ob), None, L.ptr(out), H, M, N, K, L.stream_of(a))
+    Q = torch.ops.quantized_ops
+    launch, keep = _graph_of(torch, lambda: Q.matmul_mx(a, b, input_scale=a_s, weight_scale=b_s, block_size=bs,
+                                                        input_code=code, weight_code=code))
     fmt = "nf4_6 indices + 16-entry code" if coded else "int6"
     nbytes = 2 * H * (M * K + K * N + M * (K // bs) + (K // bs) * N + M * N)
-    return [lambda: fn(*args)], dict(
-        name=f"C6 attention {which.upper()} of LLaMA-7B through vqx_mx_matmul: [32,{M},{K}] x [32,{K},{N}] "
-             f"({fmt}, bf16 fp8_e5m3-grid scales per 64 along K on both sides, decoded in the kernel) -> bf16",
+    return [launch], dict(
+        name=f"C6 attention {which.upper()} of LLaMA-7B through quantized_ops::matmul_mx: [1,32,{M},{K}] x "
+             f"[1,32,{K},{N}] ({fmt}, bf16 fp8_e5m3-grid scales per 64 along K on both sides) -> bf16; one call "
+             f"replayed from a HIP graph",
         elements=H * M * N, flops=2 * H * M * N * K, bytes=nbytes, bound="hbm", dtype="bf16",
-        keep=(a, b, a_s, b_s, code, out, oa, ob))
+        keep=(a, b, a_s, b_s, code, keep))
 
 
 def setup_c6_mxint8_linear(vqx, torch, L, M=2048, N=11008, K=4096):
-    """The MXINT8 CI scheme's linear at the LLaMA-7B MLP shape: int8
-    activations and weights (integer-valued bf16, as convert writes them),
-    power-of-two bf16 scales per 16 along K on both sides, decoded inside
-    the kernel (vqx_mx_matmul, what quantized_ops::linear_mx runs for them)."""
+    """The MXINT8 CI scheme's linear at the LLaMA-7B MLP shape through
+    quantized_ops::linear_mx: int8 activations and weights (integer-valued
+    bf16, as convert writes them), power-of-two bf16 scales per 16 along K on
+    both sides (graph replay of one call: the activation's decode, the
+    product; the weight's decode is cached per weight)."""
     g = torch.Generator().manual_seed(7)
     bs = 16
     x = torch.randint(-127, 128, (M, K), generator=g).to(torch.bfloat16).cuda()
     w = torch.randint(-127, 128, (N, K), generator=g).to(torch.bfloat16).cuda()
     xs = torch.exp2(torch.randint(-12, -4, (M, K // bs), generator=g).float()).to(torch.bfloat16).cuda()
     ws = torch.exp2(torch.randint(-12, -4, (N, K // bs), generator=g).float()).to(torch.bfloat16).cuda()
-    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-    oa = _mx_desc(L, x, xs, None, 1, 0, K, 0, K // bs, bs)
-    ob = _mx_desc(L, w, ws, None, 1, 0, K, 0, K // bs, bs)
-    fn = L.load().vqx_mx_matmul
-    import ctypes
-    args = (ctypes.byref(oa), ctypes.byref(ob), None, L.ptr(out), 1, M, N, K, L.stream_of(x))
-    return [lambda: fn(*args)], dict(
-        name=f"C6 MXINT8 linear through vqx_mx_matmul: int8 A [{M},{K}] x int8 W [{N},{K}]^T, bf16 power-of-two "
-             f"scales per 16 along K on both sides, decoded in the kernel -> bf16",
+    Q = torch.ops.quantized_ops
+    launch, keep = _graph_of(torch, lambda: Q.linear_mx(x, w, None, input_scale=xs, weight_scale=ws, block_size=bs))
+    return [launch], dict(
+        name=f"C6 MXINT8 linear through quantized_ops::linear_mx: int8 A [{M},{K}] x int8 W [{N},{K}]^T, bf16 "
+             f"power-of-two scales per 16 along K on both sides -> bf16; one call replayed from a HIP graph",
         elements=M * N, flops=2 * M * N * K, bytes=2 * (M * K + N * K + (M + N) * (K // bs) + M * N),
-        bound="mfma", dtype="bf16", keep=(x, w, xs, ws, out, oa, ob))
+        bound="mfma", dtype="bf16", keep=(x, w, xs, ws, keep))
 
 
 def setup_c6_dense_library(vqx, torch, L, which):

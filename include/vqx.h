@@ -430,6 +430,18 @@ int vqx_mx_matmul(const VqxMxOperand* a, const VqxMxOperand* b, const uint16_t* 
                   int64_t batch, int64_t M, int64_t N, int64_t K, vqx_stream_t stream);
 
 /*
+ * The operand decode of linear_mx / matmul_mx (src/vc/ops/quantized.py:
+ * 313-326, 388-398) on its own: x (a VqxMxOperand: k_major = 1 for
+ * [rows][K], 0 for [K][rows]) decoded to dense bf16 in the same layout,
+ * out contiguous [batch][rows][K] or [batch][K][rows] (16-byte aligned).
+ * The host runs it ahead of vqx_mx_matmul for an operand that many output
+ * tiles read (decoding once instead of once per tile).  K % 8 == 0;
+ * rows % 8 == 0 when k_major = 0.
+ */
+int vqx_mx_operand_decode(const VqxMxOperand* x, int64_t batch, int64_t rows, int64_t K, uint16_t* out,
+                          vqx_stream_t stream);
+
+/*
  * quantized_ops::filter_outlier (src/vc/ops/quantized.py:532-630, with
  * _pad_csr at :537-569), and the outlier half of quantize_mx_outlier
  * (:633-712, indptr_offset added to the row pointers).

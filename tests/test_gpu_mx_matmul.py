@@ -17,6 +17,7 @@ import torch
 
 from oracle import formats as F
 from oracle import reference_ops as R
+from tests.conftest import assert_bitexact
 from tests.test_gpu_linear_mx_fused import fused_only, within_tolerance
 
 Q = torch.ops.quantized_ops
@@ -291,3 +292,73 @@ def test_mx_matmul_c_abi_rejects_bad_shapes(vqx):
         run(op(a, 1, 24, s, 12, 3), op(b.t().contiguous(), 1, 24), 16, 12, 24)
     run(op(a, 1, 24), op(b.t().contiguous(), 1, 24), 16, 12, 24)
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["kmajor_code_scale", "nmajor_scale", "kt_view_code", "kc_view_scale_bs16",
+                                  "code_only", "scale_only_wide"])
+def test_mx_decode_is_the_reference_decode_bit_for_bit(vqx, case):
+    """vqx_mx_operand_decode (the decode the host runs ahead of the product for an
+    operand that many tiles read) against the oracle's decode of
+    linear_mx / matmul_mx, bit for bit: code lookup by truncated index
+    (negative from the end, out of range NaN), then bf16(value * scale)."""
+    from importlib import import_module
+
+    qops = import_module(vqx.__name__ + ".ops.quantized")
+    code = torch.linspace(-2, 2, 20).to(torch.bfloat16)
+    g = gen(91)
+    bs, kdim, use_code, use_scale = 32, -1, True, True
+    if case == "kmajor_code_scale":
+        shape = (3, 40, 96)
+    elif case == "nmajor_scale":
+        shape, kdim, use_code = (2, 96, 48), -2, False
+    elif case == "kt_view_code":
+        shape, kdim = (2, 48, 96), -2            # logical [*, K, N], stored as [*, N, K]
+    elif case == "kc_view_scale_bs16":
+        shape, bs, use_code = (2, 96, 40), 16, False   # logical [*, N, K], stored [*, K, N]
+    elif case == "code_only":
+        shape, use_scale = (5, 64), False
+    else:
+        shape, bs, use_code = (4, 4096), 64, False
+    raw = torch.randint(-20, 20, shape, generator=g).float()
+    raw = raw + 0.5 * (torch.rand(shape, generator=g) < 0.2)
+    if use_code:
+        raw.view(-1)[7] = 20.0                   # past the table: NaN
+    t = raw.to(torch.bfloat16)
+    sshape = list(shape)
+    sshape[kdim] = -(-shape[kdim] // bs)
+    scale = e5m3_scales(tuple(sshape), 92) if use_scale else None
+    if case == "kt_view_code":
+        t = t.transpose(-2, -1).contiguous().transpose(-2, -1)
+        scale = scale.transpose(-2, -1).contiguous().transpose(-2, -1)
+    if case == "kc_view_scale_bs16":
+        t = t.transpose(-2, -1).contiguous().transpose(-2, -1)
+        scale = scale.transpose(-2, -1).contiguous().transpose(-2, -1)
+    if use_code:
+        # the reference raises IndexError on the index past the table; the
+        # decode gives NaN there and the reference's values elsewhere
+        bad = t.float().trunc() >= 20
+        want = R._decode_mx(torch.where(bad, torch.zeros_like(t), t), code, scale, bs)
+        want = torch.where(bad, torch.full_like(want, float("nan")), want)
+    else:
+        want = R._decode_mx(t, None, scale, bs)
+    got = qops._mx_decoded(t.cuda(), code.cuda() if use_code else None, None if scale is None else scale.cuda(), bs,
+                           kdim)
+    assert got.shape == want.shape and got.dtype == torch.bfloat16
+    assert_bitexact(got, want, case)
+
+
+@pytest.mark.gpu
+def test_short_k_ragged_many_tiles(vqx):
+    """K = 72 (a partial second k-step) with blocks of 8, ragged M and N over
+    576 tiles, both operands decoded in the kernel (each read by at most 3
+    tiles)."""
+    print("short-K ragged", flush=True)
+    bs = 8
+    a = int_operand((64, 300, 72), -32, 32, 101)
+    a_s = e5m3_scales((64, 300, 9), 102)
+    b = int_operand((64, 72, 264), -32, 32, 103)
+    b_s = e5m3_scales((64, 9, 264), 104)
+    with fused_only():
+        got = Q.matmul_mx(*cuda(a, b), input_scale=a_s.cuda(), weight_scale=b_s.cuda(), block_size=bs)
+    within_tolerance(got, R.matmul_mx(a, b, b_s, bs, None, a_s, None))

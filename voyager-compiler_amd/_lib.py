@@ -107,6 +107,7 @@ _SIGNATURES = {
     "vqx_nf4_linear_workspace_size": ([_I64, _I64, _I64, ctypes.POINTER(_I64)], ctypes.c_int),
     "vqx_nf4_linear_ws": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P], ctypes.c_int),
     "vqx_mx_matmul": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P], ctypes.c_int),
+    "vqx_mx_operand_decode": ([_P, _I64, _I64, _I64, _P, _P], ctypes.c_int),
     "vqx_nf4_linear_noalloc": ([_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
     "vqx_nf4_pack_weight": ([_P, _I32, _P, _I32, _I64, _I64, _I32, _I32, _P, _P, _P, _P], ctypes.c_int),
     "vqx_filter_outlier": ([_P, _I32, _I64, _I64, _I64, _F, _I64, _I32, _P, _P, _P, _P, _P], ctypes.c_int),

@@ -356,6 +356,13 @@ int vqx_mx_matmul(const VqxMxOperand* a, const VqxMxOperand* b, const uint16_t* 
                  N, K, (hipStream_t)stream);
 }
 
+int vqx_mx_operand_decode(const VqxMxOperand* x, int64_t batch, int64_t rows, int64_t K, uint16_t* out,
+                          vqx_stream_t stream) {
+  g_err[0] = 0;
+  if (!x) return set_error(kErrInvalid, "mx_decode: null operand descriptor");
+  return mx_decode(*reinterpret_cast<const MxOperand*>(x), batch, rows, K, out, (hipStream_t)stream);
+}
+
 int vqx_nf4_pack_weight(const void* weight, int32_t w_dtype, const void* scale, int32_t s_dtype, int64_t N,
                         int64_t K, int32_t transposed, int32_t ncode, uint8_t* codes, float* scale_out,
                         int32_t* bad, vqx_stream_t stream) {

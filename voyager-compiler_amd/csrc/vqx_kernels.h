@@ -213,6 +213,7 @@ struct MxOperand {
 };
 int mx_gemm(const MxOperand& a, const MxOperand& b, const uint16_t* bias, uint16_t* out, int64_t batch, int64_t M,
             int64_t N, int64_t K, hipStream_t st);
+int mx_decode(const MxOperand& x, int64_t batch, int64_t rows, int64_t K, uint16_t* out, hipStream_t st);
 
 // vqx_sparse.hip
 struct CsrDecode {

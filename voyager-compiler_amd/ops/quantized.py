@@ -847,13 +847,89 @@ def _right_operand(b, code, scale, block_size, stored_kn):
     return data, s, k_major, ld, K, N
 
 
-def _mx_product(a, a_code, a_scale, b, b_code, b_scale, block_size, b_stored_kn, bias):
+# An operand that many output tiles read is decoded once, by the vqx decode
+# kernel (dequantize: about 4 bytes of HBM traffic per element), instead of
+# in every tile that reads it (about 2.5 VALU per element per tile, which
+# the product's VALU-bound staging pays in full); the kernel decodes the
+# operands that at most this many 128-wide tiles read, such as the attention
+# probabilities of P V (one column tile).
+_FUSED_DECODE_MAX_TILES = 4
+_DECODED = {}
+
+
+def _release_decoded(key):
+    _DECODED.pop(key, None)
+
+
+def _mx_decoded(t, code, scale, block_size, kdim):
+    """t (bf16, contraction dim kdim = -1 or -2, scales along it) decoded to
+    dense bf16 by vqx_mx_operand_decode, in t's own memory layout; the reference's
+    decode (quantized.py:313-326) through the decode-only pass of the product
+    kernel.  Falls back to the general decode for layouts it does not take."""
+    if t.dim() < 2:
+        return _decode_operand(t, code, scale, block_size)
+    lead = t.shape[:-2]
+    # m: the operand as stored, [*, R, C] contiguous; k_major: K is C
+    tt = t.transpose(-2, -1)
+    if t.is_contiguous():
+        m, flipped = t, False
+    elif tt.is_contiguous():
+        m, flipped = tt, True
+    else:
+        m, flipped = t.contiguous(), False
+    k_major = (kdim == -1) != flipped
+    R, C = m.shape[-2], m.shape[-1]
+    K, cols = (C, R) if k_major else (R, C)
+    if K % 8 or (not k_major and C % 8):
+        return _decode_operand(t, code, scale, block_size)
+    sm = None
+    if scale is not None:
+        sm = scale.transpose(-2, -1) if flipped else scale
+        sm = _aligned16(sm)
+    md = _aligned16(m)
+    batch = math.prod(lead)
+    op = _mx_operand(md, None if code is None else _code_bf16(code, t.device), sm, block_size, k_major,
+                     R * C, C, 0 if sm is None else sm.shape[-2] * sm.shape[-1], 0 if sm is None else sm.shape[-1])
+    out = torch.empty_like(md)
+    _lib.call("vqx_mx_operand_decode", _lib.ctypes.byref(op), batch, cols, K, _lib.ptr(out), _lib.stream_of(t))
+    return out.transpose(-2, -1) if flipped else out
+
+
+def _decoded_weight(weight, code, scale, block_size, kdim):
+    """The bf16 decode of a convert-format weight, cached per weight tensor
+    and rebuilt when the weight, its code or its scale change (version
+    counters), as the packed NF4 weight is."""
+    key = id(weight)
+    deps = (weight, code, scale)
+    versions = tuple(None if t is None else (t.data_ptr(), _lib.version_of(t)) for t in deps)
+    hit = _DECODED.get(key)
+    if hit is not None and hit[1] == versions and all(
+            (r is None and t is None) or (r is not None and r() is t) for r, t in zip(hit[0], deps)):
+        return hit[2]
+    dense = _mx_decoded(weight, code, scale, block_size, kdim)
+    if hit is None:
+        weakref.finalize(weight, _release_decoded, key)
+    _DECODED[key] = (tuple(None if t is None else weakref.ref(t) for t in deps), versions, dense)
+    return dense
+
+
+def _mx_product(a, a_code, a_scale, b, b_code, b_scale, block_size, b_stored_kn, bias, b_static=False):
     """A'[*, M, K] . B' through vqx_mx_matmul, or None when the operands fall
     outside it.  b: [*, K, N] when b_stored_kn, else [*, N, K]; batch dims
-    equal, or one side without them."""
+    equal, or one side without them.  b_static: b is a weight (its decode is
+    cached when it is decoded ahead of the product)."""
     if not (_mx_side_ok(a, a_code, a_scale, block_size, -1)
             and _mx_side_ok(b, b_code, b_scale, block_size, -2 if b_stored_kn else -1)):
         return None
+    N = b.shape[-1] if b_stored_kn else b.shape[-2]
+    if (a_code is not None or a_scale is not None) and -(-N // 128) > _FUSED_DECODE_MAX_TILES:
+        a, a_code, a_scale = _mx_decoded(a, a_code, a_scale, block_size, -1), None, None
+    rows = a.shape[-2] * (math.prod(a.shape[:-2]) if b.dim() == 2 else 1)
+    if (b_code is not None or b_scale is not None) and -(-rows // 128) > _FUSED_DECODE_MAX_TILES:
+        kdim = -2 if b_stored_kn else -1
+        b = _decoded_weight(b, b_code, b_scale, block_size, kdim) if b_static else \
+            _mx_decoded(b, b_code, b_scale, block_size, kdim)
+        b_code, b_scale = None, None
     M, K = a.shape[-2], a.shape[-1]
     Kb, N = (b.shape[-2], b.shape[-1]) if b_stored_kn else (b.shape[-1], b.shape[-2])
     if Kb != K or M < 1 or N < 1 or K < 1 or K % 8 or N % 4:
@@ -932,7 +1008,8 @@ def linear_mx(input, weight, bias=None, *, input_scale=None, weight_scale=None, 
         K = input.shape[-1]
         a = input.reshape(-1, K)
         s = None if input_scale is None else input_scale.reshape(a.shape[0], input_scale.shape[-1])
-        dense = _mx_product(a, input_code, s, weight, weight_code, weight_scale, block_size, transposed, bias)
+        dense = _mx_product(a, input_code, s, weight, weight_code, weight_scale, block_size, transposed, bias,
+                            b_static=True)
         if dense is not None:
             dense = dense.reshape(*input.shape[:-1], dense.shape[-1])
     if dense is None:
