@@ -546,6 +546,31 @@ def setup_c6_attention(vqx, torch, L, which, coded=False):
         keep=(a, b, a_s, b_s, code, keep))
 
 
+def setup_c6_mxnf4_linear(vqx, torch, L, M=2048, N=11008, K=4096):
+    """The MXNF4 CI scheme's linear at the LLaMA-7B MLP shape through
+    quantized_ops::linear_mx: nf4_6 activation indices with input_code and
+    fp8_e5m3-grid input_scale per 64 along K, a convert-format nf4_6 weight
+    (16-entry weight_code, weight_scale per 64): the activation's decode pass,
+    then the packed-weight product (graph replay of one call; the weight is
+    packed once, cached)."""
+    g = torch.Generator().manual_seed(8)
+    bs = 64
+    code = torch.tensor([-31., -22., -16., -12., -9., -6., -3., 0., 2., 5., 8., 10., 14., 17., 22., 31.],
+                        dtype=torch.bfloat16, device="cuda")
+    x = torch.randint(0, 16, (M, K), generator=g).to(torch.bfloat16).cuda()
+    w = torch.randint(0, 16, (N, K), generator=g).to(torch.bfloat16).cuda()
+    xs = _e5m3_scales(torch, g, (M, K // bs))
+    ws = _e5m3_scales(torch, g, (N, K // bs))
+    Q = torch.ops.quantized_ops
+    launch, keep = _graph_of(torch, lambda: Q.linear_mx(x, w, None, input_scale=xs, weight_scale=ws, block_size=bs,
+                                                        input_code=code, weight_code=code))
+    return [launch], dict(
+        name=f"C6 MXNF4 linear through quantized_ops::linear_mx: nf4_6 A indices [{M},{K}] + input_code + "
+             f"input_scale, nf4_6 W [{N},{K}] convert format, blocks of 64 -> bf16; one call replayed from a HIP graph",
+        elements=M * N, flops=2 * M * N * K, bytes=2 * M * K + N * K // 2 + 2 * (M + N) * (K // bs) + 2 * M * N,
+        bound="mfma", dtype="bf16", keep=(x, w, xs, ws, code, keep))
+
+
 def setup_c6_mxint8_linear(vqx, torch, L, M=2048, N=11008, K=4096):
     """The MXINT8 CI scheme's linear at the LLaMA-7B MLP shape through
     quantized_ops::linear_mx: int8 activations and weights (integer-valued
@@ -846,7 +871,6 @@ CONFIGS = {
     "g1_gptq": lambda v, t, L: setup_g1(v, t, L),
     "c6_attn_qk_int6": lambda v, t, L: setup_c6_attention(v, t, L, "qk"),
     "c6_attn_pv_int6": lambda v, t, L: setup_c6_attention(v, t, L, "pv"),
-    "c6_attn_qk_nf4_6": lambda v, t, L: setup_c6_attention(v, t, L, "qk", coded=True),
     "c6_mxint8_linear": lambda v, t, L: setup_c6_mxint8_linear(v, t, L),
 }
 HEADLINE = "c2"
@@ -1001,6 +1025,8 @@ ON_REQUEST = {
     "c5_m256_whole_tiles": lambda v, t, L: setup_c5(v, t, L, whole_tiles=True, M=256),
     "c5_dense_library": lambda v, t, L: setup_c5_dense_library(v, t, L),
     "c5_dense_library_n8192": lambda v, t, L: setup_c5_dense_library(v, t, L, N=8192),
+    "c6_attn_qk_nf4_6": lambda v, t, L: setup_c6_attention(v, t, L, "qk", coded=True),
+    "c6_mxnf4_linear": lambda v, t, L: setup_c6_mxnf4_linear(v, t, L),
     "c6_qk_dense_library": lambda v, t, L: setup_c6_dense_library(v, t, L, "qk"),
     "c6_pv_dense_library": lambda v, t, L: setup_c6_dense_library(v, t, L, "pv"),
     "c6_linear_dense_library": lambda v, t, L: setup_c6_dense_library(v, t, L, "linear"),
@@ -1033,10 +1059,9 @@ DOMINANT = {
     "g1_gptq": "gptq_block_kernel",
     "f1_outlier_opct": "mx_lut_kernel<0, 4, true, 2, false, true>",
     "f1_outlier_othr_ax2": "mx_block_kernel<unsigned short, vqx::EncLevels>",
-    "c6_attn_qk_int6": "mx_gemm_kernel<1, 1, false>",
-    "c6_attn_pv_int6": "mx_gemm_kernel<1, 1, false>",
-    "c6_attn_qk_nf4_6": "mx_gemm_kernel<3, 3, false>",
-    "c6_mxint8_linear": "mx_gemm_kernel<1, 1, true>",
+    "c6_attn_qk_int6": "mx_gemm_kernel<0, 0, false, 128, 128>",
+    "c6_attn_pv_int6": "mx_gemm_kernel<1, 0, false, 128, 128>",
+    "c6_mxint8_linear": "mx_gemm_kernel<0, 0, true, 256, 128>",
 }
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
 

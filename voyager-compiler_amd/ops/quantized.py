@@ -895,6 +895,20 @@ def _mx_decoded(t, code, scale, block_size, kdim):
     return out.transpose(-2, -1) if flipped else out
 
 
+def _activation_decoded(x, code, scale, block_size):
+    """The left operand's decode ahead of the packed-weight product: the
+    streaming decode pass when it takes the operand (bf16, scales along the
+    last dim), else the general decode."""
+    if (code is not None or scale is not None) and x.dim() >= 1 and x.shape[-1] % 8 == 0 and x.numel() > 0:
+        x2 = x.reshape(-1, x.shape[-1])
+        s2 = None
+        if scale is not None and scale.dim() == x.dim() and tuple(scale.shape[:-1]) == tuple(x.shape[:-1]):
+            s2 = scale.reshape(-1, scale.shape[-1])
+        if (scale is None or s2 is not None) and _mx_side_ok(x2, code, s2, block_size, -1):
+            return _mx_decoded(x2, code, s2, block_size, -1).reshape(x.shape)
+    return _decode_operand(x, code, scale, block_size)
+
+
 def _decoded_weight(weight, code, scale, block_size, kdim):
     """The bf16 decode of a convert-format weight, cached per weight tensor
     and rebuilt when the weight, its code or its scale change (version
@@ -998,7 +1012,7 @@ def linear_mx(input, weight, bias=None, *, input_scale=None, weight_scale=None, 
     dense = None
     x = None
     if weight_code is not None and weight_code.numel() <= 16:
-        x = _decode_operand(input, input_code, input_scale, block_size)
+        x = _activation_decoded(input, input_code, input_scale, block_size)
         if _fusable(x, weight, bias, weight_scale, block_size, weight_code, transposed):
             dense = _fused_linear(x, weight, bias, weight_scale, weight_code, transposed)
     if dense is None and _coded(input_code, input_scale, weight_code, weight_scale) and input.dim() >= 1 \
@@ -1041,7 +1055,7 @@ def matmul_mx(self, other, *, input_scale=None, weight_scale=None, block_size=No
     dense = None
     a = None
     if weight_code is not None and weight_code.numel() <= 16 and other.dim() == 2:
-        a = _decode_operand(self, input_code, input_scale, block_size)
+        a = _activation_decoded(self, input_code, input_scale, block_size)
         if a.dim() >= 1 and _fusable(a, other, None, weight_scale, block_size, weight_code, transposed):
             dense = _fused_linear(a, other, None, weight_scale, weight_code, transposed)
     if dense is None and _coded(input_code, input_scale, weight_code, weight_scale):
