@@ -1106,6 +1106,169 @@ static int launch_lut_k(const uint16_t* x, int64_t ngroups, const ScaleParams& s
   return check_launch("mx_quantize(lut)");
 }
 
+// Blocks along a middle axis of a bf16 input, table-driven: the layout and
+// per-column block scales of mx_cols_kernel, the per-element path of
+// mx_lut_kernel.  A persistent workgroup copies the format's compact table
+// (value | code << 16 per magnitude, both signs) into LDS once; a column's
+// block whose scale passes the same checks as mx_lut_kernel's fast path
+// (ABSMAX: x * rcp(s) rounds to the bf16 of the reference's x / s, as x and s
+// are bf16 values; power-of-two scales: an exact scaling) takes a clamp and
+// one LDS read per element, any other block the exact division and the full
+// table.  Outputs and outlier handling as mx_cols_kernel.
+template <bool ABSMAX>
+__global__ __launch_bounds__(256) void mx_cols_lut_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t L,
+                                                          int64_t inner, int bs, ScaleParams sp, LutView lv,
+                                                          MxOut out, int code_bytes, OutlierArgs oa) {
+  constexpr int VE = 8;
+  constexpr int TW = kColChunks * VE;
+  extern __shared__ uint32_t lds_lut[];
+  __shared__ uint32_t s_amax[256 / kColChunks][TW];
+  __shared__ float s_scale[TW];
+  __shared__ uint32_t s_cmax[TW];
+  __shared__ uint8_t thr8[256];
+  if constexpr (!ABSMAX)
+    for (int i = threadIdx.x; i < 256; i += blockDim.x) thr8[i] = (uint8_t)log2_step_threshold(i);
+  const LutLds t = lut_to_lds(lv.blob, lv.len, lds_lut);
+  const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
+  const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - 4u * t.t0m1;
+  const uint32_t nb = pb + 4u * t.len;
+  const float lo = u2f(t.t0m1 << 16), hi = u2f(t.t1 << 16);
+  const int tid = threadIdx.x, cg = tid % kColChunks, rg = tid / kColChunks;
+  const int64_t nblk = (L + bs - 1) / bs;
+  const int64_t ntc = (inner + TW - 1) / TW;
+  const int64_t ntiles = outer * nblk * ntc;
+  const uint32_t bound = outlier_bound_t<uint16_t>(oa);
+  uint32_t nskip = 0;
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t tc = tile % ntc, rest = tile / ntc;
+    const int64_t bl = rest % nblk, o = rest / nblk;
+    const int64_t l0 = bl * bs;
+    const int64_t col = tc * TW + (int64_t)cg * VE;
+    const bool cok = col < inner;
+    uint32_t v[kColRowsMax][VE];
+    uint32_t skip[kColRowsMax];
+    uint32_t m[VE];
+#pragma unroll
+    for (int e = 0; e < VE; ++e) m[e] = 0;
+#pragma unroll
+    for (int i = 0; i < kColRowsMax; ++i) {
+      const int r = rg + 16 * i;
+      const int64_t l = l0 + r;
+      skip[i] = 0;
+      if (r < bs && l < L && cok) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(x + (o * L + l) * inner + col);
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+          const uint32_t b = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          v[i][e] = b;
+          const bool sk = outlier_skip(b & 0x7FFFu, bound, 0x7F80u);
+          skip[i] |= (uint32_t)sk << e;
+          m[e] = umax32(m[e], sk ? 0u : b & 0x7FFFu);
+        }
+        nskip += __builtin_popcount(skip[i]);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < VE; ++e) s_amax[rg][cg * VE + e] = m[e];
+    __syncthreads();
+    if (tid < TW) {
+      uint32_t a = 0;
+#pragma unroll
+      for (int g = 0; g < 256 / kColChunks; ++g) a = umax32(a, s_amax[g][tid]);
+      const float sc = block_scale<uint16_t>(a, sp);
+      s_scale[tid] = sc;
+      s_cmax[tid] = a;
+      const int64_t c = tc * TW + tid;
+      if (c < inner) {
+        const int64_t si = (o * nblk + bl) * inner + c;
+        if (out.scale) static_cast<uint16_t*>(out.scale)[si] = (uint16_t)BT<uint16_t>::round_bits(sc);
+        if (out.scale_f32) out.scale_f32[si] = sc;
+        if (out.scale_e8m0) out.scale_e8m0[si] = (uint8_t)e8m0_of(sc);
+      }
+    }
+    __syncthreads();
+    // per column: the scale, its reciprocal, whether the table path holds
+    // for the column's block, and the sign rule (the negative table iff the
+    // fp32 bits of the quotient (ABSMAX) or of x (power of two) > nthr)
+    float s[VE], rcp[VE];
+    bool fast[VE];
+    uint32_t nthr[VE];
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      s[e] = s_scale[cg * VE + e];
+      const uint32_t amax = s_cmax[cg * VE + e];
+      const uint32_t sb = f2u(s[e]), sE = (sb >> 23) & 0xFFu;
+      const float amaxf = u2f(amax << 16);
+      if constexpr (ABSMAX) {
+        rcp[e] = __builtin_amdgcn_rcpf(s[e]);
+        fast[e] = sE >= 2 && sE <= 252 && amax < 0x7F80u && t.t0m1 >= 0x80u && (f2u(amaxf * rcp[e]) >> 16) + 1u < t.s;
+        nthr[e] = t.zsign ? 0x7FFFFFFFu : 0x80008000u;
+      } else {
+        rcp[e] = u2f((254u - sE) << 23);
+        fast[e] = (sb & 0x7FFFFFu) == 0 && sE >= 27 && sE <= 227 && amax < 0x7F80u && t.t0m1 >= 0x80u &&
+                  (f2u(amaxf * rcp[e]) >> 16) < t.s;
+        const int ze = (int)sE - 127 - 134;
+        const float sz = ze >= -149 ? exp2i(ze) : 0.0f;
+        nthr[e] = t.zsign ? 0x7FFFFFFFu : (0x80000000u | f2u(sz));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kColRowsMax; ++i) {
+      const int r = rg + 16 * i;
+      const int64_t l = l0 + r;
+      if (!(r < bs && l < L && cok)) continue;
+      uint32_t qv[VE], fv[VE], cd[VE];
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        const bool sk = (skip[i] >> e) & 1u;  // an outlier: encoded as +0, output unchanged
+        const uint32_t xb = (sk ? 0u : v[i][e]) << 16;
+        uint32_t ent;
+        if (fast[e]) {
+          uint32_t addr;
+          if constexpr (ABSMAX) {
+            const float q = u2f(xb) * rcp[e];
+            const uint32_t h = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(q), lo, hi), 0.0f);
+            addr = (f2u(q) > nthr[e] ? nb : pb) + 4u * h;
+          } else {
+            const float qc = __builtin_amdgcn_fmed3f(__builtin_fabsf(u2f(xb) * rcp[e]), lo, hi);
+            addr = (xb > nthr[e] ? nb : pb) + 4u * (f2u(qc) >> 16);
+          }
+          ent = *(lds_cu32*)(size_t)addr;
+        } else {
+          const float q = u2f(xb) / s[e];
+          uint32_t h = f2bf(q);
+          h = q == q ? h : (h & 0x7FFFu) | ((xb >> 16) & 0x8000u);
+          ent = full[h];
+        }
+        const uint32_t val = ent & 0xFFFFu;
+        qv[e] = val;
+        fv[e] = sk ? v[i][e] : ((ABSMAX || !fast[e]) ? f2bf(u2f(val << 16) * s[e]) : (f2u(u2f(val << 16) * s[e]) >> 16));
+        cd[e] = ent >> 16;
+      }
+      const int64_t base = (o * L + l) * inner + col;
+      auto store = [&](void* p, const uint32_t(&b)[VE]) {
+        u32x4 w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = (b[2 * j] & 0xFFFFu) | (b[2 * j + 1] << 16);
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p) + base) = w;
+      };
+      if (out.qvals) store(out.qvals, qv);
+      if (out.fq) store(out.fq, fv);
+      if (out.codes) {
+        if (code_bytes == 1) {
+#pragma unroll
+          for (int e = 0; e < VE; ++e) static_cast<uint8_t*>(out.codes)[base + e] = (uint8_t)cd[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < VE; ++e) static_cast<uint16_t*>(out.codes)[base + e] = (uint16_t)cd[e];
+        }
+      }
+    }
+    __syncthreads();  // s_amax / s_scale / s_cmax are rewritten by the next tile
+  }
+  outlier_tally(nskip, oa);
+}
+
 // The fake-quant output with outlier masking (mx_lut_kernel's OUTL form).
 template <int LPB, bool ABSMAX>
 static int launch_lut_outlier(const uint16_t* x, int64_t ngroups, const ScaleParams& sp, const LutView& lv,
@@ -1269,6 +1432,25 @@ int mx_quantize(const void* x, int dtype, int64_t outer, int64_t L, int64_t inne
     if (fast) {
       LutView lv{fmt.lut, fmt.lut_len};
       return launch_lut((const uint16_t*)x, n, (int)lpb, packed ? fmt.code_bits : 0, sp, lv, out, st);
+    }
+    // blocks along a middle axis of a bf16 input: the table-driven column kernel
+    const bool cols = dtype == kBF16 && fmt.lut && inner > 1 && inner % 8 == 0 && bs <= 16 * kColRowsMax &&
+                      !packed && (out.codes == nullptr || code_layout == 1 || code_layout == 2) &&
+                      aligned(x, 16) && (!out.qvals || aligned(out.qvals, 16)) && (!out.fq || aligned(out.fq, 16));
+    if (cols) {
+      LutView lv{fmt.lut, fmt.lut_len};
+      const int64_t tiles = outer * ((L + bs - 1) / bs) * ((inner + kColChunks * 8 - 1) / (kColChunks * 8));
+      const size_t lds = sizeof(uint32_t) * 2 * (size_t)lv.len;
+      if (sp.mode == 1) {
+        const unsigned grid = persistent_grid((const void*)mx_cols_lut_kernel<true>, 256, lds, tiles * 256);
+        hipLaunchKernelGGL((mx_cols_lut_kernel<true>), dim3(grid), dim3(256), lds, st, (const uint16_t*)x, outer, L,
+                           inner, (int)bs, sp, lv, out, code_layout, oa);
+      } else {
+        const unsigned grid = persistent_grid((const void*)mx_cols_lut_kernel<false>, 256, lds, tiles * 256);
+        hipLaunchKernelGGL((mx_cols_lut_kernel<false>), dim3(grid), dim3(256), lds, st, (const uint16_t*)x, outer,
+                           L, inner, (int)bs, sp, lv, out, code_layout, oa);
+      }
+      return check_launch("mx_quantize(cols, table)");
     }
   }
   return with_encoder(fmt, [&](auto enc) -> int {
