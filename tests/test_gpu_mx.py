@@ -283,13 +283,14 @@ def test_llama_qconfig_specs(vqx, spec):
 @pytest.mark.gpu
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape,axis,bs", [((4, 100, 24), 1, 32), ((2, 256, 136), 1, 64), ((3, 128, 64), 1, 128),
-                                           ((2, 40, 16), 1, 16), ((64, 200), 0, 32), ((2, 3, 96, 40), 2, 64)])
+                                           ((2, 40, 16), 1, 16), ((64, 200), 0, 32), ((2, 3, 96, 40), 2, 64),
+                                           ((3, 52, 32), 1, 8)])
 @pytest.mark.parametrize("dtype,qmax,pow2", [("fp8_e4m3", 448.0, True), ("nf4_6", 31.0, False),
                                              ("int6", 31.0, False)])
 def test_mx_middle_axis_tiles(vqx, xdt, shape, axis, bs, dtype, qmax, pow2):
     # blocks along a middle (or first) axis whose inner size is a multiple of
     # 16 bytes: the tiled column kernel, with short last blocks, partial
-    # column tiles, every block size up to 128 rows, NaN / Inf / zero /
+    # column tiles, block sizes 8 to 128 rows, NaN / Inf / zero /
     # subnormal elements; quantize_mx values and scales, the fake-quant, and
     # the per-element codes, which decode to the values
     print(f"middle-axis tiles {xdt} {shape} axis={axis} bs={bs} {dtype}", flush=True)

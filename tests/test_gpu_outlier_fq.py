@@ -208,8 +208,9 @@ def test_outlier_other_schemes(vqx):
 @pytest.mark.gpu
 def test_outlier_threshold_edge_values(vqx):
     # a negative threshold makes every non-NaN element an outlier (the
-    # output is the input); one above every |x| none; table (edited qmap)
-    # path of the microscaling kernel
+    # output is the input); one above every |x| none; the same and zero /
+    # mid thresholds for blocks along -2; table (edited qmap) path of the
+    # microscaling kernel
     x = activations((16, 256), torch.bfloat16, seed=50)
     for thr in (-1.0, 1e30):
         fq = spec_module(vqx, f"nf4,qs=microscaling,bs=64,ax=-1,othr={thr}")
@@ -217,6 +218,18 @@ def test_outlier_threshold_edge_values(vqx):
         ora = R.OutlierFakeQuantize(outlier_threshold=thr)
         want = ora(x, lambda xm: R.mx_fake_quantize(xm, table("nf4"), [-1], 64, 1.0, False)[1])
         assert_bitexact(got, want, f"othr={thr}")
+        assert fq.max_outlier_pct == ora.max_outlier_pct
+    # blocks along -2 (the column kernel), with NaN, +-Inf and -0 elements
+    xc = activations((2, 128, 64), torch.bfloat16, seed=51)
+    flat = xc.view(-1)
+    flat[5], flat[700], flat[9000], flat[12345] = float("nan"), float("inf"), float("-inf"), -0.0
+    for thr in (-1.0, 0.0, 2.0, 1e30):
+        fq = spec_module(vqx, f"nf4_6,qs=microscaling,bs=64,ax=-2,scale=fp8_e5m3,othr={thr}")
+        got = fq(xc.cuda()).cpu()
+        ora = R.OutlierFakeQuantize(outlier_threshold=thr)
+        want = ora(xc, lambda xm: R.mx_fake_quantize(xm, table("nf4_6"), [-2], 64, fq.quant_max, False,
+                                                     table("fp8_e5m3"))[1])
+        assert_bitexact(got, want, f"ax=-2 othr={thr}")
         assert fq.max_outlier_pct == ora.max_outlier_pct
     fq = spec_module(vqx, "int8,qs=microscaling,bs=32,ax=-1,othr=3.0")
     fq.qmap.mul_(1.0)  # an in-place edit: the kernels take the table path

@@ -1114,85 +1114,127 @@ static int launch_lut_k(const uint16_t* x, int64_t ngroups, const ScaleParams& s
 // (ABSMAX: x * rcp(s) rounds to the bf16 of the reference's x / s, as x and s
 // are bf16 values; power-of-two scales: an exact scaling) takes a clamp and
 // one LDS read per element, any other block the exact division and the full
-// table.  Outputs and outlier handling as mx_cols_kernel.
-template <bool ABSMAX>
+// table.  Outputs and outlier handling as mx_cols_kernel (OUTL: outlier
+// masking active).
+//
+// A tile is one block by 128 columns; thread (rg, cg) = (tid / 16, tid % 16)
+// holds 16 bytes (8 columns) of rows rg, rg + 16, ... (R rows).  The work is
+// done on bf16 pairs as loaded: block maxima with packed 16-bit maxima,
+// outliers as per-pair masks, two quotients rounded by one conversion, and
+// the fake-quant pair assembled by one conversion (or one byte permute for
+// the exact power-of-two products) and one bit select restoring outliers.
+// A tile's R rows are loaded together, one tile ahead: the next tile's loads
+// are issued once this tile's scales are known (its last global read) and
+// land while it is encoded and stored.  A row outside the block or the
+// tensor, or a chunk past inner, reads the block's first row at column 0
+// (in bounds) and is replaced by zeros before use, so no branch sits between
+// the loads; past the last tile the last one is read again.
+template <bool ABSMAX, int R, bool OUTL>
 __global__ __launch_bounds__(256) void mx_cols_lut_kernel(const uint16_t* __restrict__ x, int64_t outer, int64_t L,
                                                           int64_t inner, int bs, ScaleParams sp, LutView lv,
                                                           MxOut out, int code_bytes, OutlierArgs oa) {
+  static_assert(R >= 1 && R <= kColRowsMax, "rows per thread");
   constexpr int VE = 8;
   constexpr int TW = kColChunks * VE;
   extern __shared__ uint32_t lds_lut[];
-  __shared__ uint32_t s_amax[256 / kColChunks][TW];
+  __shared__ uint32_t s_amax[256 / kColChunks][TW / 2];  // column maxima of each row group, as pairs
   __shared__ float s_scale[TW];
   __shared__ uint32_t s_cmax[TW];
-  __shared__ uint8_t thr8[256];
-  if constexpr (!ABSMAX)
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) thr8[i] = (uint8_t)log2_step_threshold(i);
   const LutLds t = lut_to_lds(lv.blob, lv.len, lds_lut);
   const uint32_t* full = lv.blob + kLutHeaderWords + 2 * kLutMaxLen;
   const uint32_t pb = (uint32_t)(size_t)(lds_cu32*)lds_lut - 4u * t.t0m1;
   const uint32_t nb = pb + 4u * t.len;
   const float lo = u2f(t.t0m1 << 16), hi = u2f(t.t1 << 16);
   const int tid = threadIdx.x, cg = tid % kColChunks, rg = tid / kColChunks;
-  const int64_t nblk = (L + bs - 1) / bs;
-  const int64_t ntc = (inner + TW - 1) / TW;
-  const int64_t ntiles = outer * nblk * ntc;
-  const uint32_t bound = outlier_bound_t<uint16_t>(oa);
+  // tile coordinates in 32-bit arithmetic (the host checks ntiles < 2^31)
+  const uint32_t nblk = (uint32_t)((L + bs - 1) / bs);
+  const uint32_t ntc = (uint32_t)((inner + TW - 1) / TW);
+  const uint32_t ntiles = (uint32_t)(outer * nblk * ntc);
+  // outlier bound on the magnitude bits (0xFFFF: nothing is an outlier)
+  const uint32_t bound = OUTL ? outlier_bound_t<uint16_t>(oa) : 0xFFFFFFFFu;
+  const u16x2 b16 = {(unsigned short)(bound > 0xFFFFu ? 0xFFFFu : bound),
+                     (unsigned short)(bound > 0xFFFFu ? 0xFFFFu : bound)};
   uint32_t nskip = 0;
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t tc = tile % ntc, rest = tile / ntc;
-    const int64_t bl = rest % nblk, o = rest / nblk;
-    const int64_t l0 = bl * bs;
-    const int64_t col = tc * TW + (int64_t)cg * VE;
+  auto load_tile = [&](uint32_t tile, u32x4(&dst)[R]) {
+    const uint32_t tc = tile % ntc, rest = tile / ntc;
+    const uint32_t bl = rest % nblk, o = rest / nblk;
+    const int64_t l0 = (int64_t)bl * bs;
+    const int64_t col = (int64_t)tc * TW + (int64_t)cg * VE;
     const bool cok = col < inner;
-    uint32_t v[kColRowsMax][VE];
-    uint32_t skip[kColRowsMax];
-    uint32_t m[VE];
 #pragma unroll
-    for (int e = 0; e < VE; ++e) m[e] = 0;
+    for (int i = 0; i < R; ++i) {
+      const int64_t l = l0 + rg + 16 * i;
+      const bool ok = rg + 16 * i < bs && l < L;
+      dst[i] = *reinterpret_cast<const u32x4*>(x + ((int64_t)o * L + (ok ? l : l0)) * inner + (cok ? col : 0));
+    }
+  };
+  u32x4 w[R], wn[R];
+  load_tile(blockIdx.x < ntiles ? blockIdx.x : ntiles - 1, w);
+  for (uint32_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const uint32_t tc = tile % ntc, rest = tile / ntc;
+    const uint32_t bl = rest % nblk, o = rest / nblk;
+    const int64_t l0 = (int64_t)bl * bs;
+    const int64_t col = (int64_t)tc * TW + (int64_t)cg * VE;
+    const bool cok = col < inner;
+    bool rok[R];
+    u32x4 mk[R];  // OUTL: 0xFFFF over the outlier halves
+    u16x2 mp[4] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};  // magnitude maxima of columns 2j, 2j + 1
+    u16x2 cnt = {0, 0};                               // outliers among the low / high halves
 #pragma unroll
-    for (int i = 0; i < kColRowsMax; ++i) {
-      const int r = rg + 16 * i;
-      const int64_t l = l0 + r;
-      skip[i] = 0;
-      if (r < bs && l < L && cok) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(x + (o * L + l) * inner + col);
+    for (int i = 0; i < R; ++i) {
+      rok[i] = rg + 16 * i < bs && l0 + rg + 16 * i < L && cok;
 #pragma unroll
-        for (int e = 0; e < VE; ++e) {
-          const uint32_t b = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-          v[i][e] = b;
-          const bool sk = outlier_skip(b & 0x7FFFu, bound, 0x7F80u);
-          skip[i] |= (uint32_t)sk << e;
-          m[e] = umax32(m[e], sk ? 0u : b & 0x7FFFu);
+      for (int j = 0; j < 4; ++j) {
+        w[i][j] = rok[i] ? w[i][j] : 0u;
+        u16x2 mg = __builtin_bit_cast(u16x2, w[i][j] & 0x7FFF7FFFu);
+        if constexpr (OUTL) {
+          // outlier_skip on both halves with packed 16-bit arithmetic:
+          // bound <= mag (mag + 1 - bound > 0) and mag <= 0x7F80 (not NaN),
+          // each a saturating difference, and-ed as 0 / 1 by minima
+          const u16x2 ge = __builtin_elementwise_sub_sat(mg + (u16x2){1, 1}, b16);
+          const u16x2 le = __builtin_elementwise_sub_sat((u16x2){0x7F81, 0x7F81}, mg);
+          u16x2 one = __builtin_elementwise_min(__builtin_elementwise_min(ge, le), (u16x2){1, 1});
+          one = rok[i] ? one : (u16x2){0, 0};  // the zeros standing in for rows or chunks outside
+          cnt += one;
+          mk[i][j] = __builtin_bit_cast(uint32_t, (u16x2){0, 0} - one);
+          mg = __builtin_bit_cast(u16x2, __builtin_bit_cast(uint32_t, mg) & ~mk[i][j]);
+        } else {
+          mk[i][j] = 0u;
         }
-        nskip += __builtin_popcount(skip[i]);
+        mp[j] = __builtin_elementwise_max(mp[j], mg);
       }
     }
+    if constexpr (OUTL) nskip += (uint32_t)cnt.x + (uint32_t)cnt.y;
 #pragma unroll
-    for (int e = 0; e < VE; ++e) s_amax[rg][cg * VE + e] = m[e];
+    for (int j = 0; j < 4; ++j) s_amax[rg][cg * 4 + j] = __builtin_bit_cast(uint32_t, mp[j]);
     __syncthreads();
     if (tid < TW) {
       uint32_t a = 0;
 #pragma unroll
-      for (int g = 0; g < 256 / kColChunks; ++g) a = umax32(a, s_amax[g][tid]);
+      for (int g = 0; g < 256 / kColChunks; ++g) a = umax32(a, (s_amax[g][tid >> 1] >> (16 * (tid & 1))) & 0xFFFFu);
       const float sc = block_scale<uint16_t>(a, sp);
       s_scale[tid] = sc;
       s_cmax[tid] = a;
-      const int64_t c = tc * TW + tid;
+      const int64_t c = (int64_t)tc * TW + tid;
       if (c < inner) {
-        const int64_t si = (o * nblk + bl) * inner + c;
+        const int64_t si = ((int64_t)o * nblk + bl) * inner + c;
         if (out.scale) static_cast<uint16_t*>(out.scale)[si] = (uint16_t)BT<uint16_t>::round_bits(sc);
         if (out.scale_f32) out.scale_f32[si] = sc;
         if (out.scale_e8m0) out.scale_e8m0[si] = (uint8_t)e8m0_of(sc);
       }
     }
     __syncthreads();
+    {
+      const uint32_t next = tile + gridDim.x;  // < 2^32: tile < 2^31, gridDim.x < 2^31
+      load_tile(next < ntiles ? next : ntiles - 1, wn);
+    }
     // per column: the scale, its reciprocal, whether the table path holds
     // for the column's block, and the sign rule (the negative table iff the
     // fp32 bits of the quotient (ABSMAX) or of x (power of two) > nthr)
     float s[VE], rcp[VE];
     bool fast[VE];
     uint32_t nthr[VE];
+    bool all_fast = true;
 #pragma unroll
     for (int e = 0; e < VE; ++e) {
       s[e] = s_scale[cg * VE + e];
@@ -1211,62 +1253,105 @@ __global__ __launch_bounds__(256) void mx_cols_lut_kernel(const uint16_t* __rest
         const float sz = ze >= -149 ? exp2i(ze) : 0.0f;
         nthr[e] = t.zsign ? 0x7FFFFFFFu : (0x80000000u | f2u(sz));
       }
+      rcp[e] = cok ? rcp[e] : 0.0f;  // a chunk past inner: quotients of 0 (its rows are zeros)
+      all_fast = all_fast && fast[e];
     }
+    // Row i's outputs from its eight entries (value | code << 16), as pairs.
+    auto emit = [&](int i, const uint32_t(&ent)[VE]) {
+      u32x4 qv, fv;
 #pragma unroll
-    for (int i = 0; i < kColRowsMax; ++i) {
-      const int r = rg + 16 * i;
-      const int64_t l = l0 + r;
-      if (!(r < bs && l < L && cok)) continue;
-      uint32_t qv[VE], fv[VE], cd[VE];
-#pragma unroll
-      for (int e = 0; e < VE; ++e) {
-        const bool sk = (skip[i] >> e) & 1u;  // an outlier: encoded as +0, output unchanged
-        const uint32_t xb = (sk ? 0u : v[i][e]) << 16;
-        uint32_t ent;
-        if (fast[e]) {
-          uint32_t addr;
-          if constexpr (ABSMAX) {
-            const float q = u2f(xb) * rcp[e];
-            const uint32_t h = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(q), lo, hi), 0.0f);
-            addr = (f2u(q) > nthr[e] ? nb : pb) + 4u * h;
-          } else {
-            const float qc = __builtin_amdgcn_fmed3f(__builtin_fabsf(u2f(xb) * rcp[e]), lo, hi);
-            addr = (xb > nthr[e] ? nb : pb) + 4u * (f2u(qc) >> 16);
-          }
-          ent = *(lds_cu32*)(size_t)addr;
-        } else {
-          const float q = u2f(xb) / s[e];
-          uint32_t h = f2bf(q);
-          h = q == q ? h : (h & 0x7FFFu) | ((xb >> 16) & 0x8000u);
-          ent = full[h];
-        }
-        const uint32_t val = ent & 0xFFFFu;
-        qv[e] = val;
-        fv[e] = sk ? v[i][e] : ((ABSMAX || !fast[e]) ? f2bf(u2f(val << 16) * s[e]) : (f2u(u2f(val << 16) * s[e]) >> 16));
-        cd[e] = ent >> 16;
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t el = ent[2 * j], eh = ent[2 * j + 1];
+        qv[j] = __builtin_amdgcn_perm(eh, el, 0x05040100u);
+        const float vl = u2f(el << 16) * s[2 * j], vh = u2f(eh << 16) * s[2 * j + 1];
+        uint32_t f;
+        if (ABSMAX || !(fast[2 * j] && fast[2 * j + 1]))
+          f = pack_bf16x2(vl, vh);  // RNE (the products are finite: table values times normal scales)
+        else
+          f = __builtin_amdgcn_perm(f2u(vh), f2u(vl), 0x07060302u);  // exact power-of-two products
+        fv[j] = (mk[i][j] & w[i][j]) | (~mk[i][j] & f);  // an outlier keeps its input
       }
-      const int64_t base = (o * L + l) * inner + col;
-      auto store = [&](void* p, const uint32_t(&b)[VE]) {
-        u32x4 w;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = (b[2 * j] & 0xFFFFu) | (b[2 * j + 1] << 16);
-        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p) + base) = w;
-      };
-      if (out.qvals) store(out.qvals, qv);
-      if (out.fq) store(out.fq, fv);
+      const int64_t base = ((int64_t)o * L + l0 + rg + 16 * i) * inner + col;
+      if (out.qvals) *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out.qvals) + base) = qv;
+      if (out.fq) *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out.fq) + base) = fv;
       if (out.codes) {
         if (code_bytes == 1) {
 #pragma unroll
-          for (int e = 0; e < VE; ++e) static_cast<uint8_t*>(out.codes)[base + e] = (uint8_t)cd[e];
+          for (int e = 0; e < VE; ++e) static_cast<uint8_t*>(out.codes)[base + e] = (uint8_t)(ent[e] >> 16);
         } else {
 #pragma unroll
-          for (int e = 0; e < VE; ++e) static_cast<uint16_t*>(out.codes)[base + e] = (uint16_t)cd[e];
+          for (int e = 0; e < VE; ++e) static_cast<uint16_t*>(out.codes)[base + e] = (uint16_t)(ent[e] >> 16);
         }
+      }
+    };
+    // A chunk past inner takes no part in the wave's choice (its scales are
+    // those of empty columns).  When every chunk of the wave is on the table
+    // path, all its entries are read with no branch between the reads.
+    if (__all(all_fast || !cok)) {
+      uint32_t ent[R][VE];
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t wmj = w[i][j] & ~mk[i][j];  // outliers encode as +0
+          const float xl = u2f(wmj << 16), xh = u2f(wmj & 0xFFFF0000u);
+          uint32_t al, ah;
+          if constexpr (ABSMAX) {
+            const float ql = xl * rcp[2 * j], qh = xh * rcp[2 * j + 1];
+            // clamped magnitudes are normal and finite: hardware RNE is exact
+            const uint32_t hh = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(ql), lo, hi),
+                                            __builtin_amdgcn_fmed3f(__builtin_fabsf(qh), lo, hi));
+            al = (f2u(ql) > nthr[2 * j] ? nb : pb) + 4u * (hh & 0xFFFFu);
+            ah = (f2u(qh) > nthr[2 * j + 1] ? nb : pb) + 4u * (hh >> 16);
+          } else {
+            // the clamped quotients are bf16 values: their high halves
+            const float cl = __builtin_amdgcn_fmed3f(__builtin_fabsf(xl * rcp[2 * j]), lo, hi);
+            const float ch = __builtin_amdgcn_fmed3f(__builtin_fabsf(xh * rcp[2 * j + 1]), lo, hi);
+            al = (f2u(xl) > nthr[2 * j] ? nb : pb) + 4u * (f2u(cl) >> 16);
+            ah = (f2u(xh) > nthr[2 * j + 1] ? nb : pb) + 4u * (f2u(ch) >> 16);
+          }
+          ent[i][2 * j] = *(lds_cu32*)(size_t)al;
+          ent[i][2 * j + 1] = *(lds_cu32*)(size_t)ah;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < R; ++i)
+        if (rok[i]) emit(i, ent[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        if (!rok[i]) continue;
+        uint32_t ent[VE];
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+          const uint32_t wmj = w[i][e >> 1] & ~mk[i][e >> 1];
+          const uint32_t xb = (e & 1) ? (wmj & 0xFFFF0000u) : (wmj << 16);
+          if (fast[e]) {
+            uint32_t addr;
+            if constexpr (ABSMAX) {
+              const float q = u2f(xb) * rcp[e];
+              const uint32_t h = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(q), lo, hi), 0.0f);
+              addr = (f2u(q) > nthr[e] ? nb : pb) + 4u * h;
+            } else {
+              const float qc = __builtin_amdgcn_fmed3f(__builtin_fabsf(u2f(xb) * rcp[e]), lo, hi);
+              addr = (xb > nthr[e] ? nb : pb) + 4u * (f2u(qc) >> 16);
+            }
+            ent[e] = *(lds_cu32*)(size_t)addr;
+          } else {
+            const float q = u2f(xb) / s[e];
+            uint32_t h = f2bf(q);
+            h = q == q ? h : (h & 0x7FFFu) | ((xb >> 16) & 0x8000u);
+            ent[e] = full[h];
+          }
+        }
+        emit(i, ent);
       }
     }
     __syncthreads();  // s_amax / s_scale / s_cmax are rewritten by the next tile
+#pragma unroll
+    for (int i = 0; i < R; ++i) w[i] = wn[i];
   }
-  outlier_tally(nskip, oa);
+  if constexpr (OUTL) outlier_tally(nskip, oa);
 }
 
 // The fake-quant output with outlier masking (mx_lut_kernel's OUTL form).
@@ -1437,20 +1522,29 @@ int mx_quantize(const void* x, int dtype, int64_t outer, int64_t L, int64_t inne
     const bool cols = dtype == kBF16 && fmt.lut && inner > 1 && inner % 8 == 0 && bs <= 16 * kColRowsMax &&
                       !packed && (out.codes == nullptr || code_layout == 1 || code_layout == 2) &&
                       aligned(x, 16) && (!out.qvals || aligned(out.qvals, 16)) && (!out.fq || aligned(out.fq, 16));
-    if (cols) {
+    const int64_t col_tiles = outer * ((L + bs - 1) / bs) * ((inner + kColChunks * 8 - 1) / (kColChunks * 8));
+    if (cols && col_tiles < ((int64_t)1 << 31)) {
       LutView lv{fmt.lut, fmt.lut_len};
-      const int64_t tiles = outer * ((L + bs - 1) / bs) * ((inner + kColChunks * 8 - 1) / (kColChunks * 8));
+      const int64_t tiles = col_tiles;
       const size_t lds = sizeof(uint32_t) * 2 * (size_t)lv.len;
-      if (sp.mode == 1) {
-        const unsigned grid = persistent_grid((const void*)mx_cols_lut_kernel<true>, 256, lds, tiles * 256);
-        hipLaunchKernelGGL((mx_cols_lut_kernel<true>), dim3(grid), dim3(256), lds, st, (const uint16_t*)x, outer, L,
-                           inner, (int)bs, sp, lv, out, code_layout, oa);
-      } else {
-        const unsigned grid = persistent_grid((const void*)mx_cols_lut_kernel<false>, 256, lds, tiles * 256);
-        hipLaunchKernelGGL((mx_cols_lut_kernel<false>), dim3(grid), dim3(256), lds, st, (const uint16_t*)x, outer,
-                           L, inner, (int)bs, sp, lv, out, code_layout, oa);
-      }
-      return check_launch("mx_quantize(cols, table)");
+      auto go = [&](auto kern) {
+        const unsigned grid = persistent_grid((const void*)kern, 256, lds, tiles * 256);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, (const uint16_t*)x, outer, L, inner, (int)bs, sp,
+                           lv, out, code_layout, oa);
+        return check_launch("mx_quantize(cols, table)");
+      };
+      // rows per thread: the 16 row groups of a workgroup cover bs rows
+      const int rows = (int)((bs + 15) / 16);
+      auto by_rows = [&](auto absmax, auto outl) {
+        constexpr bool A = decltype(absmax)::value, O = decltype(outl)::value;
+        if (rows <= 1) return go(mx_cols_lut_kernel<A, 1, O>);
+        if (rows <= 2) return go(mx_cols_lut_kernel<A, 2, O>);
+        if (rows <= 4) return go(mx_cols_lut_kernel<A, 4, O>);
+        return go(mx_cols_lut_kernel<A, 8, O>);
+      };
+      if (sp.mode == 1)
+        return oa.active ? by_rows(std::true_type{}, std::true_type{}) : by_rows(std::true_type{}, std::false_type{});
+      return oa.active ? by_rows(std::false_type{}, std::true_type{}) : by_rows(std::false_type{}, std::false_type{});
     }
   }
   return with_encoder(fmt, [&](auto enc) -> int {

@@ -119,18 +119,23 @@ __device__ __forceinline__ void outlier_tally(uint32_t cnt, const OutlierArgs& o
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (bid != 0) return;
   __hip_atomic_store(outlier_word(st, cur), (unsigned long long)oa.numel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const unsigned long long n = __hip_atomic_load(outlier_word(st, prev), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (n == 0) return;
-  unsigned long long c = 0;
-  for (int s = 1; s <= kOutlierSlots; ++s) {
-    unsigned long long* w = outlier_word(st, prev + kOutlierStride * s);
-    c += __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __hip_atomic_store(outlier_word(st, prev), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const double f = (double)c / (double)n;
+  // the previous set's numel and slots and the best fraction are read
+  // together (one round trip at the end of the launch, not one per word)
+  unsigned long long v[kOutlierSlots + 1];
+#pragma unroll
+  for (int s = 0; s <= kOutlierSlots; ++s)
+    v[s] = __hip_atomic_load(outlier_word(st, prev + kOutlierStride * s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   unsigned long long* best = outlier_word(st, kOutlierBest);
   const double b = __builtin_bit_cast(double, __hip_atomic_load(best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const unsigned long long n = v[0];
+  if (n == 0) return;
+  unsigned long long c = 0;
+#pragma unroll
+  for (int s = 1; s <= kOutlierSlots; ++s) c += v[s];
+#pragma unroll
+  for (int s = 0; s <= kOutlierSlots; ++s)
+    __hip_atomic_store(outlier_word(st, prev + kOutlierStride * s), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const double f = (double)c / (double)n;
   if (f > b) __hip_atomic_store(best, __builtin_bit_cast(unsigned long long, f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -46,12 +46,8 @@ struct LutLds {
   uint32_t len, t0m1, t1, s, zsign;
 };
 
-// Cooperative copy of the two signed tables into LDS; returns the view.
-// Call with all threads of the workgroup; includes the barrier.
-__device__ __forceinline__ LutLds lut_to_lds(const uint32_t* blob, int len, uint32_t* lds) {
-  const uint32_t* src = blob + kLutHeaderWords;
-  for (int i = threadIdx.x; i < 2 * len; i += blockDim.x) lds[i] = src[i];
-  __syncthreads();
+// The blob's header words (uniform loads) and the LDS view of its tables.
+__device__ __forceinline__ LutLds lut_header(const uint32_t* blob, int len, const uint32_t* lds) {
   LutLds v;
   v.pos = lds;
   v.len = (uint32_t)len;
@@ -59,6 +55,36 @@ __device__ __forceinline__ LutLds lut_to_lds(const uint32_t* blob, int len, uint
   v.t1 = blob[kLutT1];
   v.s = blob[kLutS];
   v.zsign = blob[kLutZeroSign];
+  return v;
+}
+
+// The copy loops below issue kLutCopyBatch loads per thread before the first
+// LDS store (clamped indices, no branch between the loads), so a workgroup's
+// prologue waits for one round trip per batch rather than one per word.
+constexpr int kLutCopyBatch = 8;
+template <typename F>
+__device__ __forceinline__ void lut_copy_batched(const uint32_t* __restrict__ src, int n, F&& put) {
+  for (int b = 0; b < n; b += kLutCopyBatch * (int)blockDim.x) {
+    uint32_t r[kLutCopyBatch];
+#pragma unroll
+    for (int u = 0; u < kLutCopyBatch; ++u) {
+      const int i = b + u * (int)blockDim.x + (int)threadIdx.x;
+      r[u] = src[i < n ? i : n - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < kLutCopyBatch; ++u) {
+      const int i = b + u * (int)blockDim.x + (int)threadIdx.x;
+      if (i < n) put(i, r[u]);
+    }
+  }
+}
+
+// Cooperative copy of the two signed tables into LDS; returns the view.
+// Call with all threads of the workgroup; includes the barrier.
+__device__ __forceinline__ LutLds lut_to_lds(const uint32_t* blob, int len, uint32_t* lds) {
+  const LutLds v = lut_header(blob, len, lds);
+  lut_copy_batched(blob + kLutHeaderWords, 2 * len, [&](int i, uint32_t w) { lds[i] = w; });
+  __syncthreads();
   return v;
 }
 
@@ -73,21 +99,14 @@ constexpr int kCodeCopy2 = 4096;  // CB 4 needs 2 * len <= kCodeCopy2
 template <int CB>
 __device__ __forceinline__ LutLds lut_codes_to_lds(const uint32_t* blob, int len, uint32_t* lds) {
   static_assert(CB == 4 || CB == 8, "code tables hold 4- or 8-bit codes");
-  const uint32_t* src = blob + kLutHeaderWords;
+  const LutLds v = lut_header(blob, len, lds);
   uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
-  for (int i = threadIdx.x; i < 2 * len; i += blockDim.x) {
-    const uint32_t c = src[i] >> 16;
+  lut_copy_batched(blob + kLutHeaderWords, 2 * len, [&](int i, uint32_t w) {
+    const uint32_t c = w >> 16;
     l8[i] = (uint8_t)c;
     if constexpr (CB == 4) l8[kCodeCopy2 + i] = (uint8_t)(c << 4);
-  }
+  });
   __syncthreads();
-  LutLds v;
-  v.pos = lds;
-  v.len = (uint32_t)len;
-  v.t0m1 = blob[kLutT0m1];
-  v.t1 = blob[kLutT1];
-  v.s = blob[kLutS];
-  v.zsign = blob[kLutZeroSign];
   return v;
 }
 
