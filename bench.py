@@ -1058,7 +1058,7 @@ DOMINANT = {
     "l1_histogram": "lcq_hist_kernel<0, true, false>",
     "g1_gptq": "gptq_block_kernel",
     "f1_outlier_opct": "mx_lut_kernel<0, 4, true, 2, false, true>",
-    "f1_outlier_othr_ax2": "mx_block_kernel<unsigned short, vqx::EncLevels>",
+    "f1_outlier_othr_ax2": "mx_cols_lut_kernel<true, 4, true>",
     "c6_attn_qk_int6": "mx_gemm_kernel<0, 0, false, 128, 128>",
     "c6_attn_pv_int6": "mx_gemm_kernel<1, 0, false, 128, 128>",
     "c6_mxint8_linear": "mx_gemm_kernel<0, 0, true, 256, 128>",

@@ -446,8 +446,11 @@ def mx_fake_quantize_outlier(input, desc, axis, block_size, quant_max, force_pow
         raise AssertionError("block_size must be positive")
     x = input.contiguous()
     axis, outer, L, inner = _axis_geometry(list(x.shape), axis)
-    sshape = mx_scale_shape(x.shape, axis, block_size)
-    scale = torch.empty(sshape, dtype=x.dtype, device=x.device) if scale_f32 is None else None
+    scale = None
+    if scale_f32 is None:
+        sshape = list(x.shape)
+        sshape[axis] = -(-L // block_size)
+        scale = torch.empty(sshape, dtype=x.dtype, device=x.device)
     y = torch.empty_like(x)
     sq = _table_bf16(scale_qmap.to(x.device)) if (scale_qmap is not None and not force_pow2) else None
     shift = math.floor(math.log2(quant_max)) if force_pow2 else 0

@@ -90,8 +90,20 @@ def _direct_scale(scale, input, axis, block_size):
     write it in place (fp32, on the input's device), else None."""
     if scale.dtype != torch.float32 or scale.device != input.device:
         return None
-    scale.resize_(qops.mx_scale_shape(input.shape, axis, block_size))
+    shape = qops.mx_scale_shape(input.shape, axis, block_size)
+    if list(scale.shape) != shape:
+        scale.resize_(shape)
     return scale if scale.is_contiguous() else None
+
+
+def _run(fn, x, *args):
+    """fn.apply(x, *args), or fn's forward alone when no gradient can flow
+    through it (grad mode off, or x not requiring one): the same output
+    without an autograd node and without apply's per-call host cost.  The
+    forwards here use no ctx."""
+    if torch.is_grad_enabled() and x.requires_grad:
+        return fn.apply(x, *args)
+    return fn.forward(None, x, *args)
 
 
 class MXFakeQuantizeFunction(torch.autograd.Function):
@@ -456,19 +468,17 @@ class FusedAmaxObsFakeQuantize(_BufferFlags, FakeQuantizeBase):
         fmt = self._fmt if self._closed_form() else None
         fq_on = self._fake_quant_on()
         if self.outlier_threshold is not None:
-            return OutlierFakeQuantizeFunction.apply(x, self, fq_on, fmt)
+            return _run(OutlierFakeQuantizeFunction, x, self, fq_on, fmt)
         if self.qscheme == QScheme.MICROSCALING:
-            x = MXFakeQuantizeFunction.apply(x, fq_on, self.scale, self.qmap, self.ch_axis,
-                                             self.block_size, self.quant_max,
-                                             self.force_scale_power_of_two, self.scale_qmap, fmt)
+            x = _run(MXFakeQuantizeFunction, x, fq_on, self.scale, self.qmap, self.ch_axis, self.block_size,
+                     self.quant_max, self.force_scale_power_of_two, self.scale_qmap, fmt)
         elif self.qscheme == QScheme.GROUP_WISE_AFFINE:
-            x = GroupWiseAffineFakeQuantFunction.apply(x, fq_on, self.scale, self.zero_point, self.ch_axis,
-                                                       self.block_size, self.quant_min, self.quant_max,
-                                                       self.scale_qmap)
+            x = _run(GroupWiseAffineFakeQuantFunction, x, fq_on, self.scale, self.zero_point, self.ch_axis,
+                     self.block_size, self.quant_min, self.quant_max, self.scale_qmap)
         elif self._observer_on():
-            x = ObservedFakeQuantizeFunction.apply(x, fq_on, self, fmt)
+            x = _run(ObservedFakeQuantizeFunction, x, fq_on, self, fmt)
         else:
-            x = FakeQuantizeFunction.apply(x, fq_on, self.qmap, self.scale, fmt)
+            x = _run(FakeQuantizeFunction, x, fq_on, self.qmap, self.scale, fmt)
         return x
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
@@ -511,7 +521,7 @@ class _DerivedObserverOrFakeQuantize(_BufferFlags, FakeQuantizeBase):
         if self.qmap.numel() == 0:
             q = get_quantization_map(self.dtype, x.device)
             self.qmap = (q[1][q[0]] if isinstance(q, tuple) else q).to(x.device)
-        return FakeQuantizeFunction.apply(x, self._fake_quant_on(), self.qmap, self.calculate_qparams(), self._fmt)
+        return _run(FakeQuantizeFunction, x, self._fake_quant_on(), self.qmap, self.calculate_qparams(), self._fmt)
 
     def calculate_qparams(self):
         return self.derive_qparams_fn(self.obs_or_fqs)
