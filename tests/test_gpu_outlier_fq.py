@@ -110,6 +110,29 @@ def test_topk_running_average_matches_torch(vqx, dtype):
         assert thr.item() == ora.outlier_threshold.item(), step
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("pct", [1e-5, 0.01, 0.3])
+def test_topk_running_average_window(vqx, dtype, pct):
+    # calls after the first see the previous threshold: the first pass also
+    # counts a window of magnitudes around it and finishes the select when
+    # the k-th value falls inside (the same input again, scaled slightly),
+    # else the second pass does (scaled by 4 and 1/16, or back); ties, +-Inf,
+    # -0 and tiny values included
+    from importlib import import_module
+
+    qops = import_module(vqx.__name__ + ".ops.quantized")
+    ws = qops.outlier_topk_workspace("cuda")
+    thr = torch.zeros((), dtype=torch.float32, device="cuda")
+    ora = R.OutlierFakeQuantize(outlier_pct=pct, decay=0.9)
+    base = special_input(200003, torch.float32, seed=77)
+    for step, f in enumerate([1.0, 1.0, 1.03, 0.97, 4.0, 4.0, 1.0 / 16, 1.0, 1.0]):
+        x = (base * f).to(dtype)
+        ora(x, None)
+        topk_call(vqx, x.cuda(), max(1, math.ceil(pct * x.numel())), thr, ws, ema=step > 0, decay=0.9)
+        assert thr.item() == ora.outlier_threshold.item(), (step, f, thr.item(), ora.outlier_threshold.item())
+
+
 def spec_module(vqx, s):
     return vqx.quantization.QuantizationSpec.from_str(s).make_fake_quantize("cuda").cuda()
 

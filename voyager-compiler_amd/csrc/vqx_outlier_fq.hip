@@ -52,8 +52,10 @@ constexpr int kTopkThreads = 1024;
 // Radix-select state in caller-owned device memory, zero-initialised once.
 // A call leaves hist, ticket and nan at zero again; prefix, remaining and
 // done pass a pass's choice to the next and are rewritten by every call.
+constexpr int kTopkFine = 256;  // pass 0's window of 15-bit magnitudes
 struct TopkState {
   uint32_t hist[kTopkBins];
+  uint32_t fine[kTopkFine];  // pass 0's counts of the magnitudes in its window
   uint32_t ticket;
   uint32_t prefix;     // the magnitude's digits chosen so far
   uint64_t remaining;  // the rank (1 = largest) still wanted among those magnitudes
@@ -77,22 +79,32 @@ __device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
 // the top-k minimum into the fp32 buffer; later calls take
 // t * decay + (threshold * (1 - decay)), each operation rounded as torch
 // rounds it: t * decay in fp32 (the buffer's dtype), threshold * (1 - decay)
-// in x's dtype, the sum in fp32.
+// in x's dtype, the sum in fp32 (three roundings: no contraction into an FMA,
+// which rounds once and differs at ties).
 template <typename E>
 __device__ __forceinline__ void write_threshold(float v, int ema, float decay, float omd, float* thr) {
+#pragma clang fp contract(off)
   if (!ema) {
     *thr = v;
     return;
   }
-  const float a = __fmul_rn(*thr, decay);
-  const float b = E::val(E::round(__fmul_rn(v, omd)));
-  *thr = __fadd_rn(a, b);
+  const float a = *thr * decay;
+  const float b = E::val(E::round(v * omd));
+  *thr = a + b;
 }
 
 // One radix pass.  Every workgroup counts its share of x into an LDS
 // histogram and adds the nonzero bins to st->hist; the last one to finish
 // picks the digit.  Pass 0 also counts NaNs.  Later passes do nothing when
-// pass 0 found a NaN (it wrote the threshold already).
+// pass 0 settled the threshold (a NaN, or the window below).
+//
+// For 15-bit magnitudes with a previous threshold t (the running average),
+// pass 0 also counts every magnitude in a window of 256 from one binade
+// below t, one bin each.  When the digit it picks lies inside the window,
+// those counts are the second pass's histogram for that digit, so the last
+// workgroup finishes the select itself and pass 1 returns at once; a digit
+// outside the window leaves it to pass 1 as before.  Either way the result
+// is the same k-th largest magnitude.
 template <typename E>
 __global__ __launch_bounds__(kTopkThreads) void topk_pass_kernel(const typename E::S* __restrict__ x, int64_t n,
                                                                  int64_t k, int pass, Digit dg, int last,
@@ -100,6 +112,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pass_kernel(const typename 
                                                                  float omd) {
   using S = typename E::S;
   __shared__ uint32_t h[kTopkBins];
+  __shared__ uint32_t s_fine[kTopkFine];
   __shared__ uint32_t s_nan, s_ticket;
   __shared__ uint64_t s_wsum[kTopkThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -107,7 +120,21 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pass_kernel(const typename 
   const uint32_t prefix = pass > 0 ? ld_agent(&st->prefix) : 0u;
   const int nbins = 1 << dg.width;
   const uint32_t dmask = (uint32_t)nbins - 1u;
+  // pass 0's window [w0, w0 + 256), 16-aligned (whole second-pass digits),
+  // from one binade (128 magnitudes) below the previous threshold
+  bool win = false;
+  uint32_t w0 = 0;
+  if (E::kBits == 15 && pass == 0 && ema) {
+    const float tp = *thr;
+    if (tp > 0.0f && tp < __builtin_huge_valf()) {
+      const uint32_t tb = E::round(tp) & E::kMag;
+      w0 = (tb > 128u ? tb - 128u : 0u) & ~15u;
+      win = w0 + kTopkFine <= E::kInf;
+    }
+  }
   for (int i = tid; i < kTopkBins; i += kTopkThreads) h[i] = 0;
+  if (win)
+    for (int i = tid; i < kTopkFine; i += kTopkThreads) s_fine[i] = 0;
   if (tid == 0) s_nan = 0;
   __syncthreads();
   uint32_t nan = 0;
@@ -119,6 +146,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pass_kernel(const typename 
     }
     if (pass > 0 && (mag >> (dg.shift + dg.width)) != prefix) return;
     atomicAdd(&h[(mag >> dg.shift) & dmask], 1u);
+    if (win && mag - w0 < (uint32_t)kTopkFine) atomicAdd(&s_fine[mag - w0], 1u);
   };
   constexpr int V = 16 / sizeof(S);
   constexpr int U = 4;  // loads in flight per thread
@@ -150,6 +178,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pass_kernel(const typename 
   __syncthreads();
   for (int i = tid; i < nbins; i += kTopkThreads)
     if (h[i]) __hip_atomic_fetch_add(&st->hist[i], h[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (win)
+    for (int i = tid; i < kTopkFine; i += kTopkThreads)
+      if (s_fine[i]) __hip_atomic_fetch_add(&st->fine[i], s_fine[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (tid == 0 && s_nan) __hip_atomic_fetch_add(&st->nan, s_nan, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's bin additions have completed
   __syncthreads();
@@ -168,6 +199,12 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pass_kernel(const typename 
     h[i] = ld_agent(&st->hist[i]);
     st_agent(&st->hist[i], 0u);
   }
+  if (win) {
+    for (int i = tid; i < kTopkFine; i += kTopkThreads) {
+      s_fine[i] = ld_agent(&st->fine[i]);
+      st_agent(&st->fine[i], 0u);
+    }
+  }
   __syncthreads();
   if (s_nan) {  // a NaN ranks first: the threshold is NaN
     if (tid == 0) {
@@ -176,7 +213,6 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pass_kernel(const typename 
     }
     return;
   }
-  if (pass == 0 && tid == 0) st_agent(&st->done, 0u);
   const uint64_t want = pass == 0 ? (uint64_t)k
                                   : __hip_atomic_load(&st->remaining, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // each thread owns bins 2 tid and 2 tid + 1; the count above a thread's
@@ -208,10 +244,25 @@ __global__ __launch_bounds__(kTopkThreads) void topk_pass_kernel(const typename 
   const uint32_t digits = (prefix << dg.width) | (uint32_t)sel;
   if (last) {
     write_threshold<E>(E::val(digits << dg.shift), ema, decay, omd, thr);
-  } else {
-    st_agent(&st->prefix, digits);
-    __hip_atomic_store(&st->remaining, rem, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
   }
+  // pass 0 (the one thread that picked the digit): the window's counts of the
+  // digit's 16 magnitudes finish the select when they cover it
+  const uint32_t m0 = digits << dg.shift;
+  if (win && dg.shift == 4 && m0 >= w0 && m0 + 16u <= w0 + kTopkFine) {
+    uint64_t c = 0;
+    for (int j = 15; j >= 0; --j) {
+      c += s_fine[m0 + (uint32_t)j - w0];
+      if (c >= rem) {
+        write_threshold<E>(E::val(m0 + (uint32_t)j), ema, decay, omd, thr);
+        st_agent(&st->done, 1u);
+        return;
+      }
+    }
+  }
+  if (pass == 0) st_agent(&st->done, 0u);
+  st_agent(&st->prefix, digits);
+  __hip_atomic_store(&st->remaining, rem, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <typename E>
