@@ -978,10 +978,13 @@ __global__ __launch_bounds__(kMxLutThreads) void mx_lut_kernel(const uint16_t* _
           q[j] = u2f(xb) * rcp;
         }
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          // clamped magnitudes are normal and finite: hardware RNE is exact
-          uint32_t h = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(q[j]), lo, hi), 0.0f);
-          addr[j] = (f2u(q[j]) > nthr ? nb : pb) + ES * h;
+        for (int j = 0; j < 16; j += 2) {
+          // clamped magnitudes are normal and finite: hardware RNE is exact;
+          // one conversion rounds the pair
+          const uint32_t hh = pack_bf16x2(__builtin_amdgcn_fmed3f(__builtin_fabsf(q[j]), lo, hi),
+                                          __builtin_amdgcn_fmed3f(__builtin_fabsf(q[j + 1]), lo, hi));
+          addr[j] = (f2u(q[j]) > nthr ? nb : pb) + ES * (hh & 0xFFFFu);
+          addr[j + 1] = (f2u(q[j + 1]) > nthr ? nb : pb) + ES * (hh >> 16);
         }
       }
 #pragma unroll
